@@ -1,0 +1,161 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X HIP backend for ViperBench's normalization family.
+
+Metric: achieved HBM GB/s per kernel, as a fraction of the
+measured MI355X stream-copy peak; latency in microseconds.
+
+A "step" is one launch of the hot-path kernel over one batch of the workload.
+The default workload is the one the headline metric is quoted on (configs[1]:
+RMSNorm bf16 [8192, 4096], eps 1e-6).  Inputs are generated on the CPU with a
+fixed seed and copied to HBM before timing; the timed launches cycle through
+enough copies (>= 2 GiB in total) that no launch finds its data in the
+256 MB Infinity Cache.  ``value`` = algorithmic bytes x steps / elapsed time of
+the back-to-back timed region (device events on the launch stream).
+
+  python bench.py [--steps K] [--warmup W] [--workload KEY] [--all] [--no-cpu]
+
+Prints ONE JSON line on stdout (``--all``: one per workload).  Progress goes
+to stderr.  Only one GPU is used: ``--gpus`` above 1 exits with a message.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import subprocess
+import sys
+import time
+
+import torch
+
+from dslperfgap_amd import _lib, harness
+from dslperfgap_amd.workloads import HEADLINE, WORKLOADS
+
+METRIC = "achieved HBM GB/s and % of measured MI355X peak per kernel; latency µs"
+VENDOR_PEAK_GBPS = 8000.0
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_model() -> str:
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except Exception:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(w, cpu_args, budget_s: float) -> dict:
+    """Time the oracle's CPU restatement of the reference golden on the same
+    inputs, on this host's cores (reported baseline only)."""
+    from oracle import pytorch_impl as ref  # the checker doubles as the CPU path
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    fn = getattr(ref, w.fn)
+    warm = 1 if w.fn == "cross_entropy_fwd" else 3
+    for _ in range(warm):
+        fn(*cpu_args)
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 10 and (time.perf_counter() - t_start) < budget_s:
+        t0 = time.perf_counter()
+        fn(*cpu_args)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return {
+        "value": round(w.bytes_per_launch / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"full {w.key} shape, oracle restatement of the reference golden "
+                   f"(torch CPU), {warm} warm-up + {len(times)} timed calls, median "
+                   f"{med * 1e3:.2f} ms; CPU: {cpu_model()}"),
+        "ms": round(med * 1e3, 3),
+    }
+
+
+def run_workload(key, steps, warmup, peak_measured, with_cpu, cpu_budget):
+    w = WORKLOADS[key]
+    log(f"[bench] {key}: generating inputs")
+    cpu_args = w.make()
+    rot = harness.make_rotation(w, cpu_args, "cuda:0")
+    log(f"[bench] {key}: {rot.copies} HBM copies, {w.bytes_per_launch} B per launch")
+    r = harness.time_back_to_back(rot.launch, steps, warmup)
+    per_launch_ms = r["event_ms"] / steps
+    value = w.bytes_per_launch * steps / (r["event_ms"] * 1e-3) / 1e9
+    single = harness.time_kernel(rot.launch, reps=50, warmup=5)
+    vendor_peak = VENDOR_PEAK_GBPS
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(r["wall_ms"] / steps, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": w.dtype,
+        "accumulate": "f32",
+        "data": "synthetic: seeded CPU generator (BASELINE.json config distributions), copied to HBM",
+        "config": {"workload": key, "desc": w.desc, "hbm_copies": rot.copies},
+        "latency_us": round(per_launch_ms * 1e3, 3),
+        "latency_us_single_launch_median": round(single["median_ms"] * 1e3, 3),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(value, 2),
+            "peak": vendor_peak,
+            "unit": "GB/s",
+            "frac": round(value / vendor_peak, 4),
+            "traffic": None,
+        },
+        "measured_copy_peak_GBps": round(peak_measured / 1e9, 2),
+        "frac_of_measured_peak": round(value * 1e9 / peak_measured, 4),
+    }
+    del rot
+    torch.cuda.empty_cache()
+    if with_cpu:
+        log(f"[bench] {key}: CPU baseline")
+        line["cpu_baseline"] = cpu_baseline(w, cpu_args, cpu_budget)
+    return line
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS))
+    ap.add_argument("--all", action="store_true", help="every measured workload, one line each")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of timed CPU work")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this backend is measured on one GPU only (row kernels shard rows "
+              "with no exchange; see DESIGN.md); --gpus must be 1", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    _lib.lib()
+    log(f"[bench] device: {torch.cuda.get_device_name(0)}")
+    peak = harness.copy_peak("cuda:0")
+    log(f"[bench] measured stream-copy peak: {peak / 1e9:.1f} GB/s")
+    keys = sorted(WORKLOADS) if args.all else [args.workload]
+    for key in keys:
+        line = run_workload(key, args.steps, args.warmup, peak, not args.no_cpu, args.cpu_budget)
+        print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,51 @@
+"""Torch-side plumbing shared by the hip_impl modules: dtype codes, device
+checks, raw pointers and the current HIP stream.  Nothing here computes."""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+FLOAT_CODES = {torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}
+LABEL_CODES = {torch.int32: _lib.I32, torch.int64: _lib.I64}
+
+
+def float_code(t: torch.Tensor, what: str) -> int:
+    try:
+        return FLOAT_CODES[t.dtype]
+    except KeyError:
+        raise TypeError(f"{what}: dtype {t.dtype} is not supported by the HIP backend "
+                        "(float32, float16, bfloat16)") from None
+
+
+def require_gpu(what: str, *tensors: torch.Tensor) -> torch.device:
+    """All tensors must live on the same GPU; return that device."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError(f"{what}: the HIP backend takes GPU tensors, got one on {t.device}")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"{what}: tensors on different devices ({dev}, {t.device})")
+    if dev is None:
+        raise ValueError(f"{what}: no tensor arguments")
+    return dev
+
+
+def ptr(t: torch.Tensor | None):
+    return None if t is None else t.data_ptr()
+
+
+def stream(dev: torch.device) -> int:
+    """Handle of torch's current stream on `dev` (the library launches there)."""
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def numel_prod(shape) -> int:
+    n = 1
+    for s in shape:
+        n *= int(s)
+    return n

@@ -1,0 +1,108 @@
+"""ctypes binding of libvbhip.so (declarations in include/vbhip.h).
+
+The library is loaded after ``import torch`` so that it binds to the HIP
+runtime torch already holds (both carry the soname libamdhip64.so.7), which
+makes torch's stream handles valid for the library's launches.
+
+There is no fallback: if the library is missing, :func:`lib` raises
+``ImportError`` naming the build command.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  (loads the HIP runtime the library must share)
+
+LIB_PATH = Path(os.environ.get("VBHIP_LIB", Path(__file__).resolve().parent / "libvbhip.so"))
+
+ABI_VERSION = 1
+
+# element type codes (VBH_DTYPE_*)
+F32, F16, BF16, I32, I64 = 0, 1, 2, 3, 4
+# argument-error codes (VBH_E_*)
+E_INVALID, E_DTYPE, E_RANGE = -1, -2, -3
+# op codes for vbh_tune_override (VBH_OP_*)
+OP_LAYER_NORM, OP_RMS_NORM, OP_SOFTMAX, OP_LOGSUMEXP, OP_CROSS_ENTROPY = 0, 1, 2, 3, 4
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+_f32 = ctypes.c_float
+
+# name -> (restype, argtypes); kept in the order of include/vbhip.h
+SIGNATURES = {
+    "vbh_abi_version": (_i32, []),
+    "vbh_last_error": (ctypes.c_char_p, []),
+    "vbh_layer_norm_fwd": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _i32, _vp]),
+    "vbh_rms_norm_fwd": (_i32, [_vp, _vp, _vp, _i64, _i64, _f32, _i32, _i32, _vp]),
+    "vbh_softmax_fwd": (_i32, [_vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp]),
+    "vbh_softmax_dim_fwd": (_i32, [_vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32, _vp]),
+    "vbh_logsumexp_fwd": (_i32, [_vp, _vp, _i64, _i64, _i32, _i32, _vp]),
+    "vbh_cross_entropy_fwd": (
+        _i32,
+        [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _f32, _f32, _i64, _i64,
+         _i64, _i64, _i32, _i32, _vp],
+    ),
+    "vbh_cross_entropy_bwd": (
+        _i32,
+        [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _f32,
+         _i64, _i64, _i64, _i32, _vp],
+    ),
+    "vbh_stream_copy": (_i32, [_vp, _vp, _i64, _vp]),
+    "vbh_tune_override": (_i32, [_i32, _i32, _i32]),
+}
+
+
+class VbhError(RuntimeError):
+    """A nonzero status from libvbhip (argument error < 0, hipError_t > 0)."""
+
+    def __init__(self, fn: str, code: int, message: str):
+        super().__init__(f"{fn} failed with status {code}: {message}")
+        self.code = code
+
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load (once) and return the bound library."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise ImportError(
+                    f"{LIB_PATH} is missing: build it with `python -m dslperfgap_amd.build` "
+                    "(there is no non-HIP fallback)")
+            handle = ctypes.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.restype = res
+                fn.argtypes = args
+            version = handle.vbh_abi_version()
+            if version != ABI_VERSION:
+                raise ImportError(f"{LIB_PATH} has ABI {version}, expected {ABI_VERSION}")
+            _lib = handle
+    return _lib
+
+
+def last_error() -> str:
+    msg = lib().vbh_last_error()
+    return msg.decode() if msg else ""
+
+
+def call(name: str, *args) -> None:
+    """Call entry point `name`; raise VbhError on a nonzero status."""
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        raise VbhError(name, rc, last_error())
+
+
+def tune_override(op: int, tpr: int = 0, block: int = 0) -> None:
+    """Force threads-per-row / workgroup size for one op (0, 0 restores the heuristic)."""
+    call("vbh_tune_override", op, tpr, block)

@@ -1,0 +1,351 @@
+// C ABI of libvbhip.so: argument validation, launch-geometry selection and
+// error reporting around the kernel launchers.  Declarations and the reference
+// interface each entry point stands in for are in include/vbhip.h.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <atomic>
+
+#include "../../include/vbhip.h"
+#include "vbh_device.h"
+#include "vbh_launch.h"
+
+namespace vbh {
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) {
+    g_err[0] = '\0';
+    return 0;
+  }
+  return fail(static_cast<int>(e), "%s: %s (%s)", what, hipGetErrorName(e),
+              hipGetErrorString(e));
+}
+
+int elt_size(int dt) {
+  switch (dt) {
+    case kF32: return 4;
+    case kF16: return 2;
+    case kBF16: return 2;
+    case kI32: return 4;
+    case kI64: return 8;
+    default: return 0;
+  }
+}
+
+bool is_float(int dt) { return dt == kF32 || dt == kF16 || dt == kBF16; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// process-wide launch-geometry overrides (vbh_tune_override)
+constexpr int kNumOps = 5;
+std::atomic<int> g_tpr[kNumOps];
+std::atomic<int> g_block[kNumOps];
+
+constexpr int64_t kMaxCols = (int64_t(1) << 31) - 1;
+constexpr int64_t kMaxWorkItems = (int64_t(1) << 32) - 1;
+
+int check_grid(int64_t units, const Geometry& g) {
+  const int64_t grid = g.stream ? units : grid_for(units, g);
+  if (grid * g.block > kMaxWorkItems)
+    return fail(VBH_E_RANGE, "launch of %lld workgroups x %d lanes exceeds 2^32 work-items",
+                static_cast<long long>(grid), g.block);
+  return 0;
+}
+
+int pow2ceil(int64_t n) {
+  int p = 1;
+  while (p < n) p <<= 1;
+  return p;
+}
+
+}  // namespace
+
+Geometry pick_geometry(int64_t cols, int vec, int tpr_override, int block_override) {
+  Geometry g;
+  g.v = vec;
+  const int64_t nvec = cols / vec;
+  const int cap = lane_cap(vec);  // vectors per lane in registers
+  int tpr;
+  if (tpr_override > 0) {
+    tpr = tpr_override;
+  } else if (nvec <= int64_t(kWave) * cap) {
+    // a sub-wave or one wave64 per row
+    tpr = nvec >= kWave ? kWave : pow2ceil(nvec < 1 ? 1 : nvec);
+  } else {
+    const int64_t need = (nvec + cap - 1) / cap;
+    tpr = need >= kMaxBlock ? kMaxBlock : pow2ceil(need);
+  }
+  const int64_t it = (nvec + tpr - 1) / tpr;
+  if (it > cap) {
+    g.stream = true;
+    g.tpr = kMaxBlock;
+    g.block = kMaxBlock;
+    g.maxit = 1;
+    return g;
+  }
+  g.tpr = tpr;
+  g.maxit = pow2ceil(it < 1 ? 1 : it);
+  int block = block_override > 0 ? block_override : 256;
+  if (block < tpr) block = tpr;
+  g.block = block;
+  return g;
+}
+
+}  // namespace vbh
+
+using namespace vbh;
+
+extern "C" {
+
+int vbh_abi_version(void) { return VBH_ABI_VERSION; }
+
+const char* vbh_last_error(void) { return g_err; }
+
+int vbh_tune_override(int op, int tpr, int block) {
+  if (op < 0 || op >= kNumOps) return fail(VBH_E_INVALID, "tune_override: bad op %d", op);
+  if (tpr != 0 && (tpr < 1 || tpr > kMaxBlock || (tpr & (tpr - 1)) != 0))
+    return fail(VBH_E_INVALID, "tune_override: tpr %d is not a power of two in [1, 1024]",
+                tpr);
+  if (block != 0 && (block < kWave || block > kMaxBlock || block % kWave != 0))
+    return fail(VBH_E_INVALID, "tune_override: block %d is not a multiple of 64 in [64, 1024]",
+                block);
+  if (tpr != 0 && block != 0 && (block % tpr != 0 && tpr <= block))
+    return fail(VBH_E_INVALID, "tune_override: block %d is not a multiple of tpr %d", block,
+                tpr);
+  g_tpr[op].store(tpr);
+  g_block[op].store(block);
+  g_err[0] = '\0';
+  return 0;
+}
+
+int vbh_layer_norm_fwd(const void* x, const void* w, const void* b, void* y, int64_t rows,
+                       int64_t cols, float eps, int dtype, int w_dtype, void* stream) {
+  if (!is_float(dtype)) return fail(VBH_E_DTYPE, "layer_norm: unsupported dtype %d", dtype);
+  if (w_dtype != dtype && w_dtype != kF32)
+    return fail(VBH_E_DTYPE, "layer_norm: weight dtype %d must equal x dtype %d or be fp32",
+                w_dtype, dtype);
+  if (rows < 0 || cols < 0) return fail(VBH_E_INVALID, "layer_norm: negative size");
+  if (cols > kMaxCols) return fail(VBH_E_RANGE, "layer_norm: cols %lld too large",
+                                   static_cast<long long>(cols));
+  if (rows == 0 || cols == 0) return 0;  // empty output
+  if (!x || !w || !y) return fail(VBH_E_INVALID, "layer_norm: null pointer");
+  const int vn = 16 / elt_size(dtype);
+  const bool vec_ok = cols % vn == 0 && aligned16(x) && aligned16(y) && aligned16(w) &&
+                      (b == nullptr || aligned16(b));
+  const Geometry g = pick_geometry(cols, vec_ok ? vn : 1, g_tpr[VBH_OP_LAYER_NORM].load(),
+                                   g_block[VBH_OP_LAYER_NORM].load());
+  if (int rc = check_grid(rows, g)) return rc;
+  return hip_status(launch_layer_norm(x, w, b, y, rows, static_cast<int>(cols), eps, dtype,
+                                      w_dtype, g, static_cast<hipStream_t>(stream)),
+                    "layer_norm launch");
+}
+
+int vbh_rms_norm_fwd(const void* x, const void* w, void* y, int64_t rows, int64_t cols,
+                     float eps, int dtype, int w_dtype, void* stream) {
+  if (!is_float(dtype)) return fail(VBH_E_DTYPE, "rms_norm: unsupported dtype %d", dtype);
+  if (w_dtype != dtype && w_dtype != kF32)
+    return fail(VBH_E_DTYPE, "rms_norm: weight dtype %d must equal x dtype %d or be fp32",
+                w_dtype, dtype);
+  if (rows < 0 || cols < 0) return fail(VBH_E_INVALID, "rms_norm: negative size");
+  if (cols > kMaxCols) return fail(VBH_E_RANGE, "rms_norm: cols %lld too large",
+                                   static_cast<long long>(cols));
+  if (rows == 0 || cols == 0) return 0;  // empty output
+  if (!x || !w || !y) return fail(VBH_E_INVALID, "rms_norm: null pointer");
+  const int vn = 16 / elt_size(dtype);
+  const bool vec_ok = cols % vn == 0 && aligned16(x) && aligned16(y) && aligned16(w);
+  const Geometry g = pick_geometry(cols, vec_ok ? vn : 1, g_tpr[VBH_OP_RMS_NORM].load(),
+                                   g_block[VBH_OP_RMS_NORM].load());
+  if (int rc = check_grid(rows, g)) return rc;
+  return hip_status(launch_rms_norm(x, w, y, rows, static_cast<int>(cols), eps, dtype,
+                                    w_dtype, g, static_cast<hipStream_t>(stream)),
+                    "rms_norm launch");
+}
+
+static bool softmax_pair_ok(int idt, int odt) {
+  if (!is_float(idt) || !is_float(odt)) return false;
+  return idt == odt || (odt == kF32 && idt != kF32);
+}
+
+int vbh_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols, int in_dtype,
+                    int out_dtype, int log_mode, void* stream) {
+  if (!softmax_pair_ok(in_dtype, out_dtype))
+    return fail(VBH_E_DTYPE, "softmax: unsupported (in, out) dtype pair (%d, %d)", in_dtype,
+                out_dtype);
+  if (log_mode != 0 && log_mode != 1)
+    return fail(VBH_E_INVALID, "softmax: log_mode must be 0 or 1");
+  if (rows < 0 || cols < 0) return fail(VBH_E_INVALID, "softmax: negative size");
+  if (cols > kMaxCols) return fail(VBH_E_RANGE, "softmax: cols %lld too large",
+                                   static_cast<long long>(cols));
+  if (rows == 0 || cols == 0) return 0;
+  if (!x || !y) return fail(VBH_E_INVALID, "softmax: null pointer");
+  const int vn = 16 / elt_size(in_dtype);
+  const bool vec_ok = cols % vn == 0 && aligned16(x) && aligned16(y);
+  const Geometry g = pick_geometry(cols, vec_ok ? vn : 1, g_tpr[VBH_OP_SOFTMAX].load(),
+                                   g_block[VBH_OP_SOFTMAX].load());
+  if (int rc = check_grid(rows, g)) return rc;
+  return hip_status(launch_softmax(x, y, rows, static_cast<int>(cols), in_dtype, out_dtype,
+                                   log_mode, g, static_cast<hipStream_t>(stream)),
+                    "softmax launch");
+}
+
+int vbh_softmax_dim_fwd(const void* x, void* y, int64_t outer, int64_t n, int64_t inner,
+                        int in_dtype, int out_dtype, int log_mode, void* stream) {
+  if (!softmax_pair_ok(in_dtype, out_dtype))
+    return fail(VBH_E_DTYPE, "softmax_dim: unsupported (in, out) dtype pair (%d, %d)",
+                in_dtype, out_dtype);
+  if (log_mode != 0 && log_mode != 1)
+    return fail(VBH_E_INVALID, "softmax_dim: log_mode must be 0 or 1");
+  if (outer < 0 || n < 0 || inner < 0) return fail(VBH_E_INVALID, "softmax_dim: negative size");
+  if (n > kMaxCols) return fail(VBH_E_RANGE, "softmax_dim: n too large");
+  if (outer == 0 || n == 0 || inner == 0) return 0;
+  if (!x || !y) return fail(VBH_E_INVALID, "softmax_dim: null pointer");
+  if ((outer * inner + 255) / 256 * 256 > kMaxWorkItems)
+    return fail(VBH_E_RANGE, "softmax_dim: outer * inner too large");
+  return hip_status(launch_softmax_dim(x, y, outer, static_cast<int>(n), inner, in_dtype,
+                                       out_dtype, log_mode, static_cast<hipStream_t>(stream)),
+                    "softmax_dim launch");
+}
+
+int vbh_logsumexp_fwd(const void* x, void* y, int64_t rows, int64_t cols, int in_dtype,
+                      int out_dtype, void* stream) {
+  if (!softmax_pair_ok(in_dtype, out_dtype))
+    return fail(VBH_E_DTYPE, "logsumexp: unsupported (in, out) dtype pair (%d, %d)", in_dtype,
+                out_dtype);
+  if (rows < 0 || cols < 0) return fail(VBH_E_INVALID, "logsumexp: negative size");
+  if (cols > kMaxCols) return fail(VBH_E_RANGE, "logsumexp: cols %lld too large",
+                                   static_cast<long long>(cols));
+  if (rows == 0) return 0;
+  // cols == 0 is valid: every row reduces an empty set and gets -inf (x unread)
+  if ((!x && cols > 0) || !y) return fail(VBH_E_INVALID, "logsumexp: null pointer");
+  const int vn = 16 / elt_size(in_dtype);
+  const bool vec_ok = cols % vn == 0 && aligned16(x);
+  const Geometry g = pick_geometry(cols, vec_ok ? vn : 1, g_tpr[VBH_OP_LOGSUMEXP].load(),
+                                   g_block[VBH_OP_LOGSUMEXP].load());
+  if (int rc = check_grid(rows, g)) return rc;
+  return hip_status(launch_logsumexp(x, y, rows, static_cast<int>(cols), in_dtype, out_dtype,
+                                     g, static_cast<hipStream_t>(stream)),
+                    "logsumexp launch");
+}
+
+int vbh_cross_entropy_fwd(const void* logits, const void* labels, int logits_dtype,
+                          int label_dtype, void* loss, void* lse, void* z_loss,
+                          int64_t n_rows, int64_t n_cols, int64_t row_stride, float smoothing,
+                          float logit_scale, float lse_square_scale, int64_t ignored_index,
+                          int64_t total_classes, int64_t class_start_idx, int64_t block_size,
+                          int has_smoothing, int split, void* stream) {
+  if (!is_float(logits_dtype))
+    return fail(VBH_E_DTYPE, "cross_entropy_fwd: unsupported logits dtype %d", logits_dtype);
+  if (label_dtype != kI32 && label_dtype != kI64)
+    return fail(VBH_E_DTYPE, "cross_entropy_fwd: labels must be int32 or int64");
+  if (n_rows < 0 || n_cols < 0) return fail(VBH_E_INVALID, "cross_entropy_fwd: negative size");
+  if (block_size <= 0) return fail(VBH_E_INVALID, "cross_entropy_fwd: BLOCK_SIZE must be > 0");
+  if (n_cols > (int64_t(1) << 30))
+    return fail(VBH_E_RANGE, "cross_entropy_fwd: n_cols too large");
+  if (row_stride < n_cols) return fail(VBH_E_INVALID, "cross_entropy_fwd: row_stride < n_cols");
+  if (n_rows == 0 || n_cols == 0) return 0;
+  if (!logits || !labels || !loss || !lse || !z_loss)
+    return fail(VBH_E_INVALID, "cross_entropy_fwd: null pointer");
+  const int64_t bs = block_size < n_cols ? block_size : n_cols;
+  const int64_t ncb = (n_cols + block_size - 1) / block_size;
+  const int vn = 16 / elt_size(logits_dtype);
+  const bool vec_ok =
+      n_cols % vn == 0 && bs % vn == 0 && row_stride % vn == 0 && aligned16(logits);
+  const Geometry g = pick_geometry(bs, vec_ok ? vn : 1, g_tpr[VBH_OP_CROSS_ENTROPY].load(),
+                                   g_block[VBH_OP_CROSS_ENTROPY].load());
+  if (int rc = check_grid(n_rows * ncb, g)) return rc;
+  CeArgs a;
+  a.logits = logits;
+  a.labels = labels;
+  a.logits_dt = logits_dtype;
+  a.label_i64 = label_dtype == kI64;
+  a.loss = static_cast<float*>(loss);
+  a.lse = static_cast<float*>(lse);
+  a.z_loss = static_cast<float*>(z_loss);
+  a.n_rows = n_rows;
+  a.n_cols = static_cast<int>(n_cols);
+  a.ld = row_stride;
+  a.block_size = static_cast<int>(bs);
+  a.ncb = static_cast<int>(ncb);
+  a.smoothing = smoothing;
+  a.logit_scale = logit_scale;
+  a.lse_square_scale = lse_square_scale;
+  a.ignored_index = ignored_index;
+  a.total_classes = static_cast<float>(total_classes);
+  a.class_start = class_start_idx;
+  a.has_smoothing = has_smoothing != 0;
+  a.split = split != 0;
+  return hip_status(launch_cross_entropy_fwd(a, g, static_cast<hipStream_t>(stream)),
+                    "cross_entropy_fwd launch");
+}
+
+int vbh_cross_entropy_bwd(const void* dloss, const void* logits, const void* lse,
+                          const void* labels, void* dlogits, int logits_dtype,
+                          int label_dtype, int64_t n_rows, int64_t n_cols,
+                          int64_t logits_row_stride, int64_t dlogits_row_stride,
+                          int64_t dloss_stride, float smoothing, float logit_scale,
+                          float lse_square_scale, int64_t ignored_index, int64_t total_classes,
+                          int64_t class_start_idx, int has_smoothing, void* stream) {
+  if (!is_float(logits_dtype))
+    return fail(VBH_E_DTYPE, "cross_entropy_bwd: unsupported logits dtype %d", logits_dtype);
+  if (label_dtype != kI32 && label_dtype != kI64)
+    return fail(VBH_E_DTYPE, "cross_entropy_bwd: labels must be int32 or int64");
+  if (n_rows < 0 || n_cols < 0) return fail(VBH_E_INVALID, "cross_entropy_bwd: negative size");
+  if (n_cols > kMaxCols) return fail(VBH_E_RANGE, "cross_entropy_bwd: n_cols too large");
+  if (logits_row_stride < n_cols || dlogits_row_stride < n_cols || dloss_stride < 0)
+    return fail(VBH_E_INVALID, "cross_entropy_bwd: bad stride");
+  if (n_rows == 0 || n_cols == 0) return 0;
+  if (!dloss || !logits || !lse || !labels || !dlogits)
+    return fail(VBH_E_INVALID, "cross_entropy_bwd: null pointer");
+  if (n_rows * 256 > kMaxWorkItems) return fail(VBH_E_RANGE, "cross_entropy_bwd: too many rows");
+  const int vn = 16 / elt_size(logits_dtype);
+  CeBwdArgs a;
+  a.dloss = static_cast<const float*>(dloss);
+  a.logits = logits;
+  a.lse = static_cast<const float*>(lse);
+  a.labels = labels;
+  a.dlogits = dlogits;
+  a.logits_dt = logits_dtype;
+  a.label_i64 = label_dtype == kI64;
+  a.n_rows = n_rows;
+  a.n_cols = static_cast<int>(n_cols);
+  a.ld_logits = logits_row_stride;
+  a.ld_dlogits = dlogits_row_stride;
+  a.dloss_stride = dloss_stride;
+  a.smoothing = smoothing;
+  a.logit_scale = logit_scale;
+  a.lse_square_scale = lse_square_scale;
+  a.ignored_index = ignored_index;
+  a.total_classes = static_cast<float>(total_classes);
+  a.class_start = class_start_idx;
+  a.has_smoothing = has_smoothing != 0;
+  a.vec = (n_cols % vn == 0 && logits_row_stride % vn == 0 && dlogits_row_stride % vn == 0 &&
+           aligned16(logits) && aligned16(dlogits))
+              ? vn
+              : 1;
+  return hip_status(launch_cross_entropy_bwd(a, static_cast<hipStream_t>(stream)),
+                    "cross_entropy_bwd launch");
+}
+
+int vbh_stream_copy(const void* src, void* dst, int64_t bytes, void* stream) {
+  if (bytes < 0 || bytes % 16 != 0)
+    return fail(VBH_E_INVALID, "stream_copy: bytes must be a non-negative multiple of 16");
+  if (bytes == 0) return 0;
+  if (!src || !dst || !aligned16(src) || !aligned16(dst))
+    return fail(VBH_E_INVALID, "stream_copy: pointers must be non-null and 16-byte aligned");
+  return hip_status(launch_stream_copy(src, dst, bytes, static_cast<hipStream_t>(stream)),
+                    "stream_copy launch");
+}
+
+}  // extern "C"

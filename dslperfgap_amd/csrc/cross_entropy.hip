@@ -1,0 +1,335 @@
+// Column-blocked cross-entropy forward and backward for gfx950.
+//
+// Forward: a "segment" is one (row, column block) pair, i.e. up to block_size
+// consecutive logits of one row.  `tpr` lanes own one segment, load it once
+// into fp32 registers (scaled by logit_scale; padding lanes hold -inf),
+// all-reduce max, sum of exp(x - max) and, with smoothing, the plain sum of the
+// logits, and one lane writes loss / lse / z_loss at flat index
+// cb * n_rows + row.  The label logit is fetched by that lane at kernel start,
+// so its latency overlaps the segment loads.  Segments wider than the register
+// budget use a streaming online (max, rescaled sum) pass.
+//
+// Semantics: ViperBench/cross_entropy/pytorch_impl.py:22-90 (golden) and
+// ViperBench/cross_entropy/triton_impl.py:33-75 (per-(row, block) program).
+// Backward: ViperBench/cross_entropy/pytorch_impl.py:93-141 and
+// ViperBench/cross_entropy/triton_impl.py:98-120.
+#include "vbh_device.h"
+#include "vbh_launch.h"
+
+namespace vbh {
+
+namespace {
+
+constexpr float kNegInf = -__builtin_huge_valf();
+
+// Scalar parameters.  The golden evaluates `1 - smoothing`,
+// `smoothing / total_classes` and `2.0 * lse_square_scale` in Python double
+// precision before they meet an fp32 tensor, so the host precomputes them in
+// double and rounds once.
+struct CeScalars {
+  float smoothing, logit_scale, lse_square_scale, total_classes;
+  float one_minus_smoothing, smooth_negative, two_lse_square_scale;
+  int64_t ignored_index, class_start;
+  int has_smoothing, split;
+};
+
+CeScalars make_scalars(float smoothing, float logit_scale, float lse_square_scale,
+                       float total_classes, int64_t ignored_index, int64_t class_start,
+                       int has_smoothing, int split) {
+  CeScalars c;
+  c.smoothing = smoothing;
+  c.logit_scale = logit_scale;
+  c.lse_square_scale = lse_square_scale;
+  c.total_classes = total_classes;
+  c.one_minus_smoothing = static_cast<float>(1.0 - static_cast<double>(smoothing));
+  c.smooth_negative =
+      static_cast<float>(static_cast<double>(smoothing) / static_cast<double>(total_classes));
+  c.two_lse_square_scale = static_cast<float>(2.0 * static_cast<double>(lse_square_scale));
+  c.ignored_index = ignored_index;
+  c.class_start = class_start;
+  c.has_smoothing = has_smoothing;
+  c.split = split;
+  return c;
+}
+
+__device__ __forceinline__ int64_t read_label(const void* labels, int label_i64, int64_t row) {
+  return label_i64 ? static_cast<const int64_t*>(labels)[row]
+                   : static_cast<int64_t>(static_cast<const int32_t*>(labels)[row]);
+}
+
+// Per-segment epilogue (pytorch_impl.py:37-76), executed by one lane.
+__device__ __forceinline__ void ce_store(float lse, float sum_logits, bool in_block,
+                                         float logit_label, bool ignored,
+                                         const CeScalars& c, float* loss, float* lse_out,
+                                         float* z_out, int64_t idx) {
+  lse_out[idx] = lse;
+  float l, z;
+  if (ignored) {
+    l = 0.f;
+    z = 0.f;
+  } else {
+    const float lse_term = c.split ? 0.f : lse;
+    if (c.has_smoothing) {
+      if (in_block)
+        l = lse_term - c.smoothing * sum_logits / c.total_classes -
+            c.one_minus_smoothing * logit_label;
+      else
+        l = c.smoothing * (lse_term - sum_logits / c.total_classes);
+    } else {
+      l = in_block ? lse_term - logit_label : 0.f;
+    }
+    if (!c.split) {
+      z = c.lse_square_scale * lse * lse;
+      l = l + z;
+    } else {
+      z = 0.f;
+    }
+  }
+  loss[idx] = l;
+  z_out[idx] = z;
+}
+
+template <typename T, int V, int MAXIT>
+__global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
+    const T* __restrict__ logits, const void* __restrict__ labels, int label_i64,
+    float* __restrict__ loss, float* __restrict__ lse_out, float* __restrict__ z_out,
+    int64_t n_rows, int n_cols, int64_t ld, int bs, int ncb, int tpr, CeScalars c) {
+  __shared__ float lds[3][kMaxWaves];
+  const int g = threadIdx.x & (tpr - 1);
+  const int64_t nseg = n_rows * ncb;
+  int64_t seg = static_cast<int64_t>(blockIdx.x) * (blockDim.x / tpr) + threadIdx.x / tpr;
+  const bool live = seg < nseg;
+  if (!live) seg = nseg - 1;
+  const int64_t row = seg / ncb;
+  const int cb = static_cast<int>(seg - row * ncb);
+  const int col0 = cb * bs;
+  const int col_end = min(n_cols, col0 + bs);
+  const int nvec = (col_end - col0) / V;
+  const T* lr = logits + row * ld;
+
+  // label logit, fetched early by the storing lane
+  bool ignored = false, in_block = false;
+  float logit_label = 0.f;
+  if (live && g == 0) {
+    const int64_t label = read_label(labels, label_i64, row);
+    ignored = label == c.ignored_index;
+    const int64_t adj = label - c.class_start;
+    in_block = adj >= col0 && adj < col_end;
+    if (!ignored && in_block) logit_label = static_cast<float>(lr[adj]) * c.logit_scale;
+  }
+
+  float v[MAXIT][V];
+#pragma unroll
+  for (int i = 0; i < MAXIT; ++i) {
+    const int j = i * tpr + g;
+    if (j < nvec) {
+      load_f32<T, V>(lr + col0 + static_cast<int64_t>(j) * V, v[i]);
+#pragma unroll
+      for (int k = 0; k < V; ++k) v[i][k] *= c.logit_scale;
+    } else {
+#pragma unroll
+      for (int k = 0; k < V; ++k) v[i][k] = kNegInf;
+    }
+  }
+
+  float mx[V];
+#pragma unroll
+  for (int k = 0; k < V; ++k) mx[k] = v[0][k];
+#pragma unroll
+  for (int i = 1; i < MAXIT; ++i)
+#pragma unroll
+    for (int k = 0; k < V; ++k) mx[k] = fmaxf(mx[k], v[i][k]);
+  float lm = mx[0];
+#pragma unroll
+  for (int k = 1; k < V; ++k) lm = fmaxf(lm, mx[k]);
+  const float m = group_allreduce<Max>(lm, tpr, lds[0]);
+
+  float se[V], sl[V];
+#pragma unroll
+  for (int k = 0; k < V; ++k) se[k] = sl[k] = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXIT; ++i) {
+#pragma unroll
+    for (int k = 0; k < V; ++k) se[k] += fast_exp(v[i][k] - m);
+    if (c.has_smoothing && i * tpr + g < nvec) {
+#pragma unroll
+      for (int k = 0; k < V; ++k) sl[k] += v[i][k];
+    }
+  }
+#pragma unroll
+  for (int w = V / 2; w >= 1; w /= 2)
+#pragma unroll
+    for (int k = 0; k < w; ++k) {
+      se[k] += se[k + w];
+      sl[k] += sl[k + w];
+    }
+  const float s = group_allreduce<Sum>(se[0], tpr, lds[1]);
+  float sum_logits = 0.f;
+  if (c.has_smoothing) sum_logits = group_allreduce<Sum>(sl[0], tpr, lds[2]);
+
+  if (live && g == 0) {
+    const float lse = fast_log(s) + m;
+    ce_store(lse, sum_logits, in_block, logit_label, ignored, c, loss, lse_out, z_out,
+             static_cast<int64_t>(cb) * n_rows + row);
+  }
+}
+
+// Segments wider than the register budget: one workgroup per segment,
+// online (max, rescaled sum) over 16-byte chunks.
+template <typename T, int V>
+__global__ __launch_bounds__(kMaxBlock) void ce_fwd_stream(
+    const T* __restrict__ logits, const void* __restrict__ labels, int label_i64,
+    float* __restrict__ loss, float* __restrict__ lse_out, float* __restrict__ z_out,
+    int64_t n_rows, int n_cols, int64_t ld, int bs, int ncb, CeScalars c) {
+  __shared__ float lds[3][kMaxWaves];
+  const int tpr = blockDim.x;
+  const int64_t seg = blockIdx.x;
+  const int64_t row = seg / ncb;
+  const int cb = static_cast<int>(seg - row * ncb);
+  const int col0 = cb * bs;
+  const int col_end = min(n_cols, col0 + bs);
+  const int nvec = (col_end - col0) / V;
+  const T* lr = logits + row * ld + col0;
+
+  // per-thread running max (NaN ignored), rescaled sum, NaN-propagating sum of logits
+  float m = kNegInf, s = 0.f, sl = 0.f, nan = 0.f;
+  for (int j = threadIdx.x; j < nvec; j += tpr) {
+    float v[V];
+    load_f32<T, V>(lr + static_cast<int64_t>(j) * V, v);
+    float cm = kNegInf;
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      v[k] *= c.logit_scale;
+      cm = fmaxf(cm, v[k]);
+      sl += v[k];
+      if (v[k] != v[k]) nan = 1.f;
+    }
+    if (cm > m) {
+      s = (m == kNegInf) ? 0.f : s * fast_exp(m - cm);
+      m = cm;
+    }
+    if (m != kNegInf && m != -kNegInf) {
+#pragma unroll
+      for (int k = 0; k < V; ++k) s += (v[k] != v[k]) ? 0.f : fast_exp(v[k] - m);
+    }
+  }
+  const float gm = group_allreduce<Max>(m, tpr, lds[0]);
+  const bool finite = gm != kNegInf && gm != -kNegInf;
+  const float t = (finite && m != kNegInf) ? s * fast_exp(m - gm) : 0.f;
+  const float gs = group_allreduce<Sum>(t, tpr, lds[1]);
+  // The NaN flag rides on the sum of logits: a NaN logit makes that sum NaN in
+  // the golden as well (pytorch_impl.py:56).
+  const float gl = group_allreduce<Sum>(nan != 0.f ? __builtin_nanf("") : sl, tpr, lds[2]);
+  if (threadIdx.x != 0) return;
+  // Golden lse = log(sum(exp(L - max))) + max with a NaN-propagating max: a NaN
+  // logit, a +inf max (inf - inf) or an all -inf segment (-inf - -inf) give NaN.
+  const bool has_nan = nan != 0.f || (gl != gl);
+  const float lse = (has_nan || !finite) ? __builtin_nanf("") : fast_log(gs) + gm;
+  const int64_t label = read_label(labels, label_i64, row);
+  const bool ignored = label == c.ignored_index;
+  const int64_t adj = label - c.class_start;
+  const bool in_block = adj >= col0 && adj < col_end;
+  float logit_label = 0.f;
+  if (!ignored && in_block)
+    logit_label = static_cast<float>(logits[row * ld + adj]) * c.logit_scale;
+  ce_store(lse, gl, in_block, logit_label, ignored, c, loss, lse_out, z_out,
+           static_cast<int64_t>(cb) * n_rows + row);
+}
+
+// Backward: one workgroup per row, elementwise over the row.
+template <typename T, int V>
+__global__ __launch_bounds__(256) void ce_bwd_rows(
+    const float* __restrict__ dloss, const T* __restrict__ logits,
+    const float* __restrict__ lse, const void* __restrict__ labels, int label_i64,
+    T* __restrict__ dlogits, int n_cols, int64_t ld_in, int64_t ld_out,
+    int64_t dloss_stride, CeScalars c) {
+  const int64_t row = blockIdx.x;
+  const int64_t label = read_label(labels, label_i64, row);
+  const float dl = label != c.ignored_index ? dloss[row * dloss_stride] : 0.f;
+  const float lse_r = lse[row];
+  const int64_t adj = label - c.class_start;
+  // (dl * logit_scale) is a Python-double product in the golden
+  const float scale = static_cast<float>(static_cast<double>(dl) * c.logit_scale);
+  const float zfac = c.two_lse_square_scale * lse_r;
+  const float smooth_neg = c.has_smoothing ? c.smooth_negative : 0.f;
+  const float hit = c.has_smoothing ? c.one_minus_smoothing : 1.0f;
+  const T* lr = logits + row * ld_in;
+  T* dr = dlogits + row * ld_out;
+  const int nvec = n_cols / V;
+  for (int j = threadIdx.x; j < nvec; j += blockDim.x) {
+    float v[V], o[V];
+    load_f32<T, V>(lr + static_cast<int64_t>(j) * V, v);
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      float p = fast_exp(v[k] * c.logit_scale - lse_r);
+      p = p + zfac * p;
+      const int64_t col = static_cast<int64_t>(j) * V + k;
+      if (col == adj) p = p - hit;
+      if (c.has_smoothing) p = p - smooth_neg;
+      o[k] = scale * p;
+    }
+    store_from_f32<T, V>(dr + static_cast<int64_t>(j) * V, o);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_cross_entropy_fwd(const CeArgs& a, const Geometry& g, hipStream_t s) {
+  hipError_t err = hipErrorInvalidValue;
+  const CeScalars c =
+      make_scalars(a.smoothing, a.logit_scale, a.lse_square_scale, a.total_classes,
+                   a.ignored_index, a.class_start, a.has_smoothing, a.split);
+  const int64_t nseg = a.n_rows * a.ncb;
+  dispatch_float_type(a.logits_dt, [&](auto tt) {
+    using T = typename decltype(tt)::type;
+    constexpr int VN = Vec<T>::n;
+    auto go = [&](auto vc) {
+      constexpr int V = decltype(vc)::value;
+      if (g.stream) {
+        hipLaunchKernelGGL((ce_fwd_stream<T, V>), dim3(nseg), dim3(g.block), 0, s,
+                           static_cast<const T*>(a.logits), a.labels, a.label_i64, a.loss,
+                           a.lse, a.z_loss, a.n_rows, a.n_cols, a.ld, a.block_size, a.ncb,
+                           c);
+        err = hipGetLastError();
+        return;
+      }
+      dispatch_maxit(g.maxit, [&](auto mc) {
+        constexpr int M = decltype(mc)::value;
+        if constexpr (M <= lane_cap(V)) {
+          hipLaunchKernelGGL((ce_fwd_rows<T, V, M>), dim3(grid_for(nseg, g)), dim3(g.block),
+                             0, s, static_cast<const T*>(a.logits), a.labels, a.label_i64,
+                             a.loss, a.lse, a.z_loss, a.n_rows, a.n_cols, a.ld,
+                             a.block_size, a.ncb, g.tpr, c);
+          err = hipGetLastError();
+        }
+      });
+    };
+    if (g.v == 1) go(std::integral_constant<int, 1>{});
+    else go(std::integral_constant<int, VN>{});
+  });
+  return err;
+}
+
+hipError_t launch_cross_entropy_bwd(const CeBwdArgs& a, hipStream_t s) {
+  hipError_t err = hipErrorInvalidValue;
+  const CeScalars c =
+      make_scalars(a.smoothing, a.logit_scale, a.lse_square_scale, a.total_classes,
+                   a.ignored_index, a.class_start, a.has_smoothing, 0);
+  dispatch_float_type(a.logits_dt, [&](auto tt) {
+    using T = typename decltype(tt)::type;
+    constexpr int VN = Vec<T>::n;
+    auto go = [&](auto vc) {
+      constexpr int V = decltype(vc)::value;
+      hipLaunchKernelGGL((ce_bwd_rows<T, V>), dim3(a.n_rows), dim3(256), 0, s, a.dloss,
+                         static_cast<const T*>(a.logits), a.lse, a.labels, a.label_i64,
+                         static_cast<T*>(a.dlogits), a.n_cols, a.ld_logits, a.ld_dlogits,
+                         a.dloss_stride, c);
+      err = hipGetLastError();
+    };
+    if (a.vec == 1) go(std::integral_constant<int, 1>{});
+    else go(std::integral_constant<int, VN>{});
+  });
+  return err;
+}
+
+}  // namespace vbh

@@ -1,0 +1,367 @@
+// Softmax, log-softmax and logsumexp forward for gfx950.
+//
+// Register-resident path: `tpr` lanes own one row, load it once into fp32
+// registers (padding lanes hold -inf), all-reduce the row max, then the sum of
+// exp(x - max), and write the row once.
+// Streaming path (rows wider than the register budget): one workgroup per row,
+// online (max, rescaled sum) statistics pass, then an output pass.
+// Middle-axis path: contiguous [outer, n, inner] reduced over n; one thread per
+// (outer, inner) column, consecutive threads on consecutive inner indices so
+// every access is coalesced.
+//
+// Semantics: ViperBench/softmax/pytorch_impl.py:4-6 (F.softmax, dim=-1),
+// ViperBench/log_softmax/pytorch_impl.py:4-8 (F.log_softmax(x, dim, dtype)),
+// ViperBench/logsumexp/pytorch_impl.py:3-5 (torch.logsumexp, dim=-1: the max
+// used for the shift is replaced by 0 when it is infinite).
+#include "vbh_device.h"
+#include "vbh_launch.h"
+
+namespace vbh {
+
+namespace {
+
+constexpr float kNegInf = -__builtin_huge_valf();
+
+template <typename T, int V, int MAXIT>
+__device__ __forceinline__ void load_row_fill(const T* __restrict__ xr, int nvec, int g,
+                                              int tpr, float fill, float (&v)[MAXIT][V]) {
+#pragma unroll
+  for (int i = 0; i < MAXIT; ++i) {
+    const int j = i * tpr + g;
+    if (j < nvec) {
+      load_f32<T, V>(xr + static_cast<int64_t>(j) * V, v[i]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < V; ++k) v[i][k] = fill;
+    }
+  }
+}
+
+template <int MAXIT, int V>
+__device__ __forceinline__ float lane_max(const float (&v)[MAXIT][V]) {
+  float m[V];
+#pragma unroll
+  for (int k = 0; k < V; ++k) m[k] = v[0][k];
+#pragma unroll
+  for (int i = 1; i < MAXIT; ++i)
+#pragma unroll
+    for (int k = 0; k < V; ++k) m[k] = fmaxf(m[k], v[i][k]);
+  float r = m[0];
+#pragma unroll
+  for (int k = 1; k < V; ++k) r = fmaxf(r, m[k]);
+  return r;
+}
+
+// sum over the lane's values of exp(v - shift); padding values are -inf and
+// contribute exp(-inf) = 0 whenever shift is finite.
+template <int MAXIT, int V>
+__device__ __forceinline__ float lane_sum_exp(const float (&v)[MAXIT][V], float shift) {
+  float a[V];
+#pragma unroll
+  for (int k = 0; k < V; ++k) a[k] = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXIT; ++i)
+#pragma unroll
+    for (int k = 0; k < V; ++k) a[k] += fast_exp(v[i][k] - shift);
+#pragma unroll
+  for (int w = V / 2; w >= 1; w /= 2)
+#pragma unroll
+    for (int k = 0; k < w; ++k) a[k] += a[k + w];
+  return a[0];
+}
+
+template <typename Ti, typename To, int V, int MAXIT, bool LOG>
+__global__ __launch_bounds__(kMaxBlock) void softmax_rows(const Ti* __restrict__ x,
+                                                          To* __restrict__ y, int64_t rows,
+                                                          int cols, int tpr) {
+  __shared__ float lds[2][kMaxWaves];
+  const int nvec = cols / V;
+  const int g = threadIdx.x & (tpr - 1);
+  int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / tpr) + threadIdx.x / tpr;
+  const bool live = row < rows;
+  if (!live) row = rows - 1;
+
+  float v[MAXIT][V];
+  load_row_fill<Ti, V, MAXIT>(x + row * cols, nvec, g, tpr, kNegInf, v);
+  const float m = group_allreduce<Max>(lane_max<MAXIT, V>(v), tpr, lds[0]);
+  const float s = group_allreduce<Sum>(lane_sum_exp<MAXIT, V>(v, m), tpr, lds[1]);
+  if (!live) return;
+
+  To* yr = y + row * cols;
+  if constexpr (LOG) {
+    const float ls = fast_log(s);
+#pragma unroll
+    for (int i = 0; i < MAXIT; ++i) {
+      const int j = i * tpr + g;
+      if (j < nvec) {
+        float o[V];
+#pragma unroll
+        for (int k = 0; k < V; ++k) o[k] = (v[i][k] - m) - ls;
+        store_from_f32<To, V>(yr + static_cast<int64_t>(j) * V, o);
+      }
+    }
+  } else {
+    const float r = 1.0f / s;
+#pragma unroll
+    for (int i = 0; i < MAXIT; ++i) {
+      const int j = i * tpr + g;
+      if (j < nvec) {
+        float o[V];
+#pragma unroll
+        for (int k = 0; k < V; ++k) o[k] = fast_exp(v[i][k] - m) * r;
+        store_from_f32<To, V>(yr + static_cast<int64_t>(j) * V, o);
+      }
+    }
+  }
+}
+
+template <typename Ti, typename To, int V, int MAXIT>
+__global__ __launch_bounds__(kMaxBlock) void logsumexp_rows(const Ti* __restrict__ x,
+                                                            To* __restrict__ y, int64_t rows,
+                                                            int cols, int tpr) {
+  __shared__ float lds[2][kMaxWaves];
+  const int nvec = cols / V;
+  const int g = threadIdx.x & (tpr - 1);
+  int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / tpr) + threadIdx.x / tpr;
+  const bool live = row < rows;
+  if (!live) row = rows - 1;
+
+  float v[MAXIT][V];
+  load_row_fill<Ti, V, MAXIT>(x + row * cols, nvec, g, tpr, kNegInf, v);
+  float m = group_allreduce<Max>(lane_max<MAXIT, V>(v), tpr, lds[0]);
+  if (__builtin_isinf(m)) m = 0.f;
+  const float s = group_allreduce<Sum>(lane_sum_exp<MAXIT, V>(v, m), tpr, lds[1]);
+  if (live && g == 0) {
+    const float r = fast_log(s) + m;
+    store_from_f32<To, 1>(y + row, &r);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// streaming (one workgroup per row)
+// ---------------------------------------------------------------------------
+
+// Online row statistics for the streaming path: running max `m` (NaN ignored),
+// sum `s` of exp(x - m) rescaled whenever m grows, and a NaN flag.  The final
+// outputs reproduce torch's special values explicitly:
+//   softmax / log_softmax: a row holding NaN or +inf, or only -inf, is all NaN;
+//   logsumexp: NaN row -> NaN, a +inf max -> +inf, an all -inf row -> -inf.
+struct RowStats {
+  float m, s, nan;
+};
+
+template <typename T, int V>
+__device__ __forceinline__ RowStats stream_stats(const T* __restrict__ xr, int nvec,
+                                                 float* lds) {
+  float m = kNegInf, s = 0.f, nan = 0.f;
+  for (int j = threadIdx.x; j < nvec; j += blockDim.x) {
+    float v[V];
+    load_f32<T, V>(xr + static_cast<int64_t>(j) * V, v);
+    float cm = kNegInf;
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      cm = fmaxf(cm, v[k]);
+      if (v[k] != v[k]) nan = 1.f;
+    }
+    if (cm > m) {
+      s = (m == kNegInf) ? 0.f : s * fast_exp(m - cm);
+      m = cm;
+    }
+    if (m != kNegInf && m != -kNegInf) {
+#pragma unroll
+      for (int k = 0; k < V; ++k) s += (v[k] != v[k]) ? 0.f : fast_exp(v[k] - m);
+    }
+  }
+  const int tpr = blockDim.x;
+  const float gm = group_allreduce<Max>(m, tpr, lds);
+  const bool finite = gm != kNegInf && gm != -kNegInf;
+  const float t = (finite && m != kNegInf) ? s * fast_exp(m - gm) : 0.f;
+  const float gs = group_allreduce<Sum>(t, tpr, lds + kMaxWaves);
+  const float gn = group_allreduce<Max>(nan, tpr, lds + 2 * kMaxWaves);
+  return RowStats{gm, gs, gn};
+}
+
+template <typename Ti, typename To, int V, bool LOG>
+__global__ __launch_bounds__(kMaxBlock) void softmax_stream(const Ti* __restrict__ x,
+                                                            To* __restrict__ y, int cols) {
+  __shared__ float lds[3 * kMaxWaves];
+  const int nvec = cols / V;
+  const int64_t row = blockIdx.x;
+  const Ti* xr = x + row * cols;
+  const RowStats st = stream_stats<Ti, V>(xr, nvec, lds);
+  const bool special = st.nan != 0.f || st.m == kNegInf || st.m == -kNegInf;
+  const float qnan = __builtin_nanf("");
+  const float m = st.m;
+  To* yr = y + row * cols;
+  if constexpr (LOG) {
+    const float ls = special ? qnan : fast_log(st.s);
+    for (int j = threadIdx.x; j < nvec; j += blockDim.x) {
+      float v[V], o[V];
+      load_f32<Ti, V>(xr + static_cast<int64_t>(j) * V, v);
+#pragma unroll
+      for (int k = 0; k < V; ++k) o[k] = (v[k] - m) - ls;
+      store_from_f32<To, V>(yr + static_cast<int64_t>(j) * V, o);
+    }
+  } else {
+    const float r = special ? qnan : 1.0f / st.s;
+    for (int j = threadIdx.x; j < nvec; j += blockDim.x) {
+      float v[V], o[V];
+      load_f32<Ti, V>(xr + static_cast<int64_t>(j) * V, v);
+#pragma unroll
+      for (int k = 0; k < V; ++k) o[k] = fast_exp(v[k] - m) * r;
+      store_from_f32<To, V>(yr + static_cast<int64_t>(j) * V, o);
+    }
+  }
+}
+
+template <typename Ti, typename To, int V>
+__global__ __launch_bounds__(kMaxBlock) void logsumexp_stream(const Ti* __restrict__ x,
+                                                              To* __restrict__ y, int cols) {
+  __shared__ float lds[3 * kMaxWaves];
+  const int nvec = cols / V;
+  const int64_t row = blockIdx.x;
+  const RowStats st = stream_stats<Ti, V>(x + row * cols, nvec, lds);
+  if (threadIdx.x == 0) {
+    float r;
+    if (st.nan != 0.f) r = __builtin_nanf("");
+    else if (st.m == kNegInf || st.m == -kNegInf) r = st.m;
+    else r = fast_log(st.s) + st.m;
+    store_from_f32<To, 1>(y + row, &r);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// middle axis: [outer, n, inner], reduce over n
+// ---------------------------------------------------------------------------
+template <typename Ti, typename To, bool LOG>
+__global__ __launch_bounds__(256) void softmax_mid(const Ti* __restrict__ x,
+                                                   To* __restrict__ y, int64_t outer, int n,
+                                                   int64_t inner) {
+  const int64_t col = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (col >= outer * inner) return;
+  const int64_t o = col / inner;
+  const int64_t i = col - o * inner;
+  const Ti* xc = x + o * n * inner + i;
+  To* yc = y + o * n * inner + i;
+  float m = kNegInf;
+  for (int r = 0; r < n; ++r) m = fmaxf(m, static_cast<float>(xc[r * inner]));
+  float s = 0.f;
+  for (int r = 0; r < n; ++r) s += fast_exp(static_cast<float>(xc[r * inner]) - m);
+  if constexpr (LOG) {
+    const float ls = fast_log(s);
+    for (int r = 0; r < n; ++r) {
+      const float out = (static_cast<float>(xc[r * inner]) - m) - ls;
+      store_from_f32<To, 1>(yc + r * inner, &out);
+    }
+  } else {
+    const float rs = 1.0f / s;
+    for (int r = 0; r < n; ++r) {
+      const float out = fast_exp(static_cast<float>(xc[r * inner]) - m) * rs;
+      store_from_f32<To, 1>(yc + r * inner, &out);
+    }
+  }
+}
+
+// (in, out) dtype pairs: same type, or fp16/bf16 in with fp32 out
+template <typename Fn>
+bool dispatch_in_out(int idt, int odt, Fn&& fn) {
+  if (idt == odt) {
+    return dispatch_float_type(idt, [&](auto t) { fn(t, t); });
+  }
+  if (odt == kF32 && (idt == kF16 || idt == kBF16)) {
+    return dispatch_float_type(idt, [&](auto t) { fn(t, TypeTag<float>{}); });
+  }
+  return false;
+}
+
+}  // namespace
+
+hipError_t launch_softmax(const void* x, void* y, int64_t rows, int cols, int idt, int odt,
+                          int log_mode, const Geometry& g, hipStream_t s) {
+  hipError_t err = hipErrorInvalidValue;
+  dispatch_in_out(idt, odt, [&](auto ti, auto to) {
+    using Ti = typename decltype(ti)::type;
+    using To = typename decltype(to)::type;
+    constexpr int VN = Vec<Ti>::n;
+    auto go = [&](auto vc, auto lc) {
+      constexpr int V = decltype(vc)::value;
+      constexpr bool LOG = decltype(lc)::value;
+      if (g.stream) {
+        hipLaunchKernelGGL((softmax_stream<Ti, To, V, LOG>), dim3(rows), dim3(g.block), 0, s,
+                           static_cast<const Ti*>(x), static_cast<To*>(y), cols);
+        err = hipGetLastError();
+        return;
+      }
+      dispatch_maxit(g.maxit, [&](auto mc) {
+        constexpr int M = decltype(mc)::value;
+        if constexpr (M <= lane_cap(V)) {
+          hipLaunchKernelGGL((softmax_rows<Ti, To, V, M, LOG>), dim3(grid_for(rows, g)),
+                             dim3(g.block), 0, s, static_cast<const Ti*>(x),
+                             static_cast<To*>(y), rows, cols, g.tpr);
+          err = hipGetLastError();
+        }
+      });
+    };
+    auto with_log = [&](auto vc) {
+      if (log_mode) go(vc, std::true_type{});
+      else go(vc, std::false_type{});
+    };
+    if (g.v == 1) with_log(std::integral_constant<int, 1>{});
+    else with_log(std::integral_constant<int, VN>{});
+  });
+  return err;
+}
+
+hipError_t launch_logsumexp(const void* x, void* y, int64_t rows, int cols, int idt, int odt,
+                            const Geometry& g, hipStream_t s) {
+  hipError_t err = hipErrorInvalidValue;
+  auto body = [&](auto ti, auto to) {
+    using Ti = typename decltype(ti)::type;
+    using To = typename decltype(to)::type;
+    constexpr int VN = Vec<Ti>::n;
+    auto go = [&](auto vc) {
+      constexpr int V = decltype(vc)::value;
+      if (g.stream) {
+        hipLaunchKernelGGL((logsumexp_stream<Ti, To, V>), dim3(rows), dim3(g.block), 0, s,
+                           static_cast<const Ti*>(x), static_cast<To*>(y), cols);
+        err = hipGetLastError();
+        return;
+      }
+      dispatch_maxit(g.maxit, [&](auto mc) {
+        constexpr int M = decltype(mc)::value;
+        if constexpr (M <= lane_cap(V)) {
+          hipLaunchKernelGGL((logsumexp_rows<Ti, To, V, M>), dim3(grid_for(rows, g)),
+                             dim3(g.block), 0, s, static_cast<const Ti*>(x),
+                             static_cast<To*>(y), rows, cols, g.tpr);
+          err = hipGetLastError();
+        }
+      });
+    };
+    if (g.v == 1) go(std::integral_constant<int, 1>{});
+    else go(std::integral_constant<int, VN>{});
+  };
+  dispatch_in_out(idt, odt, body);
+  return err;
+}
+
+hipError_t launch_softmax_dim(const void* x, void* y, int64_t outer, int n, int64_t inner,
+                              int idt, int odt, int log_mode, hipStream_t s) {
+  hipError_t err = hipErrorInvalidValue;
+  const int64_t cols = outer * inner;
+  const int block = 256;
+  const int64_t grid = (cols + block - 1) / block;
+  dispatch_in_out(idt, odt, [&](auto ti, auto to) {
+    using Ti = typename decltype(ti)::type;
+    using To = typename decltype(to)::type;
+    if (log_mode)
+      hipLaunchKernelGGL((softmax_mid<Ti, To, true>), dim3(grid), dim3(block), 0, s,
+                         static_cast<const Ti*>(x), static_cast<To*>(y), outer, n, inner);
+    else
+      hipLaunchKernelGGL((softmax_mid<Ti, To, false>), dim3(grid), dim3(block), 0, s,
+                         static_cast<const Ti*>(x), static_cast<To*>(y), outer, n, inner);
+    err = hipGetLastError();
+  });
+  return err;
+}
+
+}  // namespace vbh

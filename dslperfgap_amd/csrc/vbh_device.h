@@ -1,0 +1,203 @@
+// Device building blocks shared by every row kernel of libvbhip (gfx950 / CDNA4).
+//
+//  * 16-byte global loads/stores with conversion to and from fp32 registers
+//    (fp32 x4, fp16 x8, bf16 x8; scalar variants for unaligned rows).
+//  * Group all-reduce over `tpr` consecutive lanes (tpr a power of two):
+//    DPP quad_perm / row_half_mirror / row_mirror inside a 16-lane row,
+//    v_permlane16_swap and v_permlane32_swap across rows of one wave64,
+//    and an LDS exchange across the waves of a workgroup when tpr > 64.
+//    Every step combines a value with its partner through a commutative
+//    operation, so all lanes of a group end with bit-identical results.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vbh {
+
+constexpr int kWave = 64;
+constexpr int kMaxBlock = 1024;
+constexpr int kMaxWaves = kMaxBlock / kWave;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// Elements per 16-byte vector for each storage type.
+template <typename T> struct Vec;
+template <> struct Vec<float> { static constexpr int n = 4; };
+template <> struct Vec<_Float16> { static constexpr int n = 8; };
+template <> struct Vec<__bf16> { static constexpr int n = 8; };
+
+// ---------------------------------------------------------------------------
+// loads / stores
+// ---------------------------------------------------------------------------
+
+// Read V consecutive elements at p (V == Vec<T>::n: one 16-byte load, p 16-byte
+// aligned; V == 1: one element) and widen them to fp32.
+template <typename T, int V>
+__device__ __forceinline__ void load_f32(const T* __restrict__ p, float* o) {
+  if constexpr (V == 1) {
+    o[0] = static_cast<float>(p[0]);
+  } else {
+    typedef T vec_t __attribute__((ext_vector_type(V)));
+    const vec_t v = *reinterpret_cast<const vec_t*>(p);
+#pragma unroll
+    for (int k = 0; k < V; ++k) o[k] = static_cast<float>(v[k]);
+  }
+}
+
+// Round V fp32 values to T (round-to-nearest-even, NaN preserved) and store.
+template <typename T, int V>
+__device__ __forceinline__ void store_from_f32(T* __restrict__ p, const float* o) {
+  if constexpr (V == 1) {
+    p[0] = static_cast<T>(o[0]);
+  } else {
+    typedef T vec_t __attribute__((ext_vector_type(V)));
+    vec_t v;
+#pragma unroll
+    for (int k = 0; k < V; ++k) v[k] = static_cast<T>(o[k]);
+    *reinterpret_cast<vec_t*>(p) = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// reductions
+// ---------------------------------------------------------------------------
+
+struct Sum {
+  __device__ static float apply(float a, float b) { return a + b; }
+};
+// fmaxf drops a NaN operand.  The row kernels never expose the max itself:
+// every output that depends on it also depends on exp(x - max) summed over the
+// row, and a NaN element poisons that sum, so NaN rows still come out NaN.
+struct Max {
+  __device__ static float apply(float a, float b) { return fmaxf(a, b); }
+};
+
+template <int Ctrl>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(v), Ctrl, 0xF, 0xF, false));
+}
+
+// All-reduce across aligned groups of `width` lanes of one wave64
+// (width a power of two in [1, 64], uniform across the wave).
+template <class Op>
+__device__ __forceinline__ float wave_allreduce(float v, int width) {
+  if (width >= 2) v = Op::apply(v, dpp<0xB1>(v));   // quad_perm [1,0,3,2]: lane ^ 1
+  if (width >= 4) v = Op::apply(v, dpp<0x4E>(v));   // quad_perm [2,3,0,1]: lane ^ 2
+  if (width >= 8) v = Op::apply(v, dpp<0x141>(v));  // row_half_mirror: other quad of 8
+  if (width >= 16) v = Op::apply(v, dpp<0x140>(v)); // row_mirror: other half of 16
+  if (width >= 32) {
+    // rows (0,1) and (2,3) exchange: lo = even row, hi = odd row in every lane
+    auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                              false, false);
+    v = Op::apply(__uint_as_float(p[0]), __uint_as_float(p[1]));
+  }
+  if (width >= 64) {
+    auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                              false, false);
+    v = Op::apply(__uint_as_float(p[0]), __uint_as_float(p[1]));
+  }
+  return v;
+}
+
+// All-reduce across the `tpr` threads that own one row.  For tpr <= 64 the
+// group lives inside one wave; for tpr > 64 a row spans tpr / 64 consecutive
+// waves of the workgroup and wave partials are exchanged through `lds`
+// (kMaxWaves floats, one slot per wave of the workgroup).  When tpr > 64 every
+// thread of the workgroup must reach the call (it contains a barrier), and each
+// `lds` buffer may serve only one reduction per kernel instance (there is no
+// trailing barrier).
+template <class Op>
+__device__ __forceinline__ float group_allreduce(float v, int tpr, float* lds) {
+  if (tpr <= kWave) return wave_allreduce<Op>(v, tpr);
+  v = wave_allreduce<Op>(v, kWave);
+  const int wave = threadIdx.x / kWave;
+  const int nwaves = tpr / kWave;
+  const int first = wave - (wave & (nwaves - 1));
+  if ((threadIdx.x & (kWave - 1)) == 0) lds[wave] = v;
+  __syncthreads();
+  float r = lds[first];
+  for (int w = 1; w < nwaves; ++w) r = Op::apply(r, lds[first + w]);
+  return r;
+}
+
+// Welford / Chan partial statistics (count, mean, sum of squared deviations).
+struct Moments {
+  float n, mean, m2;
+};
+
+// Chan et al. pairwise merge in a form that is symmetric in (a, b), so both
+// partners of a butterfly step compute bit-identical results.
+__device__ __forceinline__ Moments merge_moments(Moments a, Moments b) {
+  const float n = a.n + b.n;
+  if (n == 0.f) return Moments{0.f, 0.f, 0.f};
+  const float inv = 1.0f / n;
+  const float d = b.mean - a.mean;
+  Moments r;
+  r.n = n;
+  r.mean = (a.n * a.mean + b.n * b.mean) * inv;
+  r.m2 = (a.m2 + b.m2) + d * d * (a.n * b.n * inv);
+  return r;
+}
+
+template <int Ctrl>
+__device__ __forceinline__ Moments dpp_moments(Moments m) {
+  return Moments{dpp<Ctrl>(m.n), dpp<Ctrl>(m.mean), dpp<Ctrl>(m.m2)};
+}
+
+__device__ __forceinline__ float swap16_partner(float v) {
+  // lane i receives lane i ^ 16
+  auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                            false);
+  const bool odd_row = (threadIdx.x & 16) != 0;
+  return __uint_as_float(odd_row ? p[0] : p[1]);
+}
+__device__ __forceinline__ float swap32_partner(float v) {
+  // lane i receives lane i ^ 32
+  auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                            false);
+  const bool hi = (threadIdx.x & 32) != 0;
+  return __uint_as_float(hi ? p[0] : p[1]);
+}
+
+// All-reduce of Moments over the `tpr` threads of one row (see group_allreduce;
+// `lds` must hold 3 * kMaxWaves floats).
+__device__ __forceinline__ Moments group_allreduce_moments(Moments m, int tpr, float* lds) {
+  const int width = tpr < kWave ? tpr : kWave;
+  if (width >= 2) m = merge_moments(m, dpp_moments<0xB1>(m));
+  if (width >= 4) m = merge_moments(m, dpp_moments<0x4E>(m));
+  if (width >= 8) m = merge_moments(m, dpp_moments<0x141>(m));
+  if (width >= 16) m = merge_moments(m, dpp_moments<0x140>(m));
+  if (width >= 32)
+    m = merge_moments(m, Moments{swap16_partner(m.n), swap16_partner(m.mean),
+                                 swap16_partner(m.m2)});
+  if (width >= 64)
+    m = merge_moments(m, Moments{swap32_partner(m.n), swap32_partner(m.mean),
+                                 swap32_partner(m.m2)});
+  if (tpr <= kWave) return m;
+  const int wave = threadIdx.x / kWave;
+  const int nwaves = tpr / kWave;
+  const int first = wave - (wave & (nwaves - 1));
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    lds[wave] = m.n;
+    lds[kMaxWaves + wave] = m.mean;
+    lds[2 * kMaxWaves + wave] = m.m2;
+  }
+  __syncthreads();
+  Moments r{lds[first], lds[kMaxWaves + first], lds[2 * kMaxWaves + first]};
+  for (int w = first + 1; w < first + nwaves; ++w)
+    r = merge_moments(r, Moments{lds[w], lds[kMaxWaves + w], lds[2 * kMaxWaves + w]});
+  return r;
+}
+
+// Fast exp / log on the hardware transcendental unit (v_exp_f32 / v_log_f32,
+// 1 ulp in the base-2 domain).  exp(x) = 2^(x * log2 e); log(x) = log2(x) * ln 2.
+__device__ __forceinline__ float fast_exp(float x) {
+  return __builtin_amdgcn_exp2f(x * kLog2e);
+}
+__device__ __forceinline__ float fast_log(float x) {
+  return __builtin_amdgcn_logf(x) * kLn2;
+}
+
+}  // namespace vbh

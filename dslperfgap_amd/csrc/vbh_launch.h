@@ -1,0 +1,145 @@
+// Host-side contract between the C ABI (capi.hip) and the kernel translation
+// units.  Argument checking happens in capi.hip; the launchers below assume
+// valid sizes, dtype codes and a geometry produced by pick_geometry().
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+#include <utility>
+
+namespace vbh {
+
+enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2, kI32 = 3, kI64 = 4 };
+
+// Launch geometry of a row kernel.
+//   v      elements per lane access (16-byte vector width, or 1 for rows that
+//          are not 16-byte aligned)
+//   tpr    threads per row (power of two, 1..1024)
+//   block  workgroup size (a multiple of 64 and of tpr)
+//   maxit  vectors held in registers per lane (power of two)
+//   stream row too wide for registers: chunked two-pass kernel instead
+struct Geometry {
+  int v = 1;
+  int tpr = 64;
+  int block = 256;
+  int maxit = 1;
+  bool stream = false;
+};
+
+// Register budget per lane for the register-resident path: at most 64 fp32
+// values and at most 32 separate accesses (scalar rows spill beyond that).
+constexpr int kLaneValues = 64;
+constexpr int kMaxIters = 32;
+constexpr int lane_cap(int vec) {
+  return kLaneValues / vec < kMaxIters ? kLaneValues / vec : kMaxIters;
+}
+
+// Choose the geometry for rows of `cols` elements.  `vec` is the 16-byte vector
+// width when every row start is 16-byte aligned and cols % vec == 0, else 1.
+// `tpr_override` / `block_override` come from vbh_tune_override (0 = none).
+Geometry pick_geometry(int64_t cols, int vec, int tpr_override, int block_override);
+
+// ---------------------------------------------------------------------------
+// compile-time dispatch helpers
+// ---------------------------------------------------------------------------
+template <typename T> struct TypeTag { using type = T; };
+
+template <typename Fn>
+bool dispatch_float_type(int dt, Fn&& fn) {
+  switch (dt) {
+    case kF32: fn(TypeTag<float>{}); return true;
+    case kF16: fn(TypeTag<_Float16>{}); return true;
+    case kBF16: fn(TypeTag<__bf16>{}); return true;
+    default: return false;
+  }
+}
+
+// maxit buckets for the register-resident path (1..lane_cap(v))
+template <typename Fn>
+bool dispatch_maxit(int maxit, Fn&& fn) {
+  switch (maxit) {
+    case 1: fn(std::integral_constant<int, 1>{}); return true;
+    case 2: fn(std::integral_constant<int, 2>{}); return true;
+    case 4: fn(std::integral_constant<int, 4>{}); return true;
+    case 8: fn(std::integral_constant<int, 8>{}); return true;
+    case 16: fn(std::integral_constant<int, 16>{}); return true;
+    case 32: fn(std::integral_constant<int, 32>{}); return true;
+    default: return false;
+  }
+}
+
+inline int64_t grid_for(int64_t rows, const Geometry& g) {
+  const int64_t rpb = g.block / g.tpr;
+  return (rows + rpb - 1) / rpb;
+}
+
+// ---------------------------------------------------------------------------
+// launchers (return hipError_t of the launch)
+// ---------------------------------------------------------------------------
+hipError_t launch_layer_norm(const void* x, const void* w, const void* b, void* y,
+                             int64_t rows, int cols, float eps, int dt, int wdt,
+                             const Geometry& g, hipStream_t s);
+hipError_t launch_rms_norm(const void* x, const void* w, void* y, int64_t rows,
+                           int cols, float eps, int dt, int wdt, const Geometry& g,
+                           hipStream_t s);
+hipError_t launch_softmax(const void* x, void* y, int64_t rows, int cols, int idt,
+                          int odt, int log_mode, const Geometry& g, hipStream_t s);
+hipError_t launch_softmax_dim(const void* x, void* y, int64_t outer, int n,
+                              int64_t inner, int idt, int odt, int log_mode,
+                              hipStream_t s);
+hipError_t launch_logsumexp(const void* x, void* y, int64_t rows, int cols, int idt,
+                            int odt, const Geometry& g, hipStream_t s);
+
+struct CeArgs {
+  const void* logits;
+  const void* labels;
+  int logits_dt;
+  int label_i64;
+  float* loss;
+  float* lse;
+  float* z_loss;
+  int64_t n_rows;
+  int n_cols;
+  int64_t ld;
+  int block_size;
+  int ncb;
+  float smoothing;
+  float logit_scale;
+  float lse_square_scale;
+  int64_t ignored_index;
+  float total_classes;
+  int64_t class_start;
+  int has_smoothing;
+  int split;
+};
+hipError_t launch_cross_entropy_fwd(const CeArgs& a, const Geometry& g, hipStream_t s);
+
+struct CeBwdArgs {
+  const float* dloss;
+  const void* logits;
+  const float* lse;
+  const void* labels;
+  void* dlogits;
+  int logits_dt;
+  int label_i64;
+  int64_t n_rows;
+  int n_cols;
+  int64_t ld_logits;
+  int64_t ld_dlogits;
+  int64_t dloss_stride;
+  float smoothing;
+  float logit_scale;
+  float lse_square_scale;
+  int64_t ignored_index;
+  float total_classes;
+  int64_t class_start;
+  int has_smoothing;
+  int vec;
+};
+hipError_t launch_cross_entropy_bwd(const CeBwdArgs& a, hipStream_t s);
+
+hipError_t launch_stream_copy(const void* src, void* dst, int64_t bytes, hipStream_t s);
+
+}  // namespace vbh

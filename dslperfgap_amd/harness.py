@@ -1,0 +1,229 @@
+"""Measurement harness for the HIP backend on one MI355X.
+
+MI355X counterparts of the reference's timing and roofline helpers:
+
+* ``profile_fn``     wall-clock median with a synchronize on both sides of every
+                     call, 10 warm-up + 100 timed calls (ViperBench/benchmark.py:26-58);
+* ``time_kernel``    per-call device-event timing, median/mean/min
+                     (experiments/_harness.py:110-139);
+* ``essential_work`` algorithmic bytes of one call -- the norm/softmax rule of
+                     experiments/exp_cliff_roofline.py:229-234 (read x + write y),
+                     plus the logsumexp and cross-entropy models the reference lacks;
+* ``PEAKS`` / ``select_peak``  an MI355X entry (vendor HBM figure) next to the
+                     measured stream-copy rate (exp_cliff_roofline.py:192-218);
+* ``Rotation``       HBM-resident copies of a workload's inputs and outputs that
+                     successive launches cycle through, so that no launch finds its
+                     data in the 256 MB Infinity Cache (MALL) or the L2;
+* ``copy_peak``      the sustained device-to-device copy rate (vbh_stream_copy).
+
+The timed launches go straight through the C ABI with preallocated buffers
+(what ``hip_impl`` calls after its checks and allocation), so host overhead per
+launch is a few microseconds and the GPU is kept busy.
+"""
+from __future__ import annotations
+
+import math
+import statistics
+import time
+from dataclasses import dataclass
+from typing import Callable
+
+import torch
+
+from . import _bridge, _lib
+from .workloads import Workload
+
+# vendor figures for context; the measured stream-copy rate is the bar
+PEAKS = {
+    "MI355X": dict(memory=8.0e12, note="AMD Instinct MI355X: 288 GB HBM3E, 8.0 TB/s (vendor)"),
+    "MI300X": dict(memory=5.3e12, note="AMD Instinct MI300X: 192 GB HBM3, 5.3 TB/s (vendor)"),
+}
+
+
+def select_peak(device_name: str):
+    """(bytes/s, note) of the vendor HBM figure for a device name, or (None, reason)."""
+    up = device_name.upper()
+    for key, tbl in PEAKS.items():
+        if key in up:
+            return tbl["memory"], tbl["note"]
+    if "GFX950" in up or "MI355" in up or "MI350" in up:
+        return PEAKS["MI355X"]["memory"], PEAKS["MI355X"]["note"]
+    return None, f"no peak-table entry for '{device_name}'"
+
+
+def essential_work(kernel: str, inputs) -> int:
+    """Algorithmic HBM bytes of one call: every input read once, every output written once."""
+    el = lambda t: t.element_size() * t.numel()  # noqa: E731
+    x = inputs[0]
+    if kernel in ("softmax", "log_softmax"):
+        return 2 * el(x)
+    if kernel == "layer_norm":
+        w, b = inputs[1], inputs[2]
+        return 2 * el(x) + el(w) + (el(b) if b is not None else 0)
+    if kernel == "rms_norm":
+        return 2 * el(x) + el(inputs[2])
+    if kernel == "logsumexp":
+        n = x.shape[-1] if x.dim() else 1
+        return el(x) + (x.numel() // max(n, 1)) * x.element_size()
+    if kernel == "cross_entropy":
+        logits, labels, bs = inputs[0], inputs[1], int(inputs[8])
+        rows, cols = logits.shape
+        return el(logits) + el(labels) + 3 * 4 * rows * math.ceil(cols / bs)
+    raise KeyError(kernel)
+
+
+def profile_fn(fn, args, warmup: int = 10, iters: int = 100) -> float:
+    """Median wall-clock ms of fn(*args), synchronizing around every call."""
+    for _ in range(warmup):
+        fn(*args)
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(iters):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        fn(*args)
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+    times.sort()
+    return times[len(times) // 2]
+
+
+def time_kernel(launch: Callable[[int], None], reps: int = 50, warmup: int = 15,
+                before: Callable[[int], None] | None = None) -> dict:
+    """Per-launch device-event timing on the current stream (ms)."""
+    for i in range(warmup):
+        if before:
+            before(i)
+        launch(i)
+    torch.cuda.synchronize()
+    times = []
+    for i in range(reps):
+        if before:
+            before(i)
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        launch(i)
+        e.record()
+        e.synchronize()
+        times.append(s.elapsed_time(e))
+    times.sort()
+    return {"median_ms": times[len(times) // 2], "mean_ms": statistics.fmean(times),
+            "min_ms": times[0], "reps": reps}
+
+
+def time_back_to_back(launch: Callable[[int], None], steps: int, warmup: int) -> dict:
+    """`steps` launches back to back, bracketed by synchronize and device events.
+
+    Returns the event time and the wall time of the whole timed region (ms)."""
+    for i in range(warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    s.record()
+    for i in range(steps):
+        launch(warmup + i)
+    e.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3
+    return {"event_ms": s.elapsed_time(e), "wall_ms": wall, "steps": steps}
+
+
+def copy_peak(device, nbytes: int = 4 << 30, reps: int = 20) -> float:
+    """Sustained device-to-device copy rate in bytes/s (read + write counted)."""
+    src = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    dst = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    src.fill_(1)
+    stream = _bridge.stream(torch.device(device))
+
+    def launch(_):
+        _lib.call("vbh_stream_copy", src.data_ptr(), dst.data_ptr(), nbytes, stream)
+
+    r = time_back_to_back(launch, reps, 3)
+    del src, dst
+    return 2.0 * nbytes * reps / (r["event_ms"] * 1e-3)
+
+
+@dataclass
+class Rotation:
+    """Device copies of a workload and a launcher that cycles through them."""
+
+    workload: Workload
+    copies: int
+    launch: Callable[[int], None]
+    outputs: list
+    inputs: list
+
+
+def _float_code(t):
+    return _bridge.FLOAT_CODES[t.dtype]
+
+
+def make_rotation(w: Workload, cpu_args: tuple, device, min_footprint: int = 2 << 30) -> Rotation:
+    """Place ceil(min_footprint / bytes_per_launch) (at least 2) copies of the
+    workload's tensors in HBM and return a launcher for copy i % copies."""
+    copies = max(2, math.ceil(min_footprint / w.bytes_per_launch))
+    dev = torch.device(device)
+    stream = _bridge.stream(dev)
+    ins, outs = [], []
+    x0 = cpu_args[0]
+    for _ in range(copies):
+        ins.append(tuple(a.to(dev) if isinstance(a, torch.Tensor) else a for a in cpu_args))
+    p = _bridge.ptr
+    if w.fn in ("layer_norm", "rms_norm", "softmax", "log_softmax"):
+        for _ in range(copies):
+            outs.append(torch.empty(x0.shape, dtype=x0.dtype, device=dev))
+    elif w.fn == "logsumexp":
+        for _ in range(copies):
+            outs.append(torch.empty(x0.shape[:-1], dtype=x0.dtype, device=dev))
+    elif w.fn == "cross_entropy_fwd":
+        for _ in range(copies):
+            outs.append(tuple(torch.empty(x0.shape, dtype=torch.float32, device=dev)
+                              for _ in range(3)))
+    rows = x0.numel() // x0.shape[-1]
+    cols = x0.shape[-1]
+    dt = _float_code(x0)
+    call = _lib.call
+
+    if w.fn == "layer_norm":
+        eps = float(cpu_args[3])
+        wdt = _float_code(cpu_args[1])
+        argv = [(p(i[0]), p(i[1]), p(i[2]), p(o)) for i, o in zip(ins, outs)]
+
+        def launch(k):
+            a = argv[k % copies]
+            call("vbh_layer_norm_fwd", a[0], a[1], a[2], a[3], rows, cols, eps, dt, wdt, stream)
+    elif w.fn == "rms_norm":
+        eps = float(cpu_args[3])
+        wdt = _float_code(cpu_args[2])
+        argv = [(p(i[0]), p(i[2]), p(o)) for i, o in zip(ins, outs)]
+
+        def launch(k):
+            a = argv[k % copies]
+            call("vbh_rms_norm_fwd", a[0], a[1], a[2], rows, cols, eps, dt, wdt, stream)
+    elif w.fn in ("softmax", "log_softmax"):
+        mode = 1 if w.fn == "log_softmax" else 0
+        argv = [(p(i[0]), p(o)) for i, o in zip(ins, outs)]
+
+        def launch(k):
+            a = argv[k % copies]
+            call("vbh_softmax_fwd", a[0], a[1], rows, cols, dt, dt, mode, stream)
+    elif w.fn == "logsumexp":
+        argv = [(p(i[0]), p(o)) for i, o in zip(ins, outs)]
+
+        def launch(k):
+            a = argv[k % copies]
+            call("vbh_logsumexp_fwd", a[0], a[1], rows, cols, dt, dt, stream)
+    elif w.fn == "cross_entropy_fwd":
+        (_, labels, sm, scale, lss, ign, total, start, bs, has_sm, split) = cpu_args
+        ldt = _bridge.LABEL_CODES[labels.dtype]
+        argv = [(p(i[0]), p(i[1]), p(o[0]), p(o[1]), p(o[2])) for i, o in zip(ins, outs)]
+
+        def launch(k):
+            a = argv[k % copies]
+            call("vbh_cross_entropy_fwd", a[0], a[1], dt, ldt, a[2], a[3], a[4], rows, cols, cols,
+                 float(sm), float(scale), float(lss), int(ign), int(total), int(start), int(bs),
+                 int(has_sm), int(split), stream)
+    else:
+        raise KeyError(w.fn)
+    return Rotation(w, copies, launch, outs, ins)

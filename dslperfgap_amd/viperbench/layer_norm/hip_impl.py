@@ -1,0 +1,54 @@
+"""ViperBench/layer_norm - HIP backend.
+
+Unified API of ViperBench/layer_norm/pytorch_impl.py:5-12:
+``layer_norm(x, weight, bias, eps=1e-5) -> Tensor`` = F.layer_norm over the
+trailing ``weight.shape`` dims, same shape and dtype as ``x``.
+
+One read of x and one write of y per call (libvbhip ``vbh_layer_norm_fwd``);
+launched on torch's current stream, no host synchronisation.
+"""
+import os
+import sys
+
+_ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))))
+if _ROOT not in sys.path:  # loadable by file path, as ViperBench's harness loads impls
+    sys.path.insert(0, _ROOT)
+
+import torch  # noqa: E402
+
+from dslperfgap_amd import _bridge, _lib  # noqa: E402
+
+
+def layer_norm(x, weight, bias, eps=1e-5):
+    """Unified API: layer_norm(x, weight, bias, eps) -> Tensor.
+
+    Like the reference golden, eps other than 1e-5 raises ValueError
+    (ViperBench/layer_norm/pytorch_impl.py:9-11).
+    """
+    if eps != 1e-5:
+        raise ValueError(f"Only eps=1e-5 is supported (got {eps}). "
+                         "The Triton kernel hardcodes eps=1e-5.")
+    dev = _bridge.require_gpu("layer_norm", x, weight, bias)
+    norm_shape = tuple(weight.shape)
+    k = len(norm_shape)
+    if tuple(x.shape[x.dim() - k:]) != norm_shape or x.dim() < k:
+        raise RuntimeError(f"layer_norm: normalized_shape {list(norm_shape)} does not match "
+                           f"the trailing dims of input {list(x.shape)}")
+    if bias is not None and tuple(bias.shape) != norm_shape:
+        raise RuntimeError(f"layer_norm: bias shape {list(bias.shape)} != {list(norm_shape)}")
+    dt = _bridge.float_code(x, "layer_norm")
+    if weight.dtype != x.dtype and weight.dtype != torch.float32:
+        raise TypeError(f"layer_norm: weight dtype {weight.dtype} must be {x.dtype} or float32")
+    if bias is not None and bias.dtype != weight.dtype:
+        raise TypeError("layer_norm: weight and bias dtypes differ")
+    wdt = _bridge.FLOAT_CODES[weight.dtype]
+    cols = _bridge.numel_prod(norm_shape)
+    x = x.contiguous()
+    w = weight.contiguous()
+    b = bias.contiguous() if bias is not None else None
+    y = torch.empty_like(x)
+    rows = x.numel() // cols if cols else 0
+    with torch.cuda.device(dev):
+        _lib.call("vbh_layer_norm_fwd", _bridge.ptr(x), _bridge.ptr(w), _bridge.ptr(b),
+                  _bridge.ptr(y), rows, cols, float(eps), dt, wdt, _bridge.stream(dev))
+    return y

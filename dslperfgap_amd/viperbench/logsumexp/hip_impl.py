@@ -1,0 +1,37 @@
+"""ViperBench/logsumexp - HIP backend.
+
+Unified API of ViperBench/logsumexp/pytorch_impl.py:3-5:
+``logsumexp(x) -> Tensor`` = torch.logsumexp(x, dim=-1): shape ``x.shape[:-1]``
+(0-d for a 1-D input), same dtype as x.
+
+One read of x per call (libvbhip ``vbh_logsumexp_fwd``).
+"""
+import os
+import sys
+
+_ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))))
+if _ROOT not in sys.path:
+    sys.path.insert(0, _ROOT)
+
+import torch  # noqa: E402
+
+from dslperfgap_amd import _bridge, _lib  # noqa: E402
+
+
+def logsumexp(x):
+    """Logsumexp reduction along the last dimension."""
+    dev = _bridge.require_gpu("logsumexp", x)
+    dt = _bridge.float_code(x, "logsumexp")
+    if x.dim() == 0:
+        x = x.reshape(1)
+        out_shape = ()
+    else:
+        out_shape = tuple(x.shape[:-1])
+    x = x.contiguous()
+    cols = x.shape[-1]
+    rows = _bridge.numel_prod(out_shape)
+    y = torch.empty(out_shape, dtype=x.dtype, device=x.device)
+    with torch.cuda.device(dev):
+        _lib.call("vbh_logsumexp_fwd", _bridge.ptr(x), _bridge.ptr(y), rows, cols, dt, dt,
+                  _bridge.stream(dev))
+    return y

@@ -1,0 +1,31 @@
+"""ViperBench/softmax - HIP backend.
+
+Unified API of ViperBench/softmax/pytorch_impl.py:4-6:
+``softmax(x) -> Tensor`` = F.softmax(x, dim=-1), any rank, same dtype.
+
+One read and one write per call (libvbhip ``vbh_softmax_fwd``, log_mode 0).
+"""
+import os
+import sys
+
+_ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))))
+if _ROOT not in sys.path:
+    sys.path.insert(0, _ROOT)
+
+import torch  # noqa: E402
+
+from dslperfgap_amd import _bridge, _lib  # noqa: E402
+
+
+def softmax(x):
+    """Softmax along the last dimension for any shape tensor."""
+    dev = _bridge.require_gpu("softmax", x)
+    dt = _bridge.float_code(x, "softmax")
+    x = x.contiguous()
+    y = torch.empty_like(x)
+    cols = x.shape[-1] if x.dim() > 0 else 1
+    rows = x.numel() // cols if cols else 0
+    with torch.cuda.device(dev):
+        _lib.call("vbh_softmax_fwd", _bridge.ptr(x), _bridge.ptr(y), rows, cols, dt, dt, 0,
+                  _bridge.stream(dev))
+    return y

@@ -1,0 +1,146 @@
+/*
+ * vbhip.h - C ABI of libvbhip.so, the MI355X (gfx950) HIP backend for ViperBench's
+ * normalization / row-reduction family.
+ *
+ * Conventions shared by every entry point:
+ *   - All tensor pointers are caller-owned device pointers; the library never
+ *     allocates device memory and never synchronizes the host.
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the default stream).
+ *   - Return value 0 = success.  A negative value is an argument error
+ *     (VBH_E_*); a positive value is the hipError_t reported by the runtime.
+ *     In both cases vbh_last_error() returns a thread-local message.
+ *   - Tensors are row-major with unit stride along the reduced (last) axis.
+ *     `rows` is the product of all leading dimensions, `cols` the reduced length.
+ *   - Element types are selected by VBH_DTYPE_* codes.  Arithmetic is fp32.
+ *
+ * Each function below names the reference interface it stands in for
+ * (paths relative to the tingxi-li/DSLPerfGap checkout).
+ */
+#ifndef VBHIP_H
+#define VBHIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VBH_ABI_VERSION 1
+
+/* element type codes */
+#define VBH_DTYPE_F32 0
+#define VBH_DTYPE_F16 1
+#define VBH_DTYPE_BF16 2
+#define VBH_DTYPE_I32 3
+#define VBH_DTYPE_I64 4
+
+/* argument-error codes (negative) */
+#define VBH_E_INVALID (-1)   /* bad size, null pointer, bad flag            */
+#define VBH_E_DTYPE (-2)     /* unsupported dtype or dtype combination       */
+#define VBH_E_RANGE (-3)     /* size beyond what the kernels index (2^31-1)  */
+
+/* operation codes for vbh_tune_override */
+#define VBH_OP_LAYER_NORM 0
+#define VBH_OP_RMS_NORM 1
+#define VBH_OP_SOFTMAX 2
+#define VBH_OP_LOGSUMEXP 3
+#define VBH_OP_CROSS_ENTROPY 4
+
+int vbh_abi_version(void);
+const char* vbh_last_error(void);
+
+/* LayerNorm forward over the last axis: y = (x - mean) / sqrt(var + eps) * w + b,
+ * biased variance.  x, y: [rows, cols] of `dtype`; w, b: [cols] of `w_dtype`
+ * (either `dtype` or F32); b may be NULL (no bias).
+ * Replaces: ViperBench/layer_norm/pytorch_impl.py:5-12 (F.layer_norm golden),
+ *           ViperBench/layer_norm/triton_impl.py:101-137,
+ *           ViperBench/layer_norm/tilelang_impl.py:64-80. */
+int vbh_layer_norm_fwd(const void* x, const void* w, const void* b, void* y,
+                       int64_t rows, int64_t cols, float eps,
+                       int dtype, int w_dtype, void* stream);
+
+/* RMSNorm forward: y = (x / sqrt(mean(x^2) + eps)) * w, computed in fp32 and
+ * rounded to `dtype`.  x, y: [rows, cols] of `dtype`; w: [cols] of `w_dtype`.
+ * Replaces: ViperBench/rms_norm/pytorch_impl.py:3-10,
+ *           ViperBench/rms_norm/triton_impl.py:43-61,
+ *           ViperBench/rms_norm/tilelang_impl.py:53-70. */
+int vbh_rms_norm_fwd(const void* x, const void* w, void* y,
+                     int64_t rows, int64_t cols, float eps,
+                     int dtype, int w_dtype, void* stream);
+
+/* Softmax (log_mode = 0) or log-softmax (log_mode = 1) over the last axis.
+ * x: [rows, cols] of `in_dtype`; y: [rows, cols] of `out_dtype`.
+ * Supported (in, out): (F32,F32) (F16,F16) (BF16,BF16) (F16,F32) (BF16,F32).
+ * Replaces: ViperBench/softmax/pytorch_impl.py:4-6 (F.softmax, dim=-1),
+ *           ViperBench/log_softmax/pytorch_impl.py:4-8 (F.log_softmax),
+ *           ViperBench/softmax/triton_impl.py:28-47,
+ *           ViperBench/log_softmax/triton_impl.py:70-101. */
+int vbh_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols,
+                    int in_dtype, int out_dtype, int log_mode, void* stream);
+
+/* Softmax / log-softmax over the middle axis of a contiguous [outer, n, inner]
+ * tensor (the `dim` argument of log_softmax when dim is not the last axis).
+ * Replaces: the (M, N, K) stride handling of
+ *           ViperBench/log_softmax/triton_impl.py:44-67, 72-90. */
+int vbh_softmax_dim_fwd(const void* x, void* y, int64_t outer, int64_t n,
+                        int64_t inner, int in_dtype, int out_dtype,
+                        int log_mode, void* stream);
+
+/* logsumexp over the last axis: y[r] = log(sum_c exp(x[r, c])), with the
+ * max-shift of torch.logsumexp (an infinite row max shifts by 0).
+ * x: [rows, cols] of `in_dtype`; y: [rows] of `out_dtype` (F32 or in_dtype).
+ * Replaces: ViperBench/logsumexp/pytorch_impl.py:3-5 (torch.logsumexp),
+ *           ViperBench/logsumexp/triton_impl.py:48-71,
+ *           ViperBench/logsumexp/tilelang_impl.py:44-72. */
+int vbh_logsumexp_fwd(const void* x, void* y, int64_t rows, int64_t cols,
+                      int in_dtype, int out_dtype, void* stream);
+
+/* Column-blocked cross-entropy forward.  For every (row, column block cb) with
+ * cb < ceil(n_cols / block_size) it writes loss, lse and z_loss (fp32) at flat
+ * index cb * n_rows + row of the three output buffers.  Positions past
+ * n_rows * ceil(n_cols / block_size) are not written.
+ * logits: [n_rows, row_stride] of `logits_dtype` (unit column stride);
+ * labels: [n_rows] of `label_dtype` (I32 or I64).
+ * Replaces: ViperBench/cross_entropy/pytorch_impl.py:4-90,
+ *           ViperBench/cross_entropy/triton_impl.py:13-75, 123-140,
+ *           ViperBench/cross_entropy/tilelang_impl.py:213-260. */
+int vbh_cross_entropy_fwd(const void* logits, const void* labels, int logits_dtype,
+                          int label_dtype, void* loss, void* lse, void* z_loss,
+                          int64_t n_rows, int64_t n_cols, int64_t row_stride,
+                          float smoothing, float logit_scale, float lse_square_scale,
+                          int64_t ignored_index, int64_t total_classes,
+                          int64_t class_start_idx, int64_t block_size,
+                          int has_smoothing, int split, void* stream);
+
+/* Cross-entropy backward: dlogits[r, c] = dloss[r] * logit_scale *
+ * (p + 2 * lse_square_scale * lse[r] * p - target), p = exp(logit_scale * x - lse[r]).
+ * dloss is read at dloss[r * dloss_stride]; ignored rows get dlogits = 0 * (...).
+ * logits / dlogits: [n_rows, *_row_stride] of `logits_dtype`; lse: [n_rows] fp32.
+ * Replaces: ViperBench/cross_entropy/pytorch_impl.py:93-141,
+ *           ViperBench/cross_entropy/triton_impl.py:78-120, 143-158. */
+int vbh_cross_entropy_bwd(const void* dloss, const void* logits, const void* lse,
+                          const void* labels, void* dlogits, int logits_dtype,
+                          int label_dtype, int64_t n_rows, int64_t n_cols,
+                          int64_t logits_row_stride, int64_t dlogits_row_stride,
+                          int64_t dloss_stride, float smoothing, float logit_scale,
+                          float lse_square_scale, int64_t ignored_index,
+                          int64_t total_classes, int64_t class_start_idx,
+                          int has_smoothing, void* stream);
+
+/* Device-to-device stream copy of `bytes` (16-byte aligned pointers and size),
+ * the kernel whose sustained rate is the measured HBM peak.
+ * Replaces: the vendor-spec PEAKS table of experiments/exp_cliff_roofline.py:192-218
+ *           (no AMD entry there) with a measured figure. */
+int vbh_stream_copy(const void* src, void* dst, int64_t bytes, void* stream);
+
+/* Launch-geometry override for sweeps: threads per row `tpr` (power of two,
+ * 1..1024) and workgroup size `block` (64..1024, multiple of 64) for op `op`.
+ * tpr = 0 restores the built-in shape heuristic.  Process-wide setting.
+ * Replaces: the import-time config injection of ViperBench/tuning/cache.py:31-36. */
+int vbh_tune_override(int op, int tpr, int block);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VBHIP_H */

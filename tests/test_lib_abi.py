@@ -1,0 +1,96 @@
+"""C ABI surface of libvbhip.so (CPU tier: no kernel is launched).
+
+* every function declared in include/vbhip.h is exported by the library and
+  bound by dslperfgap_amd._lib with the same arity;
+* argument errors are rejected before any HIP call, with a negative status and
+  a message in vbh_last_error(), surfaced in Python as VbhError.
+"""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from dslperfgap_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "vbhip.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    decls = {}
+    for m in re.finditer(r"\b(?:int|const char\*)\s+(vbh_\w+)\s*\(([^)]*)\)\s*;", text):
+        args = [a.strip() for a in m.group(2).split(",") if a.strip() and a.strip() != "void"]
+        decls[m.group(1)] = len(args)
+    return decls
+
+
+def test_library_present():
+    assert _lib.LIB_PATH.exists(), "run `python -m dslperfgap_amd.build` first"
+
+
+def test_header_symbols_exported_and_bound():
+    decls = _declared()
+    assert len(decls) >= 10
+    lib = _lib.lib()
+    for name, arity in decls.items():
+        assert hasattr(lib, name), f"{name} declared in vbhip.h but not exported"
+        assert name in _lib.SIGNATURES, f"{name} not bound in _lib.SIGNATURES"
+        assert len(_lib.SIGNATURES[name][1]) == arity, f"{name}: arity differs from the header"
+    assert set(_lib.SIGNATURES) == set(decls)
+
+
+def test_abi_version():
+    assert _lib.lib().vbh_abi_version() == _lib.ABI_VERSION
+
+
+def _expect(code, name, *args, match=None):
+    with pytest.raises(_lib.VbhError) as ei:
+        _lib.call(name, *args)
+    assert ei.value.code == code
+    if match:
+        assert re.search(match, str(ei.value)), str(ei.value)
+
+
+def test_argument_errors_before_launch():
+    # dtype errors
+    _expect(_lib.E_DTYPE, "vbh_layer_norm_fwd", 16, 16, 16, 16, 4, 4, 1e-5, 7, 7, None,
+            match="unsupported dtype")
+    _expect(_lib.E_DTYPE, "vbh_layer_norm_fwd", 16, 16, 16, 16, 4, 4, 1e-5, _lib.BF16, _lib.F16,
+            None, match="weight dtype")
+    _expect(_lib.E_DTYPE, "vbh_softmax_fwd", 16, 16, 4, 4, _lib.F32, _lib.BF16, 0, None)
+    _expect(_lib.E_DTYPE, "vbh_cross_entropy_fwd", 16, 16, _lib.F32, _lib.F32, 16, 16, 16, 4, 4,
+            4, 0.0, 1.0, 0.0, -100, 4, 0, 4, 0, 0, None, match="int32 or int64")
+    # size / flag errors
+    _expect(_lib.E_INVALID, "vbh_rms_norm_fwd", 16, 16, 16, -1, 4, 1e-5, _lib.F32, _lib.F32,
+            None, match="negative")
+    _expect(_lib.E_INVALID, "vbh_softmax_fwd", 16, 16, 4, 4, _lib.F32, _lib.F32, 2, None,
+            match="log_mode")
+    _expect(_lib.E_INVALID, "vbh_cross_entropy_fwd", 16, 16, _lib.F32, _lib.I64, 16, 16, 16, 4,
+            4, 4, 0.0, 1.0, 0.0, -100, 4, 0, 0, 0, 0, None, match="BLOCK_SIZE")
+    _expect(_lib.E_INVALID, "vbh_cross_entropy_fwd", 16, 16, _lib.F32, _lib.I64, 16, 16, 16, 4,
+            8, 4, 0.0, 1.0, 0.0, -100, 8, 0, 8, 0, 0, None, match="row_stride")
+    _expect(_lib.E_INVALID, "vbh_layer_norm_fwd", None, 16, 16, 16, 4, 4, 1e-5, _lib.F32,
+            _lib.F32, None, match="null")
+    _expect(_lib.E_INVALID, "vbh_stream_copy", 16, 16, 15, None, match="multiple of 16")
+    _expect(_lib.E_RANGE, "vbh_softmax_fwd", 16, 16, 4, 1 << 31, _lib.F32, _lib.F32, 0, None)
+    _expect(_lib.E_INVALID, "vbh_tune_override", 0, 3, 0, match="power of two")
+    _expect(_lib.E_INVALID, "vbh_tune_override", 9, 0, 0, match="bad op")
+    assert _lib.last_error()
+
+
+def test_empty_sizes_are_noops():
+    # zero rows: nothing to launch, status 0 (no device touched)
+    _lib.call("vbh_layer_norm_fwd", None, None, None, None, 0, 128, 1e-5, _lib.F32, _lib.F32,
+              None)
+    _lib.call("vbh_softmax_fwd", None, None, 0, 7, _lib.F16, _lib.F32, 1, None)
+    _lib.call("vbh_stream_copy", None, None, 0, None)
+    _lib.call("vbh_tune_override", 2, 0, 0)
+
+
+def test_missing_library_is_loud(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "absent.so")
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(ImportError, match="no non-HIP fallback"):
+        _lib.lib()
