@@ -26,6 +26,7 @@ import platform
 import subprocess
 import sys
 import time
+from pathlib import Path
 
 import torch
 
@@ -34,6 +35,20 @@ from dslperfgap_amd.workloads import HEADLINE, WORKLOADS
 
 METRIC = "achieved HBM GB/s and % of measured MI355X peak per kernel; latency µs"
 VENDOR_PEAK_GBPS = 8000.0
+TRAFFIC_FILE = Path(__file__).resolve().parent / "profiles" / "row_kernels_all_configs_hbm_traffic.txt"
+
+
+def measured_traffic(key: str):
+    """HBM bytes per launch of workload `key` from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (scaled by the copy-kernel factors), or None."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        parts = line.split()
+        if len(parts) >= 3 and parts[0] == "TRAFFIC" and parts[1] == key:
+            fields = dict(p.split("=", 1) for p in parts[2:] if "=" in p)
+            return int(fields["bytes_per_launch"])
+    return None
 
 
 def log(msg):
@@ -88,6 +103,10 @@ def run_workload(key, steps, warmup, peak_measured, with_cpu, cpu_budget):
     cpu_args = w.make()
     rot = harness.make_rotation(w, cpu_args, "cuda:0")
     log(f"[bench] {key}: {rot.copies} HBM copies, {w.bytes_per_launch} B per launch")
+    # steady state before timing: 0.5 s of back-to-back launches (clocks, page
+    # tables), then `warmup` more launches, at least two per HBM copy
+    harness.warm_gpu(rot.launch, 0.5)
+    warmup = max(warmup, 2 * rot.copies)
     r = harness.time_back_to_back(rot.launch, steps, warmup)
     per_launch_ms = r["event_ms"] / steps
     value = w.bytes_per_launch * steps / (r["event_ms"] * 1e-3) / 1e9
@@ -116,7 +135,9 @@ def run_workload(key, steps, warmup, peak_measured, with_cpu, cpu_budget):
             "peak": vendor_peak,
             "unit": "GB/s",
             "frac": round(value / vendor_peak, 4),
-            "traffic": None,
+            "traffic": measured_traffic(key),
+            "traffic_source": f"rocprofv3 FETCH_SIZE/WRITE_SIZE, {TRAFFIC_FILE.name}",
+            "algorithmic_bytes": w.bytes_per_launch,
         },
         "measured_copy_peak_GBps": round(peak_measured / 1e9, 2),
         "frac_of_measured_peak": round(value * 1e9 / peak_measured, 4),
@@ -132,7 +153,7 @@ def run_workload(key, steps, warmup, peak_measured, with_cpu, cpu_budget):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS))
     ap.add_argument("--all", action="store_true", help="every measured workload, one line each")
@@ -141,8 +162,9 @@ def main():
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this backend is measured on one GPU only (row kernels shard rows "
-              "with no exchange; see DESIGN.md); --gpus must be 1", file=sys.stderr)
+        print("bench.py: this backend is measured on one GPU only; the row kernels would "
+              "shard rows across GPUs with no exchange, which no multi-GPU run here "
+              "measures. Use --gpus 1.", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)

@@ -52,7 +52,7 @@ SIGNATURES = {
          _i64, _i64, _i64, _i32, _vp],
     ),
     "vbh_stream_copy": (_i32, [_vp, _vp, _i64, _vp]),
-    "vbh_tune_override": (_i32, [_i32, _i32, _i32]),
+    "vbh_tune_override": (_i32, [_i32, _i32, _i32, _i32]),
 }
 
 
@@ -103,6 +103,11 @@ def call(name: str, *args) -> None:
         raise VbhError(name, rc, last_error())
 
 
-def tune_override(op: int, tpr: int = 0, block: int = 0) -> None:
-    """Force threads-per-row / workgroup size for one op (0, 0 restores the heuristic)."""
-    call("vbh_tune_override", op, tpr, block)
+# vbh_tune_override flag bits (VBH_TUNE_*)
+TUNE_PERSIST, TUNE_NO_PERSIST, TUNE_NONTEMPORAL, TUNE_TEMPORAL = 1, 2, 4, 8
+
+
+def tune_override(op: int, tpr: int = 0, block: int = 0, flags: int = 0) -> None:
+    """Force threads-per-row / workgroup size / kernel flags for one op
+    (all zero restores the built-in heuristic)."""
+    call("vbh_tune_override", op, tpr, block, flags)

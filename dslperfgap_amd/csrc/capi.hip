@@ -5,6 +5,8 @@
 #include <stdio.h>
 
 #include <atomic>
+#include <mutex>
+#include <unordered_map>
 
 #include "../../include/vbhip.h"
 #include "vbh_device.h"
@@ -52,6 +54,33 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 constexpr int kNumOps = 5;
 std::atomic<int> g_tpr[kNumOps];
 std::atomic<int> g_block[kNumOps];
+std::atomic<int> g_flags[kNumOps];
+
+// Built-in choices per op, from launch-shape sweeps on MI355X:
+//   vectors per lane before more lanes are added (pick_geometry): 2 for softmax
+//   and RMSNorm, 4 for LayerNorm (its two reductions per row favour fewer
+//   waves per row) and for the reductions that write one value per row
+//   (logsumexp, cross entropy);
+//   nontemporal row loads / stores for every op (rows are touched once);
+//   the persistent pipelined kernel for LayerNorm / RMSNorm rows that span 512
+//   or more lanes (few, wide rows: it keeps every CU streaming instead of
+//   running the grid in a handful of rounds); narrower rows run one row group
+//   per workgroup.
+constexpr int kItTarget[kNumOps] = {4, 2, 2, 4, 4};
+constexpr int kPersistMinTpr = 512;
+
+Geometry geometry_for(int op, int64_t cols, int vec) {
+  const int over = g_flags[op].load();
+  int flags = kFlagNontemporal;
+  if (over & kFlagNontemporal) flags |= kFlagNontemporal;
+  if (over & kFlagTemporal) flags &= ~kFlagNontemporal;
+  const bool norm = op == VBH_OP_LAYER_NORM || op == VBH_OP_RMS_NORM;
+  if (norm && !(over & kFlagNoPersist)) flags |= kFlagPersist;
+  Geometry g =
+      pick_geometry(cols, vec, kItTarget[op], g_tpr[op].load(), g_block[op].load(), flags);
+  if (g.persist && !(over & kFlagPersist) && g.tpr < kPersistMinTpr) g.persist = false;
+  return g;
+}
 
 constexpr int64_t kMaxCols = (int64_t(1) << 31) - 1;
 constexpr int64_t kMaxWorkItems = (int64_t(1) << 32) - 1;
@@ -72,22 +101,62 @@ int pow2ceil(int64_t n) {
 
 }  // namespace
 
-Geometry pick_geometry(int64_t cols, int vec, int tpr_override, int block_override) {
+int64_t resident_blocks(const void* kernel, int block) {
+  static std::mutex mu;
+  static std::unordered_map<uint64_t, int> per_cu;  // (kernel, block) -> blocks per CU
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cus[dev] = n;
+  }
+  const uint64_t key = reinterpret_cast<uint64_t>(kernel) ^ (static_cast<uint64_t>(block) << 52);
+  auto it = per_cu.find(key);
+  int nb;
+  if (it != per_cu.end()) {
+    nb = it->second;
+  } else {
+    nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kernel, block, 0) != hipSuccess ||
+        nb <= 0)
+      nb = 1;
+    per_cu.emplace(key, nb);
+  }
+  return static_cast<int64_t>(nb) * cus[dev];
+}
+
+Geometry pick_geometry(int64_t cols, int vec, int it_target, int tpr_override,
+                       int block_override, int flags) {
+  // Rows are held in registers at about `it_target` 16-byte vectors per lane:
+  // short rows take a power-of-two slice of one wave, longer ones as many waves
+  // as needed (any multiple of 64 lanes, up to 1024), with twice, four times...
+  // as many vectors per lane only when 16 waves are not enough.  Beyond the
+  // per-lane register budget (lane_cap) the streaming kernels take over.
   Geometry g;
   g.v = vec;
   const int64_t nvec = cols / vec;
-  const int cap = lane_cap(vec);  // vectors per lane in registers
-  int tpr;
+  const int cap = lane_cap(vec);
+  int tpr = 0;
   if (tpr_override > 0) {
     tpr = tpr_override;
-  } else if (nvec <= int64_t(kWave) * cap) {
-    // a sub-wave or one wave64 per row
-    tpr = nvec >= kWave ? kWave : pow2ceil(nvec < 1 ? 1 : nvec);
+  } else if (nvec <= int64_t(it_target) * kWave) {
+    const int64_t lanes = (nvec + it_target - 1) / it_target;
+    tpr = pow2ceil(lanes < 1 ? 1 : lanes);
   } else {
-    const int64_t need = (nvec + cap - 1) / cap;
-    tpr = need >= kMaxBlock ? kMaxBlock : pow2ceil(need);
+    for (int it = it_target; it <= cap; it *= 2) {
+      const int64_t waves = (nvec + int64_t(kWave) * it - 1) / (int64_t(kWave) * it);
+      if (waves <= kMaxWaves) {
+        tpr = static_cast<int>(waves) * kWave;
+        break;
+      }
+    }
   }
-  const int64_t it = (nvec + tpr - 1) / tpr;
+  const int64_t it = tpr > 0 ? (nvec + tpr - 1) / tpr : cap + 1;
   if (it > cap) {
     g.stream = true;
     g.tpr = kMaxBlock;
@@ -97,9 +166,12 @@ Geometry pick_geometry(int64_t cols, int vec, int tpr_override, int block_overri
   }
   g.tpr = tpr;
   g.maxit = pow2ceil(it < 1 ? 1 : it);
-  int block = block_override > 0 ? block_override : 256;
-  if (block < tpr) block = tpr;
+  int block;
+  if (block_override > 0) block = block_override < tpr ? tpr : block_override;
+  else block = tpr < 128 ? 256 : tpr;
   g.block = block;
+  g.persist = (flags & kFlagPersist) != 0 && g.maxit <= kPipeMaxIt;
+  g.nt = (flags & kFlagNontemporal) != 0;
   return g;
 }
 
@@ -113,19 +185,25 @@ int vbh_abi_version(void) { return VBH_ABI_VERSION; }
 
 const char* vbh_last_error(void) { return g_err; }
 
-int vbh_tune_override(int op, int tpr, int block) {
+int vbh_tune_override(int op, int tpr, int block, int flags) {
   if (op < 0 || op >= kNumOps) return fail(VBH_E_INVALID, "tune_override: bad op %d", op);
-  if (tpr != 0 && (tpr < 1 || tpr > kMaxBlock || (tpr & (tpr - 1)) != 0))
-    return fail(VBH_E_INVALID, "tune_override: tpr %d is not a power of two in [1, 1024]",
+  if (tpr != 0 && (tpr < 1 || tpr > kMaxBlock ||
+                   (tpr <= kWave ? (tpr & (tpr - 1)) != 0 : tpr % kWave != 0)))
+    return fail(VBH_E_INVALID,
+                "tune_override: tpr %d is neither a power of two <= 64 nor a multiple of 64 "
+                "<= 1024",
                 tpr);
   if (block != 0 && (block < kWave || block > kMaxBlock || block % kWave != 0))
     return fail(VBH_E_INVALID, "tune_override: block %d is not a multiple of 64 in [64, 1024]",
                 block);
-  if (tpr != 0 && block != 0 && (block % tpr != 0 && tpr <= block))
+  if (tpr != 0 && block != 0 && block % tpr != 0)
     return fail(VBH_E_INVALID, "tune_override: block %d is not a multiple of tpr %d", block,
                 tpr);
+  if (flags < 0 || flags > 15)
+    return fail(VBH_E_INVALID, "tune_override: unknown flag bits 0x%x", flags);
   g_tpr[op].store(tpr);
   g_block[op].store(block);
+  g_flags[op].store(flags);
   g_err[0] = '\0';
   return 0;
 }
@@ -144,8 +222,7 @@ int vbh_layer_norm_fwd(const void* x, const void* w, const void* b, void* y, int
   const int vn = 16 / elt_size(dtype);
   const bool vec_ok = cols % vn == 0 && aligned16(x) && aligned16(y) && aligned16(w) &&
                       (b == nullptr || aligned16(b));
-  const Geometry g = pick_geometry(cols, vec_ok ? vn : 1, g_tpr[VBH_OP_LAYER_NORM].load(),
-                                   g_block[VBH_OP_LAYER_NORM].load());
+  const Geometry g = geometry_for(VBH_OP_LAYER_NORM, cols, vec_ok ? vn : 1);
   if (int rc = check_grid(rows, g)) return rc;
   return hip_status(launch_layer_norm(x, w, b, y, rows, static_cast<int>(cols), eps, dtype,
                                       w_dtype, g, static_cast<hipStream_t>(stream)),
@@ -165,8 +242,7 @@ int vbh_rms_norm_fwd(const void* x, const void* w, void* y, int64_t rows, int64_
   if (!x || !w || !y) return fail(VBH_E_INVALID, "rms_norm: null pointer");
   const int vn = 16 / elt_size(dtype);
   const bool vec_ok = cols % vn == 0 && aligned16(x) && aligned16(y) && aligned16(w);
-  const Geometry g = pick_geometry(cols, vec_ok ? vn : 1, g_tpr[VBH_OP_RMS_NORM].load(),
-                                   g_block[VBH_OP_RMS_NORM].load());
+  const Geometry g = geometry_for(VBH_OP_RMS_NORM, cols, vec_ok ? vn : 1);
   if (int rc = check_grid(rows, g)) return rc;
   return hip_status(launch_rms_norm(x, w, y, rows, static_cast<int>(cols), eps, dtype,
                                     w_dtype, g, static_cast<hipStream_t>(stream)),
@@ -192,8 +268,7 @@ int vbh_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols, int in_d
   if (!x || !y) return fail(VBH_E_INVALID, "softmax: null pointer");
   const int vn = 16 / elt_size(in_dtype);
   const bool vec_ok = cols % vn == 0 && aligned16(x) && aligned16(y);
-  const Geometry g = pick_geometry(cols, vec_ok ? vn : 1, g_tpr[VBH_OP_SOFTMAX].load(),
-                                   g_block[VBH_OP_SOFTMAX].load());
+  const Geometry g = geometry_for(VBH_OP_SOFTMAX, cols, vec_ok ? vn : 1);
   if (int rc = check_grid(rows, g)) return rc;
   return hip_status(launch_softmax(x, y, rows, static_cast<int>(cols), in_dtype, out_dtype,
                                    log_mode, g, static_cast<hipStream_t>(stream)),
@@ -231,8 +306,7 @@ int vbh_logsumexp_fwd(const void* x, void* y, int64_t rows, int64_t cols, int in
   if ((!x && cols > 0) || !y) return fail(VBH_E_INVALID, "logsumexp: null pointer");
   const int vn = 16 / elt_size(in_dtype);
   const bool vec_ok = cols % vn == 0 && aligned16(x);
-  const Geometry g = pick_geometry(cols, vec_ok ? vn : 1, g_tpr[VBH_OP_LOGSUMEXP].load(),
-                                   g_block[VBH_OP_LOGSUMEXP].load());
+  const Geometry g = geometry_for(VBH_OP_LOGSUMEXP, cols, vec_ok ? vn : 1);
   if (int rc = check_grid(rows, g)) return rc;
   return hip_status(launch_logsumexp(x, y, rows, static_cast<int>(cols), in_dtype, out_dtype,
                                      g, static_cast<hipStream_t>(stream)),
@@ -262,8 +336,7 @@ int vbh_cross_entropy_fwd(const void* logits, const void* labels, int logits_dty
   const int vn = 16 / elt_size(logits_dtype);
   const bool vec_ok =
       n_cols % vn == 0 && bs % vn == 0 && row_stride % vn == 0 && aligned16(logits);
-  const Geometry g = pick_geometry(bs, vec_ok ? vn : 1, g_tpr[VBH_OP_CROSS_ENTROPY].load(),
-                                   g_block[VBH_OP_CROSS_ENTROPY].load());
+  const Geometry g = geometry_for(VBH_OP_CROSS_ENTROPY, bs, vec_ok ? vn : 1);
   if (int rc = check_grid(n_rows * ncb, g)) return rc;
   CeArgs a;
   a.logits = logits;
@@ -342,6 +415,7 @@ int vbh_stream_copy(const void* src, void* dst, int64_t bytes, void* stream) {
   if (bytes < 0 || bytes % 16 != 0)
     return fail(VBH_E_INVALID, "stream_copy: bytes must be a non-negative multiple of 16");
   if (bytes == 0) return 0;
+  if (bytes / 16 > kMaxWorkItems) return fail(VBH_E_RANGE, "stream_copy: more than 64 GiB");
   if (!src || !dst || !aligned16(src) || !aligned16(dst))
     return fail(VBH_E_INVALID, "stream_copy: pointers must be non-null and 16-byte aligned");
   return hip_status(launch_stream_copy(src, dst, bytes, static_cast<hipStream_t>(stream)),

@@ -2,7 +2,7 @@
 //
 // Forward: a "segment" is one (row, column block) pair, i.e. up to block_size
 // consecutive logits of one row.  `tpr` lanes own one segment, load it once
-// into fp32 registers (scaled by logit_scale; padding lanes hold -inf),
+// into registers in the storage type (scaled by logit_scale where used),
 // all-reduce max, sum of exp(x - max) and, with smoothing, the plain sum of the
 // logits, and one lane writes loss / lse / z_loss at flat index
 // cb * n_rows + row.  The label logit is fetched by that lane at kernel start,
@@ -89,13 +89,14 @@ __device__ __forceinline__ void ce_store(float lse, float sum_logits, bool in_bl
   z_out[idx] = z;
 }
 
-template <typename T, int V, int MAXIT>
+template <typename T, int V, int IT, bool NT>
 __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
     const T* __restrict__ logits, const void* __restrict__ labels, int label_i64,
     float* __restrict__ loss, float* __restrict__ lse_out, float* __restrict__ z_out,
     int64_t n_rows, int n_cols, int64_t ld, int bs, int ncb, int tpr, CeScalars c) {
+  typedef typename Raw<T, V>::type RT;
   __shared__ float lds[3][kMaxWaves];
-  const int g = threadIdx.x & (tpr - 1);
+  const int g = threadIdx.x % tpr;
   const int64_t nseg = n_rows * ncb;
   int64_t seg = static_cast<int64_t>(blockIdx.x) * (blockDim.x / tpr) + threadIdx.x / tpr;
   const bool live = seg < nseg;
@@ -118,42 +119,41 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
     if (!ignored && in_block) logit_label = static_cast<float>(lr[adj]) * c.logit_scale;
   }
 
-  float v[MAXIT][V];
+  RT xr[IT];
 #pragma unroll
-  for (int i = 0; i < MAXIT; ++i) {
+  for (int i = 0; i < IT; ++i) {
     const int j = i * tpr + g;
-    if (j < nvec) {
-      load_f32<T, V>(lr + col0 + static_cast<int64_t>(j) * V, v[i]);
-#pragma unroll
-      for (int k = 0; k < V; ++k) v[i][k] *= c.logit_scale;
-    } else {
-#pragma unroll
-      for (int k = 0; k < V; ++k) v[i][k] = kNegInf;
-    }
+    if (j < nvec) xr[i] = load_raw<T, V, NT>(lr + col0 + static_cast<int64_t>(j) * V);
+    else xr[i] = RT{};
   }
+  const float scale = c.logit_scale;
 
   float mx[V];
 #pragma unroll
-  for (int k = 0; k < V; ++k) mx[k] = v[0][k];
+  for (int k = 0; k < V; ++k) mx[k] = kNegInf;
 #pragma unroll
-  for (int i = 1; i < MAXIT; ++i)
+  for (int i = 0; i < IT; ++i)
+    if (i * tpr + g < nvec)
 #pragma unroll
-    for (int k = 0; k < V; ++k) mx[k] = fmaxf(mx[k], v[i][k]);
+      for (int k = 0; k < V; ++k) mx[k] = fmaxf(mx[k], raw_at<T, V>(xr[i], k) * scale);
   float lm = mx[0];
 #pragma unroll
   for (int k = 1; k < V; ++k) lm = fmaxf(lm, mx[k]);
   const float m = group_allreduce<Max>(lm, tpr, lds[0]);
+  reload_barrier<T, V, IT>(xr);
 
   float se[V], sl[V];
 #pragma unroll
   for (int k = 0; k < V; ++k) se[k] = sl[k] = 0.f;
 #pragma unroll
-  for (int i = 0; i < MAXIT; ++i) {
+  for (int i = 0; i < IT; ++i) {
+    if (i * tpr + g < nvec) {
 #pragma unroll
-    for (int k = 0; k < V; ++k) se[k] += fast_exp(v[i][k] - m);
-    if (c.has_smoothing && i * tpr + g < nvec) {
-#pragma unroll
-      for (int k = 0; k < V; ++k) sl[k] += v[i][k];
+      for (int k = 0; k < V; ++k) {
+        const float v = raw_at<T, V>(xr[i], k) * scale;
+        se[k] += fast_exp(v - m);
+        sl[k] += v;
+      }
     }
   }
 #pragma unroll
@@ -296,11 +296,15 @@ hipError_t launch_cross_entropy_fwd(const CeArgs& a, const Geometry& g, hipStrea
       dispatch_maxit(g.maxit, [&](auto mc) {
         constexpr int M = decltype(mc)::value;
         if constexpr (M <= lane_cap(V)) {
-          hipLaunchKernelGGL((ce_fwd_rows<T, V, M>), dim3(grid_for(nseg, g)), dim3(g.block),
-                             0, s, static_cast<const T*>(a.logits), a.labels, a.label_i64,
-                             a.loss, a.lse, a.z_loss, a.n_rows, a.n_cols, a.ld,
-                             a.block_size, a.ncb, g.tpr, c);
-          err = hipGetLastError();
+          auto launch = [&](auto kern) {
+            hipLaunchKernelGGL(kern, dim3(grid_for(nseg, g)), dim3(g.block), 0, s,
+                               static_cast<const T*>(a.logits), a.labels, a.label_i64, a.loss,
+                               a.lse, a.z_loss, a.n_rows, a.n_cols, a.ld, a.block_size, a.ncb,
+                               g.tpr, c);
+            err = hipGetLastError();
+          };
+          if (g.nt) launch(ce_fwd_rows<T, V, M, true>);
+          else launch(ce_fwd_rows<T, V, M, false>);
         }
       });
     };

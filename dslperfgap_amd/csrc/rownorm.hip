@@ -1,18 +1,30 @@
 // LayerNorm and RMSNorm forward for gfx950.
 //
-// Register-resident path (rows of up to 64 * tpr values per lane group):
-//   `tpr` lanes own one row; each lane loads its share of the row with 16-byte
-//   loads into fp32 registers exactly once, the row statistics are all-reduced
-//   across the group (DPP / permlane inside a wave, LDS across waves), and the
-//   normalized row is written once in the input dtype.
-// Streaming path (wider rows): one 1024-thread workgroup per row, a statistics
-//   pass (Welford/Chan moments for LayerNorm) and an output pass that reads the
-//   row again.
+// Register-resident path: `tpr` lanes own one row (a power of two up to 64, or
+// any multiple of 64 up to 1024).  Each lane loads its share of the row once,
+// with 16-byte loads, into registers that keep the storage type (two bf16/fp16
+// values per VGPR), widens to fp32 where a value is used, and the row
+// statistics are all-reduced across the group (DPP / permlane inside a wave, an
+// LDS exchange across waves).  The normalized row is
+// written once in the input dtype.
+//   LayerNorm statistics are the exact two-pass ones over the register-resident
+//   row: the row sum gives the mean, then the sum of squared deviations from it
+//   gives the biased variance (two all-reduces of plain sums).
+//   Weight / bias slices are loaded together with the row when the registers
+//   allow, so a row costs one memory round trip.
+// Persistent pipelined path (vbh_tune_override / heuristic): the grid holds as
+//   many workgroups as are resident at once; each row group loops over rows,
+//   keeps its weight / bias slice in registers for the whole kernel, and loads
+//   its next row before reducing the current one.
+// Streaming path (rows wider than the register budget): one 1024-lane
+//   workgroup per row; a Welford/Chan statistics pass, then an output pass that
+//   reads the row again.
 //
-// Semantics follow ViperBench/layer_norm/pytorch_impl.py:5-12 (F.layer_norm,
-// biased variance, y = (x - mean) * rstd * w + b) and
-// ViperBench/rms_norm/pytorch_impl.py:8-10 (rms = sqrt(mean(x^2) + eps),
-// y = (x / rms) * w, rounded to x's dtype).
+// Semantics: ViperBench/layer_norm/pytorch_impl.py:5-12 (F.layer_norm, biased
+// variance, y = (x - mean) * rstd * w + b) and ViperBench/rms_norm/pytorch_impl.py:8-10
+// (rms = sqrt(mean(x^2) + eps), y = (x / rms) * w, rounded to x's dtype).
+#include <algorithm>
+
 #include "vbh_device.h"
 #include "vbh_launch.h"
 
@@ -20,18 +32,14 @@ namespace vbh {
 
 namespace {
 
-template <typename T, int V, int MAXIT>
-__device__ __forceinline__ void load_row(const T* __restrict__ xr, int nvec, int g, int tpr,
-                                         float (&v)[MAXIT][V]) {
+template <typename T, int V, int IT, bool NT>
+__device__ __forceinline__ void load_raw_row(const T* __restrict__ xr, int nvec, int g, int tpr,
+                                             typename Raw<T, V>::type (&dst)[IT]) {
 #pragma unroll
-  for (int i = 0; i < MAXIT; ++i) {
+  for (int i = 0; i < IT; ++i) {
     const int j = i * tpr + g;
-    if (j < nvec) {
-      load_f32<T, V>(xr + static_cast<int64_t>(j) * V, v[i]);
-    } else {
-#pragma unroll
-      for (int k = 0; k < V; ++k) v[i][k] = 0.f;
-    }
+    if (j < nvec) dst[i] = load_raw<T, V, NT>(xr + static_cast<int64_t>(j) * V);
+    else dst[i] = typename Raw<T, V>::type{};
   }
 }
 
@@ -47,114 +55,290 @@ __device__ __forceinline__ float tree_sum(const float (&a)[V]) {
   return t[0];
 }
 
-// ---------------------------------------------------------------------------
-// register-resident kernels
-// ---------------------------------------------------------------------------
-
-template <typename T, typename TW, int V, int MAXIT>
-__global__ __launch_bounds__(kMaxBlock) void layer_norm_rows(
-    const T* __restrict__ x, const TW* __restrict__ w, const TW* __restrict__ b,
-    T* __restrict__ y, int64_t rows, int cols, int tpr, float eps) {
-  __shared__ float lds[2][kMaxWaves];
-  const int nvec = cols / V;
-  const int g = threadIdx.x & (tpr - 1);
-  int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / tpr) + threadIdx.x / tpr;
-  const bool live = row < rows;
-  if (!live) row = rows - 1;
-  const T* xr = x + row * cols;
-
-  float v[MAXIT][V];
-  load_row<T, V, MAXIT>(xr, nvec, g, tpr, v);
-
-  // exact two-pass moments over the register-resident row
+// Sum of the lane's values (padding vectors are zero).
+template <typename T, int V, int IT>
+__device__ __forceinline__ float lane_sum(const typename Raw<T, V>::type (&xr)[IT]) {
   float acc[V];
 #pragma unroll
   for (int k = 0; k < V; ++k) acc[k] = 0.f;
 #pragma unroll
-  for (int i = 0; i < MAXIT; ++i)
+  for (int i = 0; i < IT; ++i)
 #pragma unroll
-    for (int k = 0; k < V; ++k) acc[k] += v[i][k];
-  const float sum = group_allreduce<Sum>(tree_sum<V>(acc), tpr, lds[0]);
-  const float mean = sum / static_cast<float>(cols);
+    for (int k = 0; k < V; ++k) acc[k] += raw_at<T, V>(xr[i], k);
+  return tree_sum<V>(acc);
+}
 
+// Sum of squared deviations from `mean` over the lane's valid values
+// (vectors i with i * tpr + g < nvec).
+template <typename T, int V, int IT>
+__device__ __forceinline__ float lane_centered_sumsq(const typename Raw<T, V>::type (&xr)[IT],
+                                                     float mean, int nvec, int g, int tpr) {
+  float acc[V];
 #pragma unroll
   for (int k = 0; k < V; ++k) acc[k] = 0.f;
 #pragma unroll
-  for (int i = 0; i < MAXIT; ++i) {
+  for (int i = 0; i < IT; ++i) {
     if (i * tpr + g < nvec) {
 #pragma unroll
       for (int k = 0; k < V; ++k) {
-        const float d = v[i][k] - mean;
+        const float d = raw_at<T, V>(xr[i], k) - mean;
         acc[k] = fmaf(d, d, acc[k]);
       }
     }
   }
-  const float m2 = group_allreduce<Sum>(tree_sum<V>(acc), tpr, lds[1]);
-  const float rstd = 1.0f / sqrtf(m2 / static_cast<float>(cols) + eps);
-  if (!live) return;
-
-  T* yr = y + row * cols;
-#pragma unroll
-  for (int i = 0; i < MAXIT; ++i) {
-    const int j = i * tpr + g;
-    if (j < nvec) {
-      float wv[V], bv[V], o[V];
-      load_f32<TW, V>(w + static_cast<int64_t>(j) * V, wv);
-      if (b != nullptr) {
-        load_f32<TW, V>(b + static_cast<int64_t>(j) * V, bv);
-      } else {
-#pragma unroll
-        for (int k = 0; k < V; ++k) bv[k] = 0.f;
-      }
-#pragma unroll
-      for (int k = 0; k < V; ++k) o[k] = (v[i][k] - mean) * rstd * wv[k] + bv[k];
-      store_from_f32<T, V>(yr + static_cast<int64_t>(j) * V, o);
-    }
-  }
+  return tree_sum<V>(acc);
 }
 
-template <typename T, typename TW, int V, int MAXIT>
-__global__ __launch_bounds__(kMaxBlock) void rms_norm_rows(
-    const T* __restrict__ x, const TW* __restrict__ w, T* __restrict__ y, int64_t rows,
-    int cols, int tpr, float eps) {
-  __shared__ float lds[kMaxWaves];
-  const int nvec = cols / V;
-  const int g = threadIdx.x & (tpr - 1);
-  int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / tpr) + threadIdx.x / tpr;
-  const bool live = row < rows;
-  if (!live) row = rows - 1;
-  const T* xr = x + row * cols;
-
-  float v[MAXIT][V];
-  load_row<T, V, MAXIT>(xr, nvec, g, tpr, v);
-
+template <typename T, int V, int IT>
+__device__ __forceinline__ float lane_sumsq(const typename Raw<T, V>::type (&xr)[IT]) {
   float acc[V];
 #pragma unroll
   for (int k = 0; k < V; ++k) acc[k] = 0.f;
 #pragma unroll
-  for (int i = 0; i < MAXIT; ++i)
+  for (int i = 0; i < IT; ++i)
 #pragma unroll
-    for (int k = 0; k < V; ++k) acc[k] = fmaf(v[i][k], v[i][k], acc[k]);
-  const float ss = group_allreduce<Sum>(tree_sum<V>(acc), tpr, lds);
-  const float rinv = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+    for (int k = 0; k < V; ++k) {
+      const float v = raw_at<T, V>(xr[i], k);  // padding vectors are zero
+      acc[k] = fmaf(v, v, acc[k]);
+    }
+  return tree_sum<V>(acc);
+}
+
+// Weight / bias slices ride along with the row when they take at most 32
+// VGPRs in raw storage; otherwise they are read after the reduction.
+template <typename TW, int V, int IT> constexpr bool kEarlyLN = 2 * raw_vgprs<TW>(V, IT) <= 32;
+template <typename TW, int V, int IT> constexpr bool kEarlyRMS = raw_vgprs<TW>(V, IT) <= 32;
+
+// Deepest row slice (vectors per lane) of the persistent kernels: current and
+// next row plus the per-column vectors must stay within about 64 VGPRs of raw
+// storage.
+template <typename T, typename TW, int V, int NVEC_COL>
+constexpr int pipe_cap() {
+  int it = kPipeMaxIt;
+  while (it > 1 && 2 * raw_vgprs<T>(V, it) + NVEC_COL * raw_vgprs<TW>(V, it) > 64)
+    it /= 2;
+  return it;
+}
+
+// ---------------------------------------------------------------------------
+// register-resident kernels: one row group per row
+// ---------------------------------------------------------------------------
+
+template <typename T, typename TW, int V, int IT, bool NT>
+__global__ __launch_bounds__(kMaxBlock) void layer_norm_rows(
+    const T* __restrict__ x, const TW* __restrict__ w, const TW* __restrict__ b,
+    T* __restrict__ y, int64_t rows, int cols, int tpr, float eps) {
+  typedef typename Raw<T, V>::type RT;
+  typedef typename Raw<TW, V>::type RW;
+  __shared__ float lds[2][kMaxWaves];
+  const int nvec = cols / V;
+  const int g = threadIdx.x % tpr;
+  int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / tpr) + threadIdx.x / tpr;
+  const bool live = row < rows;
+  if (!live) row = rows - 1;
+
+  RT xr[IT];
+  load_raw_row<T, V, IT, NT>(x + row * cols, nvec, g, tpr, xr);
+  constexpr bool kEarly = kEarlyLN<TW, V, IT>;
+  RW wr[kEarly ? IT : 1], br[kEarly ? IT : 1];
+  if constexpr (kEarly) {
+    load_raw_row<TW, V, IT, false>(w, nvec, g, tpr, wr);
+    if (b != nullptr) load_raw_row<TW, V, IT, false>(b, nvec, g, tpr, br);
+  }
+
+  const float mean =
+      group_allreduce<Sum>(lane_sum<T, V, IT>(xr), tpr, lds[0]) / static_cast<float>(cols);
+  reload_barrier<T, V, IT>(xr);
+  const float m2 = group_allreduce<Sum>(lane_centered_sumsq<T, V, IT>(xr, mean, nvec, g, tpr),
+                                        tpr, lds[1]);
+  const float rstd = 1.0f / sqrtf(m2 / static_cast<float>(cols) + eps);
   if (!live) return;
+  reload_barrier<T, V, IT>(xr);
 
   T* yr = y + row * cols;
 #pragma unroll
-  for (int i = 0; i < MAXIT; ++i) {
+  for (int i = 0; i < IT; ++i) {
     const int j = i * tpr + g;
     if (j < nvec) {
-      float wv[V], o[V];
-      load_f32<TW, V>(w + static_cast<int64_t>(j) * V, wv);
+      RW wv, bv{};
+      if constexpr (kEarly) {
+        wv = wr[i];
+        if (b != nullptr) bv = br[i];
+      } else {
+        wv = load_raw<TW, V, false>(w + static_cast<int64_t>(j) * V);
+        if (b != nullptr) bv = load_raw<TW, V, false>(b + static_cast<int64_t>(j) * V);
+      }
+      float o[V];
 #pragma unroll
-      for (int k = 0; k < V; ++k) o[k] = (v[i][k] * rinv) * wv[k];
-      store_from_f32<T, V>(yr + static_cast<int64_t>(j) * V, o);
+      for (int k = 0; k < V; ++k)
+        o[k] = (raw_at<T, V>(xr[i], k) - mean) * rstd * raw_at<TW, V>(wv, k) +
+               raw_at<TW, V>(bv, k);
+      store_raw<T, V, NT>(yr + static_cast<int64_t>(j) * V, o);
+    }
+  }
+}
+
+template <typename T, typename TW, int V, int IT, bool NT>
+__global__ __launch_bounds__(kMaxBlock) void rms_norm_rows(
+    const T* __restrict__ x, const TW* __restrict__ w, T* __restrict__ y, int64_t rows,
+    int cols, int tpr, float eps) {
+  typedef typename Raw<T, V>::type RT;
+  typedef typename Raw<TW, V>::type RW;
+  __shared__ float lds[kMaxWaves];
+  const int nvec = cols / V;
+  const int g = threadIdx.x % tpr;
+  int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / tpr) + threadIdx.x / tpr;
+  const bool live = row < rows;
+  if (!live) row = rows - 1;
+
+  RT xr[IT];
+  load_raw_row<T, V, IT, NT>(x + row * cols, nvec, g, tpr, xr);
+  constexpr bool kEarly = kEarlyRMS<TW, V, IT>;
+  RW wr[kEarly ? IT : 1];
+  if constexpr (kEarly) load_raw_row<TW, V, IT, false>(w, nvec, g, tpr, wr);
+
+  const float ss = group_allreduce<Sum>(lane_sumsq<T, V, IT>(xr), tpr, lds);
+  const float rinv = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+  if (!live) return;
+  reload_barrier<T, V, IT>(xr);
+
+  T* yr = y + row * cols;
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    const int j = i * tpr + g;
+    if (j < nvec) {
+      RW wv;
+      if constexpr (kEarly) wv = wr[i];
+      else wv = load_raw<TW, V, false>(w + static_cast<int64_t>(j) * V);
+      float o[V];
+#pragma unroll
+      for (int k = 0; k < V; ++k) o[k] = (raw_at<T, V>(xr[i], k) * rinv) * raw_at<TW, V>(wv, k);
+      store_raw<T, V, NT>(yr + static_cast<int64_t>(j) * V, o);
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// streaming kernels (one 1024-thread workgroup per row, chunked two passes)
+// persistent pipelined kernels
+//
+// Row group `grp` of workgroup `blk` handles rows blk*rpb + grp, then
+// + gridDim.x*rpb, ...  The row loop is uniform across the workgroup (groups
+// past the last row still take part in the barriers), and the LDS reduction
+// buffers alternate between two parities, which makes one barrier per
+// reduction sufficient: a thread can only overwrite a parity after passing the
+// next iteration's barrier, which every thread reaches only after reading it.
+// ---------------------------------------------------------------------------
+
+template <typename T, typename TW, int V, int IT, bool NT>
+__global__ __launch_bounds__(kMaxBlock) void layer_norm_pipe(
+    const T* __restrict__ x, const TW* __restrict__ w, const TW* __restrict__ b,
+    T* __restrict__ y, int64_t rows, int cols, int tpr, float eps) {
+  typedef typename Raw<T, V>::type RT;
+  typedef typename Raw<TW, V>::type RW;
+  __shared__ float lds[2][2][kMaxWaves];
+  const int nvec = cols / V;
+  const int g = threadIdx.x % tpr;
+  const int rpb = blockDim.x / tpr;
+  const int grp = threadIdx.x / tpr;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * rpb;
+
+  RW wr[IT], br[IT];
+  load_raw_row<TW, V, IT, false>(w, nvec, g, tpr, wr);
+  if (b != nullptr) load_raw_row<TW, V, IT, false>(b, nvec, g, tpr, br);
+  else
+#pragma unroll
+    for (int i = 0; i < IT; ++i) br[i] = RW{};
+
+  RT cur[IT], nxt[IT];
+  int64_t base = static_cast<int64_t>(blockIdx.x) * rpb;
+  if (base + grp < rows) load_raw_row<T, V, IT, NT>(x + (base + grp) * cols, nvec, g, tpr, cur);
+  else load_raw_row<T, V, IT, NT>(x, 0, g, tpr, cur);  // zero fill
+  int par = 0;
+  for (; base < rows; base += stride) {
+    const int64_t row = base + grp;
+    const int64_t next = row + stride;
+    if (next < rows) load_raw_row<T, V, IT, NT>(x + next * cols, nvec, g, tpr, nxt);
+    else load_raw_row<T, V, IT, NT>(x, 0, g, tpr, nxt);
+
+    const float mean = group_allreduce<Sum>(lane_sum<T, V, IT>(cur), tpr, lds[par][0]) /
+                       static_cast<float>(cols);
+    reload_barrier<T, V, IT>(cur);
+    const float m2 = group_allreduce<Sum>(
+        lane_centered_sumsq<T, V, IT>(cur, mean, nvec, g, tpr), tpr, lds[par][1]);
+    const float rstd = 1.0f / sqrtf(m2 / static_cast<float>(cols) + eps);
+    reload_barrier<T, V, IT>(cur);
+    if (row < rows) {
+      T* yr = y + row * cols;
+#pragma unroll
+      for (int i = 0; i < IT; ++i) {
+        const int j = i * tpr + g;
+        if (j < nvec) {
+          float o[V];
+#pragma unroll
+          for (int k = 0; k < V; ++k)
+            o[k] = (raw_at<T, V>(cur[i], k) - mean) * rstd * raw_at<TW, V>(wr[i], k) +
+                   raw_at<TW, V>(br[i], k);
+          store_raw<T, V, NT>(yr + static_cast<int64_t>(j) * V, o);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < IT; ++i) cur[i] = nxt[i];
+    par ^= 1;
+  }
+}
+
+template <typename T, typename TW, int V, int IT, bool NT>
+__global__ __launch_bounds__(kMaxBlock) void rms_norm_pipe(
+    const T* __restrict__ x, const TW* __restrict__ w, T* __restrict__ y, int64_t rows,
+    int cols, int tpr, float eps) {
+  typedef typename Raw<T, V>::type RT;
+  typedef typename Raw<TW, V>::type RW;
+  __shared__ float lds[2][kMaxWaves];
+  const int nvec = cols / V;
+  const int g = threadIdx.x % tpr;
+  const int rpb = blockDim.x / tpr;
+  const int grp = threadIdx.x / tpr;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * rpb;
+
+  RW wr[IT];
+  load_raw_row<TW, V, IT, false>(w, nvec, g, tpr, wr);
+  RT cur[IT], nxt[IT];
+  int64_t base = static_cast<int64_t>(blockIdx.x) * rpb;
+  if (base + grp < rows) load_raw_row<T, V, IT, NT>(x + (base + grp) * cols, nvec, g, tpr, cur);
+  else load_raw_row<T, V, IT, NT>(x, 0, g, tpr, cur);
+  int par = 0;
+  for (; base < rows; base += stride) {
+    const int64_t row = base + grp;
+    const int64_t next = row + stride;
+    if (next < rows) load_raw_row<T, V, IT, NT>(x + next * cols, nvec, g, tpr, nxt);
+    else load_raw_row<T, V, IT, NT>(x, 0, g, tpr, nxt);
+
+    const float ss = group_allreduce<Sum>(lane_sumsq<T, V, IT>(cur), tpr, lds[par]);
+    const float rinv = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+    reload_barrier<T, V, IT>(cur);
+    if (row < rows) {
+      T* yr = y + row * cols;
+#pragma unroll
+      for (int i = 0; i < IT; ++i) {
+        const int j = i * tpr + g;
+        if (j < nvec) {
+          float o[V];
+#pragma unroll
+          for (int k = 0; k < V; ++k)
+            o[k] = (raw_at<T, V>(cur[i], k) * rinv) * raw_at<TW, V>(wr[i], k);
+          store_raw<T, V, NT>(yr + static_cast<int64_t>(j) * V, o);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < IT; ++i) cur[i] = nxt[i];
+    par ^= 1;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// streaming kernels (one 1024-lane workgroup per row, chunked two passes)
 // ---------------------------------------------------------------------------
 
 template <typename T, typename TW, int V>
@@ -242,6 +426,20 @@ bool dispatch_weight_type(int dt, int wdt, Fn&& fn) {
   return false;
 }
 
+// Launch the register-resident kernel (one row group per row) or the
+// persistent one (grid capped at the resident capacity) through `launch`.
+template <class RowsK, class PipeK, class Launch>
+hipError_t launch_rows_or_pipe(RowsK rows_k, PipeK pipe_k, bool persist, int64_t rows,
+                               const Geometry& g, Launch&& launch) {
+  if (persist) {
+    const int64_t cap = resident_blocks(reinterpret_cast<const void*>(pipe_k), g.block);
+    launch(pipe_k, std::min<int64_t>(grid_for(rows, g), std::max<int64_t>(cap, 1)));
+  } else {
+    launch(rows_k, grid_for(rows, g));
+  }
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_layer_norm(const void* x, const void* w, const void* b, void* y,
@@ -265,11 +463,21 @@ hipError_t launch_layer_norm(const void* x, const void* w, const void* b, void* 
         dispatch_maxit(g.maxit, [&](auto mc) {
           constexpr int M = decltype(mc)::value;
           if constexpr (M <= lane_cap(V)) {
-            hipLaunchKernelGGL((layer_norm_rows<T, TW, V, M>), dim3(grid_for(rows, g)),
-                               dim3(g.block), 0, s, static_cast<const T*>(x),
-                               static_cast<const TW*>(w), static_cast<const TW*>(b),
-                               static_cast<T*>(y), rows, cols, g.tpr, eps);
-            err = hipGetLastError();
+            auto body = [&](auto nt) {
+              constexpr bool NT = decltype(nt)::value;
+              constexpr int PC = pipe_cap<T, TW, V, 2>();
+              constexpr int MP = M <= PC ? M : PC;
+              err = launch_rows_or_pipe(
+                  layer_norm_rows<T, TW, V, M, NT>, layer_norm_pipe<T, TW, V, MP, NT>,
+                  g.persist && M <= PC, rows, g, [&](auto kern, int64_t grid) {
+                    hipLaunchKernelGGL(kern, dim3(grid), dim3(g.block), 0, s,
+                                       static_cast<const T*>(x), static_cast<const TW*>(w),
+                                       static_cast<const TW*>(b), static_cast<T*>(y), rows,
+                                       cols, g.tpr, eps);
+                  });
+            };
+            if (g.nt) body(std::true_type{});
+            else body(std::false_type{});
           }
         });
       };
@@ -300,11 +508,20 @@ hipError_t launch_rms_norm(const void* x, const void* w, void* y, int64_t rows, 
         dispatch_maxit(g.maxit, [&](auto mc) {
           constexpr int M = decltype(mc)::value;
           if constexpr (M <= lane_cap(V)) {
-            hipLaunchKernelGGL((rms_norm_rows<T, TW, V, M>), dim3(grid_for(rows, g)),
-                               dim3(g.block), 0, s, static_cast<const T*>(x),
-                               static_cast<const TW*>(w), static_cast<T*>(y), rows, cols,
-                               g.tpr, eps);
-            err = hipGetLastError();
+            auto body = [&](auto nt) {
+              constexpr bool NT = decltype(nt)::value;
+              constexpr int PC = pipe_cap<T, TW, V, 1>();
+              constexpr int MP = M <= PC ? M : PC;
+              err = launch_rows_or_pipe(
+                  rms_norm_rows<T, TW, V, M, NT>, rms_norm_pipe<T, TW, V, MP, NT>,
+                  g.persist && M <= PC, rows, g, [&](auto kern, int64_t grid) {
+                    hipLaunchKernelGGL(kern, dim3(grid), dim3(g.block), 0, s,
+                                       static_cast<const T*>(x), static_cast<const TW*>(w),
+                                       static_cast<T*>(y), rows, cols, g.tpr, eps);
+                  });
+            };
+            if (g.nt) body(std::true_type{});
+            else body(std::false_type{});
           }
         });
       };

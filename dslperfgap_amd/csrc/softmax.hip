@@ -1,8 +1,9 @@
 // Softmax, log-softmax and logsumexp forward for gfx950.
 //
-// Register-resident path: `tpr` lanes own one row, load it once into fp32
-// registers (padding lanes hold -inf), all-reduce the row max, then the sum of
-// exp(x - max), and write the row once.
+// Register-resident path: `tpr` lanes own one row (a power of two up to 64 or a
+// multiple of 64 up to 1024) and load it once into registers that keep the
+// storage type; the group all-reduces the row max, then the sum of
+// exp(x - max), and writes the row once.
 // Streaming path (rows wider than the register budget): one workgroup per row,
 // online (max, rescaled sum) statistics pass, then an output pass.
 // Middle-axis path: contiguous [outer, n, inner] reduced over n; one thread per
@@ -22,47 +23,47 @@ namespace {
 
 constexpr float kNegInf = -__builtin_huge_valf();
 
-template <typename T, int V, int MAXIT>
-__device__ __forceinline__ void load_row_fill(const T* __restrict__ xr, int nvec, int g,
-                                              int tpr, float fill, float (&v)[MAXIT][V]) {
+template <typename T, int V, int IT, bool NT>
+__device__ __forceinline__ void load_raw_row(const T* __restrict__ xr, int nvec, int g, int tpr,
+                                             typename Raw<T, V>::type (&dst)[IT]) {
 #pragma unroll
-  for (int i = 0; i < MAXIT; ++i) {
+  for (int i = 0; i < IT; ++i) {
     const int j = i * tpr + g;
-    if (j < nvec) {
-      load_f32<T, V>(xr + static_cast<int64_t>(j) * V, v[i]);
-    } else {
-#pragma unroll
-      for (int k = 0; k < V; ++k) v[i][k] = fill;
-    }
+    if (j < nvec) dst[i] = load_raw<T, V, NT>(xr + static_cast<int64_t>(j) * V);
+    else dst[i] = typename Raw<T, V>::type{};
   }
 }
 
-template <int MAXIT, int V>
-__device__ __forceinline__ float lane_max(const float (&v)[MAXIT][V]) {
+// max over the lane's valid values (-inf when it holds none)
+template <typename T, int V, int IT>
+__device__ __forceinline__ float lane_max(const typename Raw<T, V>::type (&xr)[IT], int nvec,
+                                          int g, int tpr) {
   float m[V];
 #pragma unroll
-  for (int k = 0; k < V; ++k) m[k] = v[0][k];
+  for (int k = 0; k < V; ++k) m[k] = kNegInf;
 #pragma unroll
-  for (int i = 1; i < MAXIT; ++i)
+  for (int i = 0; i < IT; ++i)
+    if (i * tpr + g < nvec)
 #pragma unroll
-    for (int k = 0; k < V; ++k) m[k] = fmaxf(m[k], v[i][k]);
+      for (int k = 0; k < V; ++k) m[k] = fmaxf(m[k], raw_at<T, V>(xr[i], k));
   float r = m[0];
 #pragma unroll
   for (int k = 1; k < V; ++k) r = fmaxf(r, m[k]);
   return r;
 }
 
-// sum over the lane's values of exp(v - shift); padding values are -inf and
-// contribute exp(-inf) = 0 whenever shift is finite.
-template <int MAXIT, int V>
-__device__ __forceinline__ float lane_sum_exp(const float (&v)[MAXIT][V], float shift) {
+// sum over the lane's valid values of exp(v - shift)
+template <typename T, int V, int IT>
+__device__ __forceinline__ float lane_sum_exp(const typename Raw<T, V>::type (&xr)[IT], int nvec,
+                                              int g, int tpr, float shift) {
   float a[V];
 #pragma unroll
   for (int k = 0; k < V; ++k) a[k] = 0.f;
 #pragma unroll
-  for (int i = 0; i < MAXIT; ++i)
+  for (int i = 0; i < IT; ++i)
+    if (i * tpr + g < nvec)
 #pragma unroll
-    for (int k = 0; k < V; ++k) a[k] += fast_exp(v[i][k] - shift);
+      for (int k = 0; k < V; ++k) a[k] += fast_exp(raw_at<T, V>(xr[i], k) - shift);
 #pragma unroll
   for (int w = V / 2; w >= 1; w /= 2)
 #pragma unroll
@@ -70,67 +71,64 @@ __device__ __forceinline__ float lane_sum_exp(const float (&v)[MAXIT][V], float 
   return a[0];
 }
 
-template <typename Ti, typename To, int V, int MAXIT, bool LOG>
+template <typename Ti, typename To, int V, int IT, bool LOG, bool NT>
 __global__ __launch_bounds__(kMaxBlock) void softmax_rows(const Ti* __restrict__ x,
                                                           To* __restrict__ y, int64_t rows,
                                                           int cols, int tpr) {
+  typedef typename Raw<Ti, V>::type RT;
   __shared__ float lds[2][kMaxWaves];
   const int nvec = cols / V;
-  const int g = threadIdx.x & (tpr - 1);
+  const int g = threadIdx.x % tpr;
   int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / tpr) + threadIdx.x / tpr;
   const bool live = row < rows;
   if (!live) row = rows - 1;
 
-  float v[MAXIT][V];
-  load_row_fill<Ti, V, MAXIT>(x + row * cols, nvec, g, tpr, kNegInf, v);
-  const float m = group_allreduce<Max>(lane_max<MAXIT, V>(v), tpr, lds[0]);
-  const float s = group_allreduce<Sum>(lane_sum_exp<MAXIT, V>(v, m), tpr, lds[1]);
+  RT xr[IT];
+  load_raw_row<Ti, V, IT, NT>(x + row * cols, nvec, g, tpr, xr);
+  const float m = group_allreduce<Max>(lane_max<Ti, V, IT>(xr, nvec, g, tpr), tpr, lds[0]);
+  reload_barrier<Ti, V, IT>(xr);
+  const float s =
+      group_allreduce<Sum>(lane_sum_exp<Ti, V, IT>(xr, nvec, g, tpr, m), tpr, lds[1]);
   if (!live) return;
+  reload_barrier<Ti, V, IT>(xr);
 
   To* yr = y + row * cols;
-  if constexpr (LOG) {
-    const float ls = fast_log(s);
+  const float ls = LOG ? fast_log(s) : 0.f;
+  const float r = LOG ? 0.f : 1.0f / s;
 #pragma unroll
-    for (int i = 0; i < MAXIT; ++i) {
-      const int j = i * tpr + g;
-      if (j < nvec) {
-        float o[V];
+  for (int i = 0; i < IT; ++i) {
+    const int j = i * tpr + g;
+    if (j < nvec) {
+      float o[V];
 #pragma unroll
-        for (int k = 0; k < V; ++k) o[k] = (v[i][k] - m) - ls;
-        store_from_f32<To, V>(yr + static_cast<int64_t>(j) * V, o);
+      for (int k = 0; k < V; ++k) {
+        const float d = raw_at<Ti, V>(xr[i], k) - m;
+        o[k] = LOG ? d - ls : fast_exp(d) * r;
       }
-    }
-  } else {
-    const float r = 1.0f / s;
-#pragma unroll
-    for (int i = 0; i < MAXIT; ++i) {
-      const int j = i * tpr + g;
-      if (j < nvec) {
-        float o[V];
-#pragma unroll
-        for (int k = 0; k < V; ++k) o[k] = fast_exp(v[i][k] - m) * r;
-        store_from_f32<To, V>(yr + static_cast<int64_t>(j) * V, o);
-      }
+      store_raw<To, V, NT>(yr + static_cast<int64_t>(j) * V, o);
     }
   }
 }
 
-template <typename Ti, typename To, int V, int MAXIT>
+template <typename Ti, typename To, int V, int IT, bool NT>
 __global__ __launch_bounds__(kMaxBlock) void logsumexp_rows(const Ti* __restrict__ x,
                                                             To* __restrict__ y, int64_t rows,
                                                             int cols, int tpr) {
+  typedef typename Raw<Ti, V>::type RT;
   __shared__ float lds[2][kMaxWaves];
   const int nvec = cols / V;
-  const int g = threadIdx.x & (tpr - 1);
+  const int g = threadIdx.x % tpr;
   int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / tpr) + threadIdx.x / tpr;
   const bool live = row < rows;
   if (!live) row = rows - 1;
 
-  float v[MAXIT][V];
-  load_row_fill<Ti, V, MAXIT>(x + row * cols, nvec, g, tpr, kNegInf, v);
-  float m = group_allreduce<Max>(lane_max<MAXIT, V>(v), tpr, lds[0]);
+  RT xr[IT];
+  load_raw_row<Ti, V, IT, NT>(x + row * cols, nvec, g, tpr, xr);
+  float m = group_allreduce<Max>(lane_max<Ti, V, IT>(xr, nvec, g, tpr), tpr, lds[0]);
+  reload_barrier<Ti, V, IT>(xr);
   if (__builtin_isinf(m)) m = 0.f;
-  const float s = group_allreduce<Sum>(lane_sum_exp<MAXIT, V>(v, m), tpr, lds[1]);
+  const float s =
+      group_allreduce<Sum>(lane_sum_exp<Ti, V, IT>(xr, nvec, g, tpr, m), tpr, lds[1]);
   if (live && g == 0) {
     const float r = fast_log(s) + m;
     store_from_f32<To, 1>(y + row, &r);
@@ -295,9 +293,14 @@ hipError_t launch_softmax(const void* x, void* y, int64_t rows, int cols, int id
       dispatch_maxit(g.maxit, [&](auto mc) {
         constexpr int M = decltype(mc)::value;
         if constexpr (M <= lane_cap(V)) {
-          hipLaunchKernelGGL((softmax_rows<Ti, To, V, M, LOG>), dim3(grid_for(rows, g)),
-                             dim3(g.block), 0, s, static_cast<const Ti*>(x),
-                             static_cast<To*>(y), rows, cols, g.tpr);
+          if (g.nt)
+            hipLaunchKernelGGL((softmax_rows<Ti, To, V, M, LOG, true>), dim3(grid_for(rows, g)),
+                               dim3(g.block), 0, s, static_cast<const Ti*>(x),
+                               static_cast<To*>(y), rows, cols, g.tpr);
+          else
+            hipLaunchKernelGGL((softmax_rows<Ti, To, V, M, LOG, false>), dim3(grid_for(rows, g)),
+                               dim3(g.block), 0, s, static_cast<const Ti*>(x),
+                               static_cast<To*>(y), rows, cols, g.tpr);
           err = hipGetLastError();
         }
       });
@@ -330,9 +333,14 @@ hipError_t launch_logsumexp(const void* x, void* y, int64_t rows, int cols, int 
       dispatch_maxit(g.maxit, [&](auto mc) {
         constexpr int M = decltype(mc)::value;
         if constexpr (M <= lane_cap(V)) {
-          hipLaunchKernelGGL((logsumexp_rows<Ti, To, V, M>), dim3(grid_for(rows, g)),
-                             dim3(g.block), 0, s, static_cast<const Ti*>(x),
-                             static_cast<To*>(y), rows, cols, g.tpr);
+          if (g.nt)
+            hipLaunchKernelGGL((logsumexp_rows<Ti, To, V, M, true>), dim3(grid_for(rows, g)),
+                               dim3(g.block), 0, s, static_cast<const Ti*>(x),
+                               static_cast<To*>(y), rows, cols, g.tpr);
+          else
+            hipLaunchKernelGGL((logsumexp_rows<Ti, To, V, M, false>), dim3(grid_for(rows, g)),
+                               dim3(g.block), 0, s, static_cast<const Ti*>(x),
+                               static_cast<To*>(y), rows, cols, g.tpr);
           err = hipGetLastError();
         }
       });

@@ -59,6 +59,61 @@ __device__ __forceinline__ void store_from_f32(T* __restrict__ p, const float* o
   }
 }
 
+// Raw storage vectors: a row kept in registers in its storage type (4 VGPRs
+// per 16-byte vector whatever the dtype) and widened to fp32 where used.
+template <typename T, int V> struct Raw { typedef T type __attribute__((ext_vector_type(V))); };
+template <typename T> struct Raw<T, 1> { typedef T type; };
+
+// 16-byte (or scalar) load; NT marks the access nontemporal (streamed data
+// that is touched once), which keeps it from displacing reused lines.
+template <typename T, int V, bool NT>
+__device__ __forceinline__ typename Raw<T, V>::type load_raw(const T* __restrict__ p) {
+  typedef typename Raw<T, V>::type R;
+  const R* q = reinterpret_cast<const R*>(p);
+  if constexpr (NT) return __builtin_nontemporal_load(q);
+  else return *q;
+}
+
+template <typename T, int V>
+__device__ __forceinline__ float raw_at(const typename Raw<T, V>::type& r, int k) {
+  if constexpr (V == 1) return static_cast<float>(r);
+  else return static_cast<float>(r[k]);
+}
+
+// Register barrier for a row held in a 16-bit storage type: after this point
+// the compiler must assume the raw registers changed, so it re-widens values
+// from them instead of keeping a widened fp32 copy of the whole row live across
+// a reduction (which would double the VGPRs of the row and halve occupancy).
+// fp32 rows need no barrier (raw and widened are the same registers).
+template <typename T, int V, int IT>
+__device__ __forceinline__ void reload_barrier(typename Raw<T, V>::type (&r)[IT]) {
+  if constexpr (sizeof(T) == 2 && V > 1) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    static_assert(sizeof(typename Raw<T, V>::type) == 16, "16-byte vectors expected");
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      u32x4 u = __builtin_bit_cast(u32x4, r[i]);
+      asm volatile("" : "+v"(u));
+      r[i] = __builtin_bit_cast(typename Raw<T, V>::type, u);
+    }
+  }
+}
+
+template <typename T, int V, bool NT>
+__device__ __forceinline__ void store_raw(T* __restrict__ p, const float* o) {
+  typedef typename Raw<T, V>::type R;
+  R r;
+  if constexpr (V == 1) {
+    r = static_cast<T>(o[0]);
+  } else {
+#pragma unroll
+    for (int k = 0; k < V; ++k) r[k] = static_cast<T>(o[k]);
+  }
+  R* q = reinterpret_cast<R*>(p);
+  if constexpr (NT) __builtin_nontemporal_store(r, q);
+  else *q = r;
+}
+
 // ---------------------------------------------------------------------------
 // reductions
 // ---------------------------------------------------------------------------
@@ -101,20 +156,20 @@ __device__ __forceinline__ float wave_allreduce(float v, int width) {
   return v;
 }
 
-// All-reduce across the `tpr` threads that own one row.  For tpr <= 64 the
-// group lives inside one wave; for tpr > 64 a row spans tpr / 64 consecutive
-// waves of the workgroup and wave partials are exchanged through `lds`
-// (kMaxWaves floats, one slot per wave of the workgroup).  When tpr > 64 every
-// thread of the workgroup must reach the call (it contains a barrier), and each
-// `lds` buffer may serve only one reduction per kernel instance (there is no
-// trailing barrier).
+// All-reduce across the `tpr` threads that own one row.  For tpr <= 64 (a
+// power of two) the group lives inside one wave; for tpr > 64 (any multiple of
+// 64) a row spans tpr / 64 consecutive waves of the workgroup and wave partials
+// are exchanged through `lds` (kMaxWaves floats, one slot per wave of the
+// workgroup).  When tpr > 64 every thread of the workgroup must reach the call
+// (it contains a barrier), and each `lds` buffer may serve only one reduction
+// per kernel instance (there is no trailing barrier).
 template <class Op>
 __device__ __forceinline__ float group_allreduce(float v, int tpr, float* lds) {
   if (tpr <= kWave) return wave_allreduce<Op>(v, tpr);
   v = wave_allreduce<Op>(v, kWave);
   const int wave = threadIdx.x / kWave;
   const int nwaves = tpr / kWave;
-  const int first = wave - (wave & (nwaves - 1));
+  const int first = (wave / nwaves) * nwaves;
   if ((threadIdx.x & (kWave - 1)) == 0) lds[wave] = v;
   __syncthreads();
   float r = lds[first];
@@ -128,15 +183,21 @@ struct Moments {
 };
 
 // Chan et al. pairwise merge in a form that is symmetric in (a, b), so both
-// partners of a butterfly step compute bit-identical results.
+// partners of a butterfly step compute bit-identical results:
+//   mean = (ma + mb) / 2 + (mb - ma) * (nb - na) / (2 n)
+// (= (na ma + nb mb) / n), which is exact when the two means are equal, and
+//   m2   = m2a + m2b + (mb - ma)^2 * na nb / n.
+// Swapping a and b negates both factors of the correction term, which leaves
+// every rounded intermediate unchanged.
 __device__ __forceinline__ Moments merge_moments(Moments a, Moments b) {
+  if (a.n == 0.f) return b;
+  if (b.n == 0.f) return a;
   const float n = a.n + b.n;
-  if (n == 0.f) return Moments{0.f, 0.f, 0.f};
   const float inv = 1.0f / n;
   const float d = b.mean - a.mean;
   Moments r;
   r.n = n;
-  r.mean = (a.n * a.mean + b.n * b.mean) * inv;
+  r.mean = 0.5f * (a.mean + b.mean) + (0.5f * d) * ((b.n - a.n) * inv);
   r.m2 = (a.m2 + b.m2) + d * d * (a.n * b.n * inv);
   return r;
 }
@@ -178,7 +239,7 @@ __device__ __forceinline__ Moments group_allreduce_moments(Moments m, int tpr, f
   if (tpr <= kWave) return m;
   const int wave = threadIdx.x / kWave;
   const int nwaves = tpr / kWave;
-  const int first = wave - (wave & (nwaves - 1));
+  const int first = (wave / nwaves) * nwaves;
   if ((threadIdx.x & (kWave - 1)) == 0) {
     lds[wave] = m.n;
     lds[kMaxWaves + wave] = m.mean;

@@ -20,26 +20,54 @@ enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2, kI32 = 3, kI64 = 4 };
 //   block  workgroup size (a multiple of 64 and of tpr)
 //   maxit  vectors held in registers per lane (power of two)
 //   stream row too wide for registers: chunked two-pass kernel instead
+//   persist  persistent pipelined kernel: grid sized to the resident
+//          capacity, each row group loops over rows, keeps per-column vectors
+//          (weight, bias) in registers and prefetches its next row
+//   nt     nontemporal hints on the streamed row loads / output stores
 struct Geometry {
   int v = 1;
   int tpr = 64;
   int block = 256;
   int maxit = 1;
   bool stream = false;
+  bool persist = false;
+  bool nt = false;
 };
 
-// Register budget per lane for the register-resident path: at most 64 fp32
-// values and at most 32 separate accesses (scalar rows spill beyond that).
-constexpr int kLaneValues = 64;
-constexpr int kMaxIters = 32;
-constexpr int lane_cap(int vec) {
-  return kLaneValues / vec < kMaxIters ? kLaneValues / vec : kMaxIters;
+// vbh_tune_override flag bits
+constexpr int kFlagPersist = 1;
+constexpr int kFlagNoPersist = 2;
+constexpr int kFlagNontemporal = 4;
+constexpr int kFlagTemporal = 8;
+
+// The persistent kernels keep up to this many 16-byte vectors per lane for each
+// of: current row, next row, and every per-column vector (their register cap
+// per instantiation is pipe_cap in rownorm.hip).
+constexpr int kPipeMaxIt = 4;
+
+// Number of workgroups of `block` lanes of `kernel` that are resident on the
+// whole current device at once (occupancy x compute units), cached.
+int64_t resident_blocks(const void* kernel, int block);
+
+// Register budget per lane for a register-resident row: 64 values (the
+// compiler widens every 16-bit value it reuses to an fp32 register), i.e. 16
+// fp32 or 8 bf16/fp16 vectors of 16 bytes, or 16 scalar elements for rows that
+// are not 16-byte aligned (each scalar access also holds its own address).
+constexpr int lane_cap(int vec) { return vec > 1 ? 64 / vec : 16; }
+
+// VGPRs that IT vectors of V elements of type T occupy in raw storage.
+template <typename T>
+constexpr int raw_vgprs(int v, int it) {
+  return static_cast<int>((it * v * sizeof(T) + 3) / 4);
 }
 
 // Choose the geometry for rows of `cols` elements.  `vec` is the 16-byte vector
-// width when every row start is 16-byte aligned and cols % vec == 0, else 1.
-// `tpr_override` / `block_override` come from vbh_tune_override (0 = none).
-Geometry pick_geometry(int64_t cols, int vec, int tpr_override, int block_override);
+// width when every row start is 16-byte aligned and cols % vec == 0, else 1;
+// `it_target` the preferred vectors per lane.  `tpr_override` /
+// `block_override` come from vbh_tune_override (0 = none), `flags` are the
+// resolved kFlagPersist / kFlagNontemporal bits.
+Geometry pick_geometry(int64_t cols, int vec, int it_target, int tpr_override,
+                       int block_override, int flags);
 
 // ---------------------------------------------------------------------------
 // compile-time dispatch helpers

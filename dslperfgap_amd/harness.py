@@ -129,6 +129,20 @@ def time_back_to_back(launch: Callable[[int], None], steps: int, warmup: int) ->
     return {"event_ms": s.elapsed_time(e), "wall_ms": wall, "steps": steps}
 
 
+def warm_gpu(launch: Callable[[int], None], seconds: float = 0.5) -> int:
+    """Run `launch` back to back for about `seconds` so that clocks and page
+    tables are at steady state before a timed region; returns launches made."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(16):
+            launch(n)
+            n += 1
+        torch.cuda.synchronize()
+    return n
+
+
 def copy_peak(device, nbytes: int = 4 << 30, reps: int = 20) -> float:
     """Sustained device-to-device copy rate in bytes/s (read + write counted)."""
     src = torch.empty(nbytes, dtype=torch.uint8, device=device)
@@ -139,9 +153,33 @@ def copy_peak(device, nbytes: int = 4 << 30, reps: int = 20) -> float:
     def launch(_):
         _lib.call("vbh_stream_copy", src.data_ptr(), dst.data_ptr(), nbytes, stream)
 
+    warm_gpu(launch, 0.3)
     r = time_back_to_back(launch, reps, 3)
     del src, dst
     return 2.0 * nbytes * reps / (r["event_ms"] * 1e-3)
+
+
+def copy_rate_at(device, traffic_bytes: int, reps: int = 200,
+                 min_footprint: int = 2 << 30) -> float:
+    """Copy rate (bytes/s, read + write) when one launch moves `traffic_bytes`
+    (half read, half written), cycling through enough buffers that no launch
+    hits the Infinity Cache: the achievable rate at a kernel's own size."""
+    half = max(16, (traffic_bytes // 2) // 16 * 16)
+    copies = max(2, math.ceil(min_footprint / (2 * half)))
+    bufs = [(torch.empty(half, dtype=torch.uint8, device=device),
+             torch.empty(half, dtype=torch.uint8, device=device)) for _ in range(copies)]
+    for a, _ in bufs:
+        a.fill_(1)
+    stream = _bridge.stream(torch.device(device))
+
+    def launch(k):
+        a, b = bufs[k % copies]
+        _lib.call("vbh_stream_copy", a.data_ptr(), b.data_ptr(), half, stream)
+
+    warm_gpu(launch, 0.3)
+    r = time_back_to_back(launch, reps, 2 * copies)
+    del bufs
+    return 2.0 * half * reps / (r["event_ms"] * 1e-3)
 
 
 @dataclass

@@ -133,11 +133,18 @@ int vbh_cross_entropy_bwd(const void* dloss, const void* logits, const void* lse
  *           (no AMD entry there) with a measured figure. */
 int vbh_stream_copy(const void* src, void* dst, int64_t bytes, void* stream);
 
-/* Launch-geometry override for sweeps: threads per row `tpr` (power of two,
- * 1..1024) and workgroup size `block` (64..1024, multiple of 64) for op `op`.
- * tpr = 0 restores the built-in shape heuristic.  Process-wide setting.
+/* Launch-geometry override for sweeps: threads per row `tpr` (a power of two
+ * up to 64, or a multiple of 64 up to 1024) and workgroup size `block`
+ * (64..1024, a multiple of 64 and of tpr)
+ * for op `op`; `flags` ORs VBH_TUNE_* bits.  tpr = 0 keeps the built-in shape
+ * heuristic, block = 0 its workgroup size, flags = 0 its kernel choice.
+ * Process-wide setting.
  * Replaces: the import-time config injection of ViperBench/tuning/cache.py:31-36. */
-int vbh_tune_override(int op, int tpr, int block);
+#define VBH_TUNE_PERSIST 1      /* force the persistent pipelined row kernel    */
+#define VBH_TUNE_NO_PERSIST 2   /* force one row group per workgroup            */
+#define VBH_TUNE_NONTEMPORAL 4  /* force nontemporal row loads / output stores  */
+#define VBH_TUNE_TEMPORAL 8     /* force plain row loads / output stores        */
+int vbh_tune_override(int op, int tpr, int block, int flags);
 
 #ifdef __cplusplus
 }

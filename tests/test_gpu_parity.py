@@ -291,32 +291,43 @@ def test_empty_and_degenerate():
 # ---------------------------------------------------------------------------
 # launch-geometry overrides: every group size must give the same answer
 # ---------------------------------------------------------------------------
-@pytest.mark.parametrize("tpr,block", [(1, 64), (4, 256), (16, 128), (64, 64), (128, 512),
-                                       (256, 256), (512, 1024), (1024, 1024)])
-def test_geometry_overrides(tpr, block):
+GEOMETRIES = [(1, 64), (4, 256), (16, 128), (64, 64), (128, 512), (192, 384), (256, 256),
+              (320, 960), (512, 1024), (640, 640), (1024, 1024)]
+
+
+@pytest.mark.parametrize("flags", [0, _lib.TUNE_PERSIST | _lib.TUNE_NONTEMPORAL,
+                                   _lib.TUNE_NONTEMPORAL])
+@pytest.mark.parametrize("tpr,block", GEOMETRIES)
+@pytest.mark.parametrize("cols", [200, 3000])
+def test_geometry_overrides(tpr, block, flags, cols):
     g = _g(110)
-    x = torch.randn(50, 3000, generator=g)
-    w, b = torch.randn(3000, generator=g), torch.randn(3000, generator=g)
-    logits = torch.randn(20, 3000, generator=g)
-    labels = torch.randint(0, 3000, (20,), generator=g)
+    x = torch.randn(50, cols, generator=g)
+    w, b = torch.randn(cols, generator=g), torch.randn(cols, generator=g)
+    xb, wb, bb = x.to(torch.bfloat16), w.to(torch.bfloat16), b.to(torch.bfloat16)
+    logits = torch.randn(20, cols, generator=g)
+    labels = torch.randint(0, cols, (20,), generator=g)
     xd, wd, bd, ld, lbd = cuda(x, w, b, logits, labels)
+    xbd, wbd, bbd = cuda(xb, wb, bb)
     ops = [_lib.OP_LAYER_NORM, _lib.OP_RMS_NORM, _lib.OP_SOFTMAX, _lib.OP_LOGSUMEXP,
            _lib.OP_CROSS_ENTROPY]
     try:
         for op in ops:
-            _lib.tune_override(op, tpr, block)
-        tag = f"tpr={tpr} block={block}"
+            _lib.tune_override(op, tpr, block, flags)
+        tag = f"tpr={tpr} block={block} flags={flags} cols={cols}"
         check(layer_norm(xd, wd, bd), ref.layer_norm(x, w, b), torch.float32, what=tag)
-        check(rms_norm(xd, (3000,), wd), ref.rms_norm(x, (3000,), w), torch.float32, what=tag)
+        check(layer_norm(xbd, wbd, bbd), ref.layer_norm(xb, wb, bb), torch.bfloat16, what=tag)
+        check(rms_norm(xd, (cols,), wd), ref.rms_norm(x, (cols,), w), torch.float32, what=tag)
+        check(rms_norm(xbd, (cols,), wbd), ref.rms_norm(xb, (cols,), wb), torch.bfloat16,
+              what=tag)
         check(softmax(xd), ref.softmax(x), torch.float32, what=tag)
-        check(log_softmax(xd), ref.log_softmax(x), torch.float32, what=tag)
+        check(log_softmax(xbd), ref.log_softmax(xb), torch.bfloat16, what=tag)
         check(logsumexp(xd), ref.logsumexp(x), torch.float32, what=tag)
-        args = (0.1, 1.0, 0.01, -100, 3000, 0, 1024, True, False)
+        args = (0.1, 1.0, 0.01, -100, cols, 0, 1024, True, False)
         check_ce(cross_entropy_fwd(ld, lbd, *args), ref.cross_entropy_fwd(logits, labels, *args),
-                 20, 3000, 1024, False, what=tag)
+                 20, cols, 1024, False, what=tag)
     finally:
         for op in ops:
-            _lib.tune_override(op, 0, 0)
+            _lib.tune_override(op, 0, 0, 0)
 
 
 # ---------------------------------------------------------------------------

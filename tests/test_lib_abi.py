@@ -75,8 +75,11 @@ def test_argument_errors_before_launch():
             _lib.F32, None, match="null")
     _expect(_lib.E_INVALID, "vbh_stream_copy", 16, 16, 15, None, match="multiple of 16")
     _expect(_lib.E_RANGE, "vbh_softmax_fwd", 16, 16, 4, 1 << 31, _lib.F32, _lib.F32, 0, None)
-    _expect(_lib.E_INVALID, "vbh_tune_override", 0, 3, 0, match="power of two")
-    _expect(_lib.E_INVALID, "vbh_tune_override", 9, 0, 0, match="bad op")
+    _expect(_lib.E_INVALID, "vbh_tune_override", 0, 3, 0, 0, match="power of two")
+    _expect(_lib.E_INVALID, "vbh_tune_override", 0, 96, 0, 0, match="multiple of 64")
+    _expect(_lib.E_INVALID, "vbh_tune_override", 0, 128, 192, 0, match="multiple of tpr")
+    _expect(_lib.E_INVALID, "vbh_tune_override", 9, 0, 0, 0, match="bad op")
+    _expect(_lib.E_INVALID, "vbh_tune_override", 0, 0, 0, 64, match="flag")
     assert _lib.last_error()
 
 
@@ -86,7 +89,7 @@ def test_empty_sizes_are_noops():
               None)
     _lib.call("vbh_softmax_fwd", None, None, 0, 7, _lib.F16, _lib.F32, 1, None)
     _lib.call("vbh_stream_copy", None, None, 0, None)
-    _lib.call("vbh_tune_override", 2, 0, 0)
+    _lib.call("vbh_tune_override", 2, 0, 0, 0)
 
 
 def test_missing_library_is_loud(monkeypatch, tmp_path):
