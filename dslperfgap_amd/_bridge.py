@@ -2,6 +2,8 @@
 checks, raw pointers and the current HIP stream.  Nothing here computes."""
 from __future__ import annotations
 
+import contextlib
+
 import torch
 
 from . import _lib
@@ -39,9 +41,22 @@ def ptr(t: torch.Tensor | None):
     return None if t is None else t.data_ptr()
 
 
+# torch's raw current-stream accessor skips building a Stream object per call
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream(dev: torch.device) -> int:
     """Handle of torch's current stream on `dev` (the library launches there)."""
+    if _raw_stream is not None:
+        return _raw_stream(dev.index if dev.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(dev).cuda_stream
+
+
+def device_guard(dev: torch.device):
+    """Make `dev` current for the launch; a no-op when it already is."""
+    if dev.index is None or dev.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(dev)
 
 
 def numel_prod(shape) -> int:

@@ -25,7 +25,9 @@ F32, F16, BF16, I32, I64 = 0, 1, 2, 3, 4
 # argument-error codes (VBH_E_*)
 E_INVALID, E_DTYPE, E_RANGE = -1, -2, -3
 # op codes for vbh_tune_override (VBH_OP_*)
-OP_LAYER_NORM, OP_RMS_NORM, OP_SOFTMAX, OP_LOGSUMEXP, OP_CROSS_ENTROPY = 0, 1, 2, 3, 4
+OP_LAYER_NORM, OP_RMS_NORM, OP_SOFTMAX, OP_LOGSUMEXP, OP_CROSS_ENTROPY, OP_REDUCE = 0, 1, 2, 3, 4, 5
+# reduction codes (VBH_REDUCE_*)
+REDUCE_MEAN, REDUCE_MAX, REDUCE_ARGMAX = 0, 1, 2
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -51,6 +53,7 @@ SIGNATURES = {
         [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _f32,
          _i64, _i64, _i64, _i32, _vp],
     ),
+    "vbh_reduce_fwd": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32, _vp]),
     "vbh_stream_copy": (_i32, [_vp, _vp, _i64, _vp]),
     "vbh_tune_override": (_i32, [_i32, _i32, _i32, _i32]),
 }
@@ -66,6 +69,7 @@ class VbhError(RuntimeError):
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
+_fns: dict = {}
 
 
 def lib() -> ctypes.CDLL:
@@ -87,6 +91,7 @@ def lib() -> ctypes.CDLL:
             version = handle.vbh_abi_version()
             if version != ABI_VERSION:
                 raise ImportError(f"{LIB_PATH} has ABI {version}, expected {ABI_VERSION}")
+            _fns.update({name: getattr(handle, name) for name in SIGNATURES})
             _lib = handle
     return _lib
 
@@ -98,7 +103,9 @@ def last_error() -> str:
 
 def call(name: str, *args) -> None:
     """Call entry point `name`; raise VbhError on a nonzero status."""
-    rc = getattr(lib(), name)(*args)
+    if _lib is None:
+        lib()
+    rc = _fns[name](*args)
     if rc != 0:
         raise VbhError(name, rc, last_error())
 

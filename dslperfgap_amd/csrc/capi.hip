@@ -51,7 +51,7 @@ bool is_float(int dt) { return dt == kF32 || dt == kF16 || dt == kBF16; }
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // process-wide launch-geometry overrides (vbh_tune_override)
-constexpr int kNumOps = 5;
+constexpr int kNumOps = 6;
 std::atomic<int> g_tpr[kNumOps];
 std::atomic<int> g_block[kNumOps];
 std::atomic<int> g_flags[kNumOps];
@@ -60,13 +60,13 @@ std::atomic<int> g_flags[kNumOps];
 //   vectors per lane before more lanes are added (pick_geometry): 2 for softmax
 //   and RMSNorm, 4 for LayerNorm (its two reductions per row favour fewer
 //   waves per row) and for the reductions that write one value per row
-//   (logsumexp, cross entropy);
+//   (logsumexp, cross entropy, mean / max / argmax);
 //   nontemporal row loads / stores for every op (rows are touched once);
 //   the persistent pipelined kernel for LayerNorm / RMSNorm rows that span 512
 //   or more lanes (few, wide rows: it keeps every CU streaming instead of
 //   running the grid in a handful of rounds); narrower rows run one row group
 //   per workgroup.
-constexpr int kItTarget[kNumOps] = {4, 2, 2, 4, 4};
+constexpr int kItTarget[kNumOps] = {4, 2, 2, 4, 4, 4};
 constexpr int kPersistMinTpr = 512;
 
 Geometry geometry_for(int op, int64_t cols, int vec) {
@@ -409,6 +409,40 @@ int vbh_cross_entropy_bwd(const void* dloss, const void* logits, const void* lse
               : 1;
   return hip_status(launch_cross_entropy_bwd(a, static_cast<hipStream_t>(stream)),
                     "cross_entropy_bwd launch");
+}
+
+int vbh_reduce_fwd(const void* x, void* values, void* indices, int64_t outer, int64_t n,
+                   int64_t inner, int in_dtype, int out_dtype, int op, void* stream) {
+  if (op < 0 || op > 2) return fail(VBH_E_INVALID, "reduce: unknown op %d", op);
+  if (!is_float(in_dtype)) return fail(VBH_E_DTYPE, "reduce: unsupported dtype %d", in_dtype);
+  if (op == 0 ? !(out_dtype == in_dtype || (out_dtype == kF32 && in_dtype != kF32))
+              : out_dtype != in_dtype)
+    return fail(VBH_E_DTYPE, "reduce: unsupported (in, out) dtype pair (%d, %d)", in_dtype,
+                out_dtype);
+  if (outer < 0 || n < 0 || inner < 0) return fail(VBH_E_INVALID, "reduce: negative size");
+  if (n > kMaxCols) return fail(VBH_E_RANGE, "reduce: n too large");
+  if (outer == 0 || inner == 0) return 0;
+  if (n == 0 && op != 0) return fail(VBH_E_INVALID, "reduce: max / argmax of an empty axis");
+  if ((!x && n > 0) || (op != 2 && !values) || (op != 0 && !indices))
+    return fail(VBH_E_INVALID, "reduce: null pointer");
+  Geometry g;
+  if (inner == 1) {
+    const int vn = 16 / elt_size(in_dtype);
+    const bool vec_ok = n % vn == 0 && aligned16(x);
+    g = geometry_for(VBH_OP_REDUCE, n, vec_ok ? vn : 1);
+    if (g.stream) {  // no per-element output: the row kernel streams any length
+      g.stream = false;
+      g.tpr = kMaxBlock;
+      g.block = kMaxBlock;
+    }
+    if (int rc = check_grid(outer, g)) return rc;
+  } else if ((outer * inner + 255) / 256 * 256 > kMaxWorkItems) {
+    return fail(VBH_E_RANGE, "reduce: outer * inner too large");
+  }
+  return hip_status(launch_reduce(x, values, static_cast<int64_t*>(indices), outer,
+                                  static_cast<int>(n), inner, in_dtype, out_dtype, op, g,
+                                  static_cast<hipStream_t>(stream)),
+                    "reduce launch");
 }
 
 int vbh_stream_copy(const void* src, void* dst, int64_t bytes, void* stream) {

@@ -1,0 +1,206 @@
+// Mean, max (value + index) and argmax over one axis, for gfx950.
+//
+// The tensor is viewed as contiguous [outer, n, inner] and reduced over n.
+//   inner == 1 (last axis): `tpr` lanes own one row and stream it with 16-byte
+//   loads (nothing per element is written, so the row is never held in
+//   registers and any n works), then all-reduce across the group.
+//   inner > 1: one lane per (outer, inner) column loops over n; consecutive
+//   lanes read consecutive inner indices, so every access is coalesced.
+// Each input element is read once; one value (and/or index) per output is
+// written.
+//
+// Semantics (torch): mean accumulates in fp32 and divides by n
+// (ViperBench/mean_reduction/pytorch_impl.py:4-8); max returns (values, int64
+// indices) (ViperBench/max_reduction/pytorch_impl.py:4-11); argmax returns
+// int64 indices (ViperBench/argmax/pytorch_impl.py:4-8).  NaN counts as the
+// largest value and ties resolve to the smallest index, so the first maximal
+// (or first NaN) position is returned.
+#include "vbh_device.h"
+#include "vbh_launch.h"
+
+namespace vbh {
+
+namespace {
+
+constexpr float kNegInf = -__builtin_huge_valf();
+
+// true when (av, ai) should win over (bv, bi): a total order, so every lane of
+// a butterfly picks the same pair.
+__device__ __forceinline__ bool better(float av, int ai, float bv, int bi) {
+  const bool an = av != av, bn = bv != bv;
+  if (an || bn) return an && (!bn || ai < bi);
+  return av > bv || (av == bv && ai < bi);
+}
+
+struct ValIdx {
+  float v;
+  int i;
+};
+
+__device__ __forceinline__ ValIdx pick(ValIdx a, ValIdx b) {
+  return better(a.v, a.i, b.v, b.i) ? a : b;
+}
+
+template <int Ctrl>
+__device__ __forceinline__ ValIdx dpp_vi(ValIdx a) {
+  return ValIdx{dpp<Ctrl>(a.v),
+                __builtin_amdgcn_update_dpp(0, a.i, Ctrl, 0xF, 0xF, false)};
+}
+
+__device__ __forceinline__ int swap16_partner_i(int v) {
+  auto p = __builtin_amdgcn_permlane16_swap(static_cast<unsigned>(v), static_cast<unsigned>(v),
+                                            false, false);
+  return static_cast<int>((threadIdx.x & 16) ? p[0] : p[1]);
+}
+__device__ __forceinline__ int swap32_partner_i(int v) {
+  auto p = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(v), static_cast<unsigned>(v),
+                                            false, false);
+  return static_cast<int>((threadIdx.x & 32) ? p[0] : p[1]);
+}
+
+// All-reduce of (value, index) pairs over the tpr lanes of one row (see
+// group_allreduce for the lane layout and the LDS contract; `lds` holds
+// 2 * kMaxWaves words).
+__device__ __forceinline__ ValIdx group_allreduce_vi(ValIdx a, int tpr, float* lds) {
+  const int width = tpr < kWave ? tpr : kWave;
+  if (width >= 2) a = pick(a, dpp_vi<0xB1>(a));
+  if (width >= 4) a = pick(a, dpp_vi<0x4E>(a));
+  if (width >= 8) a = pick(a, dpp_vi<0x141>(a));
+  if (width >= 16) a = pick(a, dpp_vi<0x140>(a));
+  if (width >= 32) a = pick(a, ValIdx{swap16_partner(a.v), swap16_partner_i(a.i)});
+  if (width >= 64) a = pick(a, ValIdx{swap32_partner(a.v), swap32_partner_i(a.i)});
+  if (tpr <= kWave) return a;
+  const int wave = threadIdx.x / kWave;
+  const int nwaves = tpr / kWave;
+  const int first = (wave / nwaves) * nwaves;
+  int* ldsi = reinterpret_cast<int*>(lds + kMaxWaves);
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    lds[wave] = a.v;
+    ldsi[wave] = a.i;
+  }
+  __syncthreads();
+  ValIdx r{lds[first], ldsi[first]};
+  for (int w = first + 1; w < first + nwaves; ++w) r = pick(r, ValIdx{lds[w], ldsi[w]});
+  return r;
+}
+
+template <typename T, int V, int OP>
+__device__ __forceinline__ void write_result(void* vals, int64_t* idx, int64_t o, float sum_or_v,
+                                             int i, int n) {
+  if constexpr (OP == 0) {
+    const float m = sum_or_v / static_cast<float>(n);
+    store_from_f32<T, 1>(static_cast<T*>(vals) + o, &m);
+  } else {
+    if constexpr (OP == 1) store_from_f32<T, 1>(static_cast<T*>(vals) + o, &sum_or_v);
+    idx[o] = i;
+  }
+}
+
+// OP: 0 = mean (To = output type), 1 = max values + indices, 2 = argmax
+template <typename Ti, typename To, int V, int OP>
+__global__ __launch_bounds__(kMaxBlock) void reduce_rows(const Ti* __restrict__ x,
+                                                         void* __restrict__ vals,
+                                                         int64_t* __restrict__ idx,
+                                                         int64_t rows, int n, int tpr) {
+  __shared__ float lds[2 * kMaxWaves];
+  const int nvec = n / V;
+  const int g = threadIdx.x % tpr;
+  int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / tpr) + threadIdx.x / tpr;
+  const bool live = row < rows;
+  if (!live) row = rows - 1;
+  const Ti* xr = x + row * n;
+  if constexpr (OP == 0) {
+    float acc[V];
+#pragma unroll
+    for (int k = 0; k < V; ++k) acc[k] = 0.f;
+#pragma unroll 4
+    for (int j = g; j < nvec; j += tpr) {
+      const auto r = load_raw<Ti, V, true>(xr + static_cast<int64_t>(j) * V);
+#pragma unroll
+      for (int k = 0; k < V; ++k) acc[k] += raw_at<Ti, V>(r, k);
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < V; ++k) s += acc[k];
+    s = group_allreduce<Sum>(s, tpr, lds);
+    if (live && g == 0) write_result<To, V, OP>(vals, idx, row, s, 0, n);
+  } else {
+    ValIdx best{kNegInf, n};  // an empty lane loses to any element
+#pragma unroll 4
+    for (int j = g; j < nvec; j += tpr) {
+      const auto r = load_raw<Ti, V, true>(xr + static_cast<int64_t>(j) * V);
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        const float v = raw_at<Ti, V>(r, k);
+        const int i = j * V + k;
+        if (better(v, i, best.v, best.i)) best = ValIdx{v, i};
+      }
+    }
+    best = group_allreduce_vi(best, tpr, lds);
+    if (live && g == 0) write_result<To, V, OP>(vals, idx, row, best.v, best.i, n);
+  }
+}
+
+template <typename Ti, typename To, int OP>
+__global__ __launch_bounds__(256) void reduce_cols(const Ti* __restrict__ x,
+                                                   void* __restrict__ vals,
+                                                   int64_t* __restrict__ idx, int64_t outer,
+                                                   int n, int64_t inner) {
+  const int64_t col = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (col >= outer * inner) return;
+  const int64_t o = col / inner;
+  const int64_t c = col - o * inner;
+  const Ti* xc = x + o * n * inner + c;
+  if constexpr (OP == 0) {
+    float s = 0.f;
+    for (int r = 0; r < n; ++r) s += static_cast<float>(xc[r * inner]);
+    write_result<To, 1, OP>(vals, idx, col, s, 0, n);
+  } else {
+    ValIdx best{kNegInf, n};
+    for (int r = 0; r < n; ++r) {
+      const float v = static_cast<float>(xc[r * inner]);
+      if (better(v, r, best.v, best.i)) best = ValIdx{v, r};
+    }
+    write_result<To, 1, OP>(vals, idx, col, best.v, best.i, n);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_reduce(const void* x, void* vals, int64_t* idx, int64_t outer, int n,
+                         int64_t inner, int idt, int odt, int op, const Geometry& g,
+                         hipStream_t s) {
+  hipError_t err = hipErrorInvalidValue;
+  auto body = [&](auto ti, auto to) {
+    using Ti = typename decltype(ti)::type;
+    using To = typename decltype(to)::type;
+    constexpr int VN = Vec<Ti>::n;
+    auto go = [&](auto opc) {
+      constexpr int OP = decltype(opc)::value;
+      if (inner == 1) {
+        auto launch = [&](auto kern) {
+          hipLaunchKernelGGL(kern, dim3(grid_for(outer, g)), dim3(g.block), 0, s,
+                             static_cast<const Ti*>(x), vals, idx, outer, n, g.tpr);
+        };
+        if (g.v == 1) launch(reduce_rows<Ti, To, 1, OP>);
+        else launch(reduce_rows<Ti, To, VN, OP>);
+      } else {
+        const int64_t cols = outer * inner;
+        hipLaunchKernelGGL((reduce_cols<Ti, To, OP>), dim3((cols + 255) / 256), dim3(256), 0, s,
+                           static_cast<const Ti*>(x), vals, idx, outer, n, inner);
+      }
+      err = hipGetLastError();
+    };
+    if (op == 0) go(std::integral_constant<int, 0>{});
+    else if (op == 1) go(std::integral_constant<int, 1>{});
+    else go(std::integral_constant<int, 2>{});
+  };
+  if (idt == odt) {
+    dispatch_float_type(idt, [&](auto t) { body(t, t); });
+  } else if (op == 0 && odt == kF32 && (idt == kF16 || idt == kBF16)) {
+    dispatch_float_type(idt, [&](auto t) { body(t, TypeTag<float>{}); });
+  }
+  return err;
+}
+
+}  // namespace vbh

@@ -168,6 +168,10 @@ struct CeBwdArgs {
 };
 hipError_t launch_cross_entropy_bwd(const CeBwdArgs& a, hipStream_t s);
 
+hipError_t launch_reduce(const void* x, void* vals, int64_t* idx, int64_t outer, int n,
+                         int64_t inner, int idt, int odt, int op, const Geometry& g,
+                         hipStream_t s);
+
 hipError_t launch_stream_copy(const void* src, void* dst, int64_t bytes, hipStream_t s);
 
 }  // namespace vbh

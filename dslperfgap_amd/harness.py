@@ -72,6 +72,34 @@ def essential_work(kernel: str, inputs) -> int:
     raise KeyError(kernel)
 
 
+def library_fn(kernel: str):
+    """torch's own GPU implementation of a kernel: the library row that E_lib
+    (t_library / t_backend, experiments/_harness.py:142-146) is measured against.
+    layer_norm / softmax / log_softmax / logsumexp are the ATen calls the goldens
+    make; rms_norm is the golden's eager formula (rms_norm/pytorch_impl.py:8-10);
+    cross_entropy is torch's fused F.cross_entropy (per-row losses), the library
+    form of the same computation for one column block."""
+    import torch.nn.functional as F
+
+    if kernel == "layer_norm":
+        return lambda x, w, b, eps=1e-5: F.layer_norm(x, tuple(w.shape), w, b, eps)
+    if kernel == "rms_norm":
+        def rms(x, normalized_shape, w, eps=1e-5):
+            dims = tuple(range(x.ndim - len(normalized_shape), x.ndim))
+            r = torch.sqrt(torch.mean(x.float() ** 2, dim=dims, keepdim=True) + eps)
+            return ((x.float() / r) * w.float()).to(x.dtype)
+        return rms
+    if kernel == "softmax":
+        return lambda x: F.softmax(x, dim=-1)
+    if kernel == "log_softmax":
+        return lambda x, dim=-1, dtype=None: F.log_softmax(x, dim=dim, dtype=dtype)
+    if kernel == "logsumexp":
+        return lambda x: torch.logsumexp(x, dim=-1)
+    if kernel == "cross_entropy":
+        return lambda logits, labels, *a: F.cross_entropy(logits, labels, reduction="none")
+    raise KeyError(kernel)
+
+
 def profile_fn(fn, args, warmup: int = 10, iters: int = 100) -> float:
     """Median wall-clock ms of fn(*args), synchronizing around every call."""
     for _ in range(warmup):

@@ -65,7 +65,7 @@ def cross_entropy_fwd(
     lse = torch.empty((n_rows, n_cols), dtype=torch.float32, device=logits.device)
     z_loss = torch.empty((n_rows, n_cols), dtype=torch.float32, device=logits.device)
     row_stride = logits.stride(0) if n_rows > 1 else n_cols
-    with torch.cuda.device(dev):
+    with _bridge.device_guard(dev):
         _lib.call("vbh_cross_entropy_fwd", _bridge.ptr(logits), _bridge.ptr(labels), dt,
                   _bridge.LABEL_CODES[labels.dtype], _bridge.ptr(loss), _bridge.ptr(lse),
                   _bridge.ptr(z_loss), n_rows, n_cols, row_stride, float(smoothing),
@@ -95,7 +95,7 @@ def cross_entropy_bwd(
     if lse_flat.numel() < n_rows:
         raise ValueError(f"{what}: lse has {lse_flat.numel()} elements for {n_rows} rows")
     dlogits = torch.empty((n_rows, n_cols), dtype=logits.dtype, device=logits.device)
-    with torch.cuda.device(dev):
+    with _bridge.device_guard(dev):
         _lib.call("vbh_cross_entropy_bwd", _bridge.ptr(dl), _bridge.ptr(logits),
                   _bridge.ptr(lse_flat), _bridge.ptr(labels), _bridge.ptr(dlogits), dt,
                   _bridge.LABEL_CODES[labels.dtype], n_rows, n_cols,

@@ -48,7 +48,7 @@ def layer_norm(x, weight, bias, eps=1e-5):
     b = bias.contiguous() if bias is not None else None
     y = torch.empty_like(x)
     rows = x.numel() // cols if cols else 0
-    with torch.cuda.device(dev):
+    with _bridge.device_guard(dev):
         _lib.call("vbh_layer_norm_fwd", _bridge.ptr(x), _bridge.ptr(w), _bridge.ptr(b),
                   _bridge.ptr(y), rows, cols, float(eps), dt, wdt, _bridge.stream(dev))
     return y

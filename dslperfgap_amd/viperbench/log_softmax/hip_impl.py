@@ -43,7 +43,7 @@ def log_softmax(x, dim=-1, dtype=None):
     x = x.contiguous()
     y = torch.empty(x.shape, dtype=out_dtype, device=x.device)
     shape = list(x.shape) if x.dim() > 0 else [1]
-    with torch.cuda.device(dev):
+    with _bridge.device_guard(dev):
         if d == ndim - 1:
             cols = shape[-1]
             rows = x.numel() // cols if cols else 0

@@ -31,7 +31,7 @@ def logsumexp(x):
     cols = x.shape[-1]
     rows = _bridge.numel_prod(out_shape)
     y = torch.empty(out_shape, dtype=x.dtype, device=x.device)
-    with torch.cuda.device(dev):
+    with _bridge.device_guard(dev):
         _lib.call("vbh_logsumexp_fwd", _bridge.ptr(x), _bridge.ptr(y), rows, cols, dt, dt,
                   _bridge.stream(dev))
     return y

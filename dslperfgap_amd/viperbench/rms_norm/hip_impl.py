@@ -38,7 +38,7 @@ def rms_norm(x, normalized_shape, weight, eps=1e-5):
     x = x.contiguous()
     y = torch.empty_like(x)
     rows = x.numel() // cols if cols else 0
-    with torch.cuda.device(dev):
+    with _bridge.device_guard(dev):
         _lib.call("vbh_rms_norm_fwd", _bridge.ptr(x), _bridge.ptr(w), _bridge.ptr(y), rows, cols,
                   float(eps), dt, wdt, _bridge.stream(dev))
     return y

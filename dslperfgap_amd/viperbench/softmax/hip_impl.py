@@ -25,7 +25,7 @@ def softmax(x):
     y = torch.empty_like(x)
     cols = x.shape[-1] if x.dim() > 0 else 1
     rows = x.numel() // cols if cols else 0
-    with torch.cuda.device(dev):
+    with _bridge.device_guard(dev):
         _lib.call("vbh_softmax_fwd", _bridge.ptr(x), _bridge.ptr(y), rows, cols, dt, dt, 0,
                   _bridge.stream(dev))
     return y

@@ -112,3 +112,90 @@ HEADLINE = "C2_rms_norm"
 
 def to_device(args: tuple, device) -> tuple:
     return tuple(a.to(device) if isinstance(a, torch.Tensor) else a for a in args)
+
+
+# ---------------------------------------------------------------------------
+# The reference benchmark's own cases for this family ("small" and "large" per
+# kernel, ViperBench/benchmark.py:143-154, 187-198, 232-249, 314-335), with
+# the same shapes, dtypes and arguments.  The reference draws them with
+# unseeded torch.randn on the GPU; here they come from a seeded CPU generator.
+# ---------------------------------------------------------------------------
+@dataclass
+class RefCase:
+    kernel: str
+    size: str                 # "small" / "large"
+    fn: str
+    desc: str                 # the reference's input_desc column
+    make: Callable[[], tuple]
+    is_slow: bool             # the reference's MEASURE_ITERS_SLOW flag
+
+    @property
+    def key(self) -> str:
+        return f"{self.kernel}/{self.size}"
+
+
+def _ref_gen(kernel: str, size: str) -> torch.Generator:
+    return torch.Generator().manual_seed(2000 + 2 * KERNELS.index(kernel) + (size == "large"))
+
+
+def _ce_case(rows, cols, bs, size):
+    def make():
+        g = _ref_gen("cross_entropy", size)
+        logits = torch.randn(rows, cols, generator=g)
+        labels = torch.randint(0, cols, (rows,), generator=g, dtype=torch.int64)
+        return (logits, labels, 0.0, 1.0, 0.0, -100, cols, 0, bs, False, False)
+    return make
+
+
+def _ln_case(rows, cols, size):
+    def make():
+        g = _ref_gen("layer_norm", size)
+        x = torch.randn(rows, cols, generator=g).to(torch.bfloat16)
+        w = torch.randn(cols, generator=g).to(torch.bfloat16)
+        b = torch.randn(cols, generator=g).to(torch.bfloat16)
+        return (x, w, b)
+    return make
+
+
+def _rms_case(rows, cols, size):
+    def make():
+        g = _ref_gen("rms_norm", size)
+        x = torch.randn(rows, cols, generator=g).to(torch.float16)
+        w = torch.randn(cols, generator=g).to(torch.float16)
+        return (x, (cols,), w)
+    return make
+
+
+def _x_case(kernel, rows, cols, dtype, size):
+    def make():
+        g = _ref_gen(kernel, size)
+        return (torch.randn(rows, cols, generator=g).to(dtype),)
+    return make
+
+
+REFERENCE_CASES = [
+    RefCase("cross_entropy", "small", "cross_entropy_fwd", "logits:(256,1024) fp32",
+            _ce_case(256, 1024, 256, "small"), True),
+    RefCase("cross_entropy", "large", "cross_entropy_fwd", "logits:(4096,32768) fp32",
+            _ce_case(4096, 32768, 1024, "large"), True),
+    RefCase("layer_norm", "small", "layer_norm", "x:(512,1024) bf16", _ln_case(512, 1024, "small"),
+            False),
+    RefCase("layer_norm", "large", "layer_norm", "x:(8192,8192) bf16",
+            _ln_case(8192, 8192, "large"), False),
+    RefCase("log_softmax", "small", "log_softmax", "x:(512,1024) fp16",
+            _x_case("log_softmax", 512, 1024, torch.float16, "small"), False),
+    RefCase("log_softmax", "large", "log_softmax", "x:(4096,32768) fp16",
+            _x_case("log_softmax", 4096, 32768, torch.float16, "large"), False),
+    RefCase("logsumexp", "small", "logsumexp", "x:(512,1024) fp32",
+            _x_case("logsumexp", 512, 1024, torch.float32, "small"), False),
+    RefCase("logsumexp", "large", "logsumexp", "x:(8192,16384) fp32",
+            _x_case("logsumexp", 8192, 16384, torch.float32, "large"), False),
+    RefCase("rms_norm", "small", "rms_norm", "x:(512,1024) w:(1024,) fp16",
+            _rms_case(512, 1024, "small"), False),
+    RefCase("rms_norm", "large", "rms_norm", "x:(8192,8192) w:(8192,) fp16",
+            _rms_case(8192, 8192, "large"), False),
+    RefCase("softmax", "small", "softmax", "x:(512,1024) fp16",
+            _x_case("softmax", 512, 1024, torch.float16, "small"), False),
+    RefCase("softmax", "large", "softmax", "x:(4096,32768) fp16",
+            _x_case("softmax", 4096, 32768, torch.float16, "large"), False),
+]

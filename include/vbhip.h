@@ -45,6 +45,12 @@ extern "C" {
 #define VBH_OP_SOFTMAX 2
 #define VBH_OP_LOGSUMEXP 3
 #define VBH_OP_CROSS_ENTROPY 4
+#define VBH_OP_REDUCE 5
+
+/* reduction codes for vbh_reduce_fwd */
+#define VBH_REDUCE_MEAN 0
+#define VBH_REDUCE_MAX 1
+#define VBH_REDUCE_ARGMAX 2
 
 int vbh_abi_version(void);
 const char* vbh_last_error(void);
@@ -126,6 +132,20 @@ int vbh_cross_entropy_bwd(const void* dloss, const void* logits, const void* lse
                           float lse_square_scale, int64_t ignored_index,
                           int64_t total_classes, int64_t class_start_idx,
                           int has_smoothing, void* stream);
+
+/* Mean, max or argmax over the middle axis of a contiguous [outer, n, inner]
+ * tensor x of `in_dtype` (inner == 1 is the last axis).
+ *   VBH_REDUCE_MEAN:   values[outer * inner] of `out_dtype` (in_dtype, or F32
+ *                      for F16/BF16 input) = fp32 sum / n; indices unused.
+ *   VBH_REDUCE_MAX:    values (in_dtype) and int64 indices of the maximum.
+ *   VBH_REDUCE_ARGMAX: int64 indices only; values unused.
+ * NaN counts as the largest value; ties give the smallest index.  n == 0 is
+ * allowed for the mean only (every output is 0/0 = NaN, as torch.mean gives).
+ * Replaces: ViperBench/mean_reduction/pytorch_impl.py:4-8 (torch.mean),
+ *           ViperBench/max_reduction/pytorch_impl.py:4-11 (torch.max with dim),
+ *           ViperBench/argmax/pytorch_impl.py:4-8 (torch.argmax). */
+int vbh_reduce_fwd(const void* x, void* values, void* indices, int64_t outer, int64_t n,
+                   int64_t inner, int in_dtype, int out_dtype, int op, void* stream);
 
 /* Device-to-device stream copy of `bytes` (16-byte aligned pointers and size),
  * the kernel whose sustained rate is the measured HBM peak.

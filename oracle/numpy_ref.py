@@ -71,3 +71,24 @@ def cross_entropy_rows(logits, labels, smoothing=0.0, ignored_index=-100):
     xy = x[np.arange(x.shape[0]), safe]
     loss = (1 - smoothing) * (lse - xy) + smoothing * (lse - x.mean(axis=1))
     return np.where(lab == ignored_index, 0.0, loss)
+
+
+def mean(x, axes, keepdims=False):
+    """ViperBench/mean_reduction/pytorch_impl.py:8 in float64."""
+    return np.asarray(x, np.float64).mean(axis=tuple(np.atleast_1d(axes)), keepdims=keepdims)
+
+
+def max_argmax(x, axis, keepdims=False):
+    """ViperBench/max_reduction/pytorch_impl.py:10 and argmax/pytorch_impl.py:8: the first
+    position of the maximum along `axis`, where NaN counts as the largest value."""
+    x = np.asarray(x, np.float64)
+    nan = np.isnan(x)
+    # slices holding a NaN: the first NaN; others: numpy's first-occurrence argmax
+    key = np.where(nan.any(axis=axis, keepdims=True), nan.astype(np.float64), x)
+    idx = np.argmax(key, axis=axis)
+    vals = np.take_along_axis(x, np.expand_dims(idx, axis), axis=axis)
+    if not keepdims:
+        vals = np.squeeze(vals, axis=axis)
+    else:
+        idx = np.expand_dims(idx, axis)
+    return vals, idx

@@ -1,0 +1,150 @@
+"""GPU parity of the sibling row reductions (mean / max / argmax).
+
+The HIP path is compared with the oracle (oracle/pytorch_impl.py) on the same
+seeded inputs: means with allclose at the reference's loose fp32 tolerance
+(ViperBench/test_utils.py:12-25, x2), max values and all indices exactly
+(ViperBench/argmax/test.py:38-42 compares indices with torch.equal).
+"""
+import pytest
+import torch
+
+from dslperfgap_amd import _lib
+from dslperfgap_amd.viperbench.argmax.hip_impl import argmax
+from dslperfgap_amd.viperbench.max_reduction.hip_impl import max_reduction
+from dslperfgap_amd.viperbench.mean_reduction.hip_impl import mean_reduction
+from oracle import pytorch_impl as ref
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+TOL = {torch.float32: 2e-5, torch.float16: 2e-3, torch.bfloat16: 2e-2}
+
+
+def _g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _same(got, want, what=""):
+    assert got.device.type == "cuda", what
+    assert got.shape == want.shape and got.dtype == want.dtype, (what, got.shape, want.shape,
+                                                                 got.dtype, want.dtype)
+    g, w = got.cpu(), want
+    if g.is_floating_point():
+        ok = torch.equal(g.isnan(), w.isnan()) and torch.equal(g[~g.isnan()], w[~w.isnan()])
+    else:
+        ok = torch.equal(g, w)
+    assert ok, f"{what}: results differ"
+
+
+def _close(got, want, what=""):
+    assert got.shape == want.shape and got.dtype == want.dtype, (what, got.shape, want.shape)
+    tol = TOL[want.dtype]
+    assert torch.allclose(got.float().cpu(), want.float(), atol=tol, rtol=tol, equal_nan=True), what
+
+
+MEAN_CASES = [((64, 128), 0, False), ((64, 128), 1, True), ((2, 3, 4, 5), [1, 2], False),
+              ((8, 16, 32), 2, False)]  # mean_reduction/test.py:12-33
+MAX_CASES = [((128, 256), 0, False), ((256, 128), 1, False), ((32, 64, 128), 2, False),
+             ((64, 256), 1, True), ((16, 32, 64), -1, False)]  # max_reduction/test.py:13-38
+ARGMAX_CASES = [((128, 256), 0, False), ((256, 128), 1, False), ((32, 64, 128), 2, False),
+                ((16, 32, 64), 1, True)]  # argmax/test.py:13-33
+
+
+@pytest.mark.parametrize("shape,dim,keep", MEAN_CASES)
+def test_mean_reference_cases(shape, dim, keep):
+    x = torch.randn(shape, generator=_g(300))
+    _close(mean_reduction(x.to(DEV), dim, keep), ref.mean_reduction(x, dim, keep))
+
+
+@pytest.mark.parametrize("shape,dim,keep", MAX_CASES)
+def test_max_reference_cases(shape, dim, keep):
+    x = torch.randn(shape, generator=_g(301))
+    v, i = max_reduction(x.to(DEV), dim, keep)
+    rv, ri = ref.max_reduction(x, dim, keep)
+    _same(v, rv, "values")
+    _same(i, ri, "indices")
+
+
+@pytest.mark.parametrize("shape,dim,keep", ARGMAX_CASES)
+def test_argmax_reference_cases(shape, dim, keep):
+    x = torch.randn(shape, generator=_g(302))
+    _same(argmax(x.to(DEV), dim, keep), ref.argmax(x, dim, keep))
+
+
+@pytest.mark.parametrize("shape,dtype", [((1024, 1024), torch.float16), ((8192, 32768), torch.float16),
+                                         ((1024, 1024), torch.float32),
+                                         ((8192, 32768), torch.float32)])
+def test_benchmark_shapes(shape, dtype):
+    """ViperBench/benchmark.py:274-291 (and argmax :89-97): dim = 1."""
+    print(f"[gpu] reductions {shape} {dtype}", flush=True)
+    x = torch.randn(shape, generator=_g(303)).to(dtype)
+    xd = x.to(DEV)
+    v, i = max_reduction(xd, 1)
+    rv, ri = ref.max_reduction(x, 1)
+    _same(v, rv, "max values")
+    _same(i, ri, "max indices")
+    _same(argmax(xd, 1), ref.argmax(x, 1), "argmax")
+    if dtype == torch.float32:
+        _close(mean_reduction(xd, 1), ref.mean_reduction(x, 1), "mean")
+
+
+@pytest.mark.parametrize("cols", [1, 7, 64, 100, 1000, 4096, 65537])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_widths_ties_and_special_values(cols, dtype):
+    g = _g(304)
+    x = torch.randint(-3, 4, (40, cols), generator=g).float()  # many ties
+    x[1, cols // 2] = float("nan")
+    x[2, :] = float("-inf")
+    x[3, cols - 1] = float("inf")
+    x[4, cols // 3] = float("nan")
+    x[4, cols - 1] = float("nan")
+    x = x.to(dtype)
+    xd = x.to(DEV)
+    v, i = max_reduction(xd, 1)
+    rv, ri = ref.max_reduction(x, 1)
+    _same(v, rv, f"values cols={cols}")
+    _same(i, ri, f"indices cols={cols}")
+    _same(argmax(xd, -1), ref.argmax(x, -1), f"argmax cols={cols}")
+    y = torch.randn(40, cols, generator=g).to(dtype)
+    _close(mean_reduction(y.to(DEV), 1), ref.mean_reduction(y, 1), f"mean cols={cols}")
+    _close(mean_reduction(y.to(DEV), 0, True), ref.mean_reduction(y, 0, True), "mean dim0")
+
+
+def test_dims_dtype_and_degenerate():
+    g = _g(305)
+    x = torch.randn(3, 4, 5, 6, generator=g)
+    xd = x.to(DEV)
+    for dims in ([0, 2], [1, 3], [0, 1, 2, 3], [3, 1], -1, None):
+        _close(mean_reduction(xd, dims, True), ref.mean_reduction(x, dims, True), f"dims={dims}")
+    xb = x.to(torch.bfloat16)
+    _close(mean_reduction(xb.to(DEV), [1, 2], False, torch.float32),
+           ref.mean_reduction(xb, [1, 2], False, torch.float32), "bf16 -> fp32")
+    _close(mean_reduction(xd, 1, False, torch.float16),
+           ref.mean_reduction(x, 1, False, torch.float16), "fp32 -> fp16 cast first")
+    e = torch.empty(4, 0)
+    _close(mean_reduction(e.to(DEV), 1), ref.mean_reduction(e, 1), "empty axis -> NaN")
+    s = torch.tensor(1.5)
+    _same(argmax(s.to(DEV), 0), ref.argmax(s, 0), "0-d argmax")
+    _same(argmax(x.to(DEV), None), ref.argmax(x, None), "flattened argmax")
+    v, i = max_reduction(s.to(DEV), 0)
+    rv, ri = ref.max_reduction(s, 0)
+    _same(v, rv)
+    _same(i, ri)
+    base = torch.randn(40 * 1000 + 1, generator=g)
+    (bd,) = (base.to(DEV),)
+    _same(argmax(bd[1:].view(40, 1000), 1), ref.argmax(base[1:].view(40, 1000), 1), "unaligned")
+
+
+@pytest.mark.parametrize("tpr,block", [(1, 64), (16, 256), (64, 64), (192, 384), (1024, 1024)])
+def test_reduce_geometry_overrides(tpr, block):
+    x = torch.randn(33, 3001, generator=_g(306))
+    xd = x.to(DEV)
+    try:
+        _lib.tune_override(_lib.OP_REDUCE, tpr, block, 0)
+        v, i = max_reduction(xd, 1)
+        rv, ri = ref.max_reduction(x, 1)
+        _same(v, rv)
+        _same(i, ri)
+        _close(mean_reduction(xd, 1), ref.mean_reduction(x, 1))
+    finally:
+        _lib.tune_override(_lib.OP_REDUCE, 0, 0, 0)

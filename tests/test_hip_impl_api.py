@@ -24,6 +24,9 @@ FUNCS = {
     "log_softmax": ["log_softmax"],
     "logsumexp": ["logsumexp"],
     "cross_entropy": ["cross_entropy_fwd", "cross_entropy_bwd"],
+    "mean_reduction": ["mean_reduction"],
+    "max_reduction": ["max_reduction"],
+    "argmax": ["argmax"],
 }
 
 

@@ -325,3 +325,39 @@ def test_golden_fixtures_pin_oracle():
             n = rows * ncb
             for t, key in zip(got, ("loss", "lse", "z_loss")):
                 _close(t.reshape(-1)[:n], c[key][:n], 2e-5, 2e-5)
+
+
+# ---------------------------------------------------------------------------
+# sibling reductions: mean / max / argmax
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("shape,dim,keep", [((64, 128), 0, False), ((64, 128), 1, True),
+                                            ((2, 3, 4, 5), [1, 2], False), ((8, 16, 32), 2, False),
+                                            ((3, 4, 5), [0, 2], True)])
+def test_mean_reduction_vs_numpy(shape, dim, keep):
+    x = torch.randn(shape, generator=_g(20))
+    _close(ref.mean_reduction(x, dim, keep), numpy_ref.mean(x.numpy(), dim, keep), 1e-6, 1e-5)
+    # dtype casts first: a bf16 input with dtype=float32 equals the mean of its fp32 values
+    xb = x.to(torch.bfloat16)
+    _close(ref.mean_reduction(xb, dim, keep, torch.float32),
+           numpy_ref.mean(xb.float().numpy(), dim, keep), 1e-6, 1e-5)
+
+
+def test_max_argmax_semantics():
+    nan, inf = float("nan"), float("inf")
+    x = torch.tensor([[1., 3., 3., 2.], [1., nan, 5., nan], [-inf] * 4, [2., inf, inf, 0.]])
+    v, i = ref.max_reduction(x, 1)
+    # first maximal position; NaN is the largest value; an all -inf row gives index 0
+    assert i.tolist() == [1, 1, 0, 1]
+    assert v[0] == 3 and torch.isnan(v[1]) and v[2] == -inf and v[3] == inf
+    assert ref.argmax(x, 1).tolist() == [1, 1, 0, 1]
+    nv, ni = numpy_ref.max_argmax(x.numpy(), 1)
+    assert ni.tolist() == [1, 1, 0, 1]
+    g = torch.randn(16, 33, 7, generator=_g(21))
+    for d in (0, 1, 2):
+        rv, ri = ref.max_reduction(g, d, keepdim=True)
+        nv, ni = numpy_ref.max_argmax(g.numpy(), d, keepdims=True)
+        _close(rv, nv, 0, 0)
+        assert (ri.numpy() == ni).all()
+        assert (ref.argmax(g, d).numpy() == np.squeeze(ni, d)).all()
+    with pytest.raises(TypeError):
+        ref.max_reduction([1, 2], 0)
