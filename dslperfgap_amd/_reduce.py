@@ -30,13 +30,14 @@ def reduce(x: torch.Tensor, dims: list[int], keepdim: bool, op: int, out_dtype, 
     dev = _bridge.require_gpu(what, x)
     idt = _bridge.float_code(x, what)
     odt = _bridge.FLOAT_CODES[out_dtype]
-    shape = list(x.shape) if x.dim() > 0 else [1]
-    xc = x.reshape(shape)
-    if dims == list(range(dims[0], dims[-1] + 1)):
+    shape = tuple(x.shape) if x.dim() > 0 else (1,)
+    xc = x if x.dim() > 0 else x.reshape(shape)
+    if dims[-1] - dims[0] == len(dims) - 1:  # adjacent dims collapse into one axis
         outer = _bridge.numel_prod(shape[:dims[0]])
         n = _bridge.numel_prod(shape[dims[0]:dims[-1] + 1])
         inner = _bridge.numel_prod(shape[dims[-1] + 1:])
-        xc = xc.contiguous()
+        if not xc.is_contiguous():
+            xc = xc.contiguous()
     else:
         # reduced dims are not adjacent: move them last (one extra copy pass)
         keep = [d for d in range(len(shape)) if d not in dims]

@@ -109,15 +109,26 @@ __global__ __launch_bounds__(kMaxBlock) void reduce_rows(const Ti* __restrict__ 
   const bool live = row < rows;
   if (!live) row = rows - 1;
   const Ti* xr = x + row * n;
+  typedef typename Raw<Ti, V>::type RT;
+  // Each lane loads kChunk vectors (kChunk * tpr apart... j, j + tpr, ...) before
+  // processing any of them, so a chunk's loads are in flight together whatever
+  // the data-dependent branches below do.
+  constexpr int kChunk = 4;
   if constexpr (OP == 0) {
     float acc[V];
 #pragma unroll
     for (int k = 0; k < V; ++k) acc[k] = 0.f;
-#pragma unroll 4
-    for (int j = g; j < nvec; j += tpr) {
-      const auto r = load_raw<Ti, V, true>(xr + static_cast<int64_t>(j) * V);
+    for (int base = g; base < nvec; base += kChunk * tpr) {
+      RT r[kChunk];
 #pragma unroll
-      for (int k = 0; k < V; ++k) acc[k] += raw_at<Ti, V>(r, k);
+      for (int c = 0; c < kChunk; ++c) {
+        const int j = base + c * tpr;
+        r[c] = j < nvec ? load_raw<Ti, V, true>(xr + static_cast<int64_t>(j) * V) : RT{};
+      }
+#pragma unroll
+      for (int c = 0; c < kChunk; ++c)
+#pragma unroll
+        for (int k = 0; k < V; ++k) acc[k] += raw_at<Ti, V>(r[c], k);  // padding is zero
     }
     float s = 0.f;
 #pragma unroll
@@ -125,15 +136,47 @@ __global__ __launch_bounds__(kMaxBlock) void reduce_rows(const Ti* __restrict__ 
     s = group_allreduce<Sum>(s, tpr, lds);
     if (live && g == 0) write_result<To, V, OP>(vals, idx, row, s, 0, n);
   } else {
+    // A lane visits its positions in increasing order, so a later value only
+    // wins when it is strictly larger (or the first NaN).  Per 16-byte vector:
+    // an fmax tree and a NaN test; the index search runs only when the vector
+    // beats the lane's best, which is rare after the first few vectors.
     ValIdx best{kNegInf, n};  // an empty lane loses to any element
-#pragma unroll 4
-    for (int j = g; j < nvec; j += tpr) {
-      const auto r = load_raw<Ti, V, true>(xr + static_cast<int64_t>(j) * V);
+    bool done = false;        // a NaN was found: nothing later can win
+    for (int base = g; base < nvec; base += kChunk * tpr) {
+      RT r[kChunk];
 #pragma unroll
-      for (int k = 0; k < V; ++k) {
-        const float v = raw_at<Ti, V>(r, k);
-        const int i = j * V + k;
-        if (better(v, i, best.v, best.i)) best = ValIdx{v, i};
+      for (int c = 0; c < kChunk; ++c) {
+        const int j = base + c * tpr;
+        r[c] = j < nvec ? load_raw<Ti, V, true>(xr + static_cast<int64_t>(j) * V) : RT{};
+      }
+#pragma unroll
+      for (int c = 0; c < kChunk; ++c) {
+        const int j = base + c * tpr;
+        if (done || j >= nvec) continue;
+        float v[V];
+#pragma unroll
+        for (int k = 0; k < V; ++k) v[k] = raw_at<Ti, V>(r[c], k);
+        float m = v[0];
+        bool nan = v[0] != v[0];
+#pragma unroll
+        for (int k = 1; k < V; ++k) {
+          m = fmaxf(m, v[k]);
+          nan |= v[k] != v[k];
+        }
+        if (nan) {  // first NaN of the vector (unrolled selects, no indexed registers)
+          int kk = V - 1;
+#pragma unroll
+          for (int k = V - 1; k >= 0; --k)
+            if (v[k] != v[k]) kk = k;
+          best = ValIdx{__builtin_nanf(""), j * V + kk};
+          done = true;
+        } else if (m > best.v || best.i == n) {  // first position of the vector max
+          int kk = V - 1;
+#pragma unroll
+          for (int k = V - 1; k >= 0; --k)
+            if (v[k] == m) kk = k;
+          best = ValIdx{m, j * V + kk};
+        }
       }
     }
     best = group_allreduce_vi(best, tpr, lds);

@@ -69,6 +69,14 @@ def essential_work(kernel: str, inputs) -> int:
         logits, labels, bs = inputs[0], inputs[1], int(inputs[8])
         rows, cols = logits.shape
         return el(logits) + el(labels) + 3 * 4 * rows * math.ceil(cols / bs)
+    if kernel in ("argmax", "max_reduction", "mean_reduction"):
+        # read x once; outputs: int64 indices and/or one value per reduced slice
+        dim = inputs[1]
+        n = x.shape[dim] if isinstance(dim, int) else math.prod(x.shape[d] for d in dim)
+        outs = x.numel() // max(n, 1)
+        per_out = {"argmax": 8, "max_reduction": 8 + x.element_size(),
+                   "mean_reduction": x.element_size()}[kernel]
+        return el(x) + outs * per_out
     raise KeyError(kernel)
 
 
@@ -97,6 +105,13 @@ def library_fn(kernel: str):
         return lambda x: torch.logsumexp(x, dim=-1)
     if kernel == "cross_entropy":
         return lambda logits, labels, *a: F.cross_entropy(logits, labels, reduction="none")
+    if kernel == "argmax":
+        return lambda x, dim, keepdim=False: torch.argmax(x, dim=dim, keepdim=keepdim)
+    if kernel == "max_reduction":
+        return lambda x, dim, keepdim=False: torch.max(x, dim, keepdim=keepdim)
+    if kernel == "mean_reduction":
+        return lambda x, dim, keepdim=False, dtype=None: torch.mean(x, dim, keepdim=keepdim,
+                                                                    dtype=dtype)
     raise KeyError(kernel)
 
 

@@ -17,7 +17,8 @@ from typing import Callable
 
 import torch
 
-KERNELS = ("layer_norm", "rms_norm", "softmax", "log_softmax", "logsumexp", "cross_entropy")
+KERNELS = ("layer_norm", "rms_norm", "softmax", "log_softmax", "logsumexp", "cross_entropy",
+           "argmax", "max_reduction", "mean_reduction")
 
 
 @dataclass
@@ -173,6 +174,13 @@ def _x_case(kernel, rows, cols, dtype, size):
     return make
 
 
+def _red_case(kernel, rows, cols, dtype, size):
+    def make():
+        g = _ref_gen(kernel, size)
+        return (torch.randn(rows, cols, generator=g).to(dtype), 1)
+    return make
+
+
 REFERENCE_CASES = [
     RefCase("cross_entropy", "small", "cross_entropy_fwd", "logits:(256,1024) fp32",
             _ce_case(256, 1024, 256, "small"), True),
@@ -198,4 +206,17 @@ REFERENCE_CASES = [
             _x_case("softmax", 512, 1024, torch.float16, "small"), False),
     RefCase("softmax", "large", "softmax", "x:(4096,32768) fp16",
             _x_case("softmax", 4096, 32768, torch.float16, "large"), False),
+    # sibling row reductions (benchmark.py:89-97, 274-291)
+    RefCase("argmax", "small", "argmax", "x:(1024,1024) dim=1 fp16",
+            _red_case("argmax", 1024, 1024, torch.float16, "small"), False),
+    RefCase("argmax", "large", "argmax", "x:(8192,32768) dim=1 fp16",
+            _red_case("argmax", 8192, 32768, torch.float16, "large"), False),
+    RefCase("max_reduction", "small", "max_reduction", "x:(1024,1024) dim=1 fp16",
+            _red_case("max_reduction", 1024, 1024, torch.float16, "small"), False),
+    RefCase("max_reduction", "large", "max_reduction", "x:(8192,32768) dim=1 fp16",
+            _red_case("max_reduction", 8192, 32768, torch.float16, "large"), False),
+    RefCase("mean_reduction", "small", "mean_reduction", "x:(1024,1024) dim=1 fp32",
+            _red_case("mean_reduction", 1024, 1024, torch.float32, "small"), False),
+    RefCase("mean_reduction", "large", "mean_reduction", "x:(8192,32768) dim=1 fp32",
+            _red_case("mean_reduction", 8192, 32768, torch.float32, "large"), False),
 ]
