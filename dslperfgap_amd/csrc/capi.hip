@@ -99,6 +99,40 @@ int pow2ceil(int64_t n) {
   return p;
 }
 
+// A workgroup holds whole row groups: a requested size is rounded down to a
+// multiple of tpr (and is at least tpr).  A tpr alone may come from the
+// heuristic while the size comes from vbh_tune_override.
+int fit_block(int block, int tpr) { return block < tpr ? tpr : block / tpr * tpr; }
+
+// The reduction row kernel streams its row whatever the vectors per lane, so
+// its geometry has no register cap: about kItTarget vectors per lane, with
+// more lanes per row (a power of two up to 64, then whole waves up to 1024)
+// as the row grows.  Rows of more than 2048 vectors take 8 per lane: a
+// 1024-lane group with 4 (a single batch of loads per lane) streamed fp16 rows
+// of 4096 vectors at 4.8 TB/s on MI355X, 512 lanes x 8 at 6.5 TB/s.
+Geometry reduce_geometry(int64_t n, int vec) {
+  Geometry g;
+  g.v = vec;
+  g.nt = true;
+  const int64_t nvec = n / vec;
+  int tpr = g_tpr[VBH_OP_REDUCE].load();
+  if (tpr <= 0) {
+    const int per_lane = nvec > 2048 ? 8 : kItTarget[VBH_OP_REDUCE];
+    const int64_t lanes = (nvec + per_lane - 1) / per_lane;
+    if (lanes <= kWave) {
+      tpr = pow2ceil(lanes < 1 ? 1 : lanes);
+    } else {
+      const int64_t waves = (lanes + kWave - 1) / kWave;
+      tpr = static_cast<int>(waves < kMaxWaves ? waves : kMaxWaves) * kWave;
+    }
+  }
+  int block = g_block[VBH_OP_REDUCE].load();
+  if (block <= 0) block = tpr < 128 ? 256 : tpr;
+  g.tpr = tpr;
+  g.block = fit_block(block, tpr);
+  return g;
+}
+
 }  // namespace
 
 int64_t resident_blocks(const void* kernel, int block) {
@@ -167,7 +201,7 @@ Geometry pick_geometry(int64_t cols, int vec, int it_target, int tpr_override,
   g.tpr = tpr;
   g.maxit = pow2ceil(it < 1 ? 1 : it);
   int block;
-  if (block_override > 0) block = block_override < tpr ? tpr : block_override;
+  if (block_override > 0) block = fit_block(block_override, tpr);
   else block = tpr < 128 ? 256 : tpr;
   g.block = block;
   g.persist = (flags & kFlagPersist) != 0 && g.maxit <= kPipeMaxIt;
@@ -429,12 +463,7 @@ int vbh_reduce_fwd(const void* x, void* values, void* indices, int64_t outer, in
   if (inner == 1) {
     const int vn = 16 / elt_size(in_dtype);
     const bool vec_ok = n % vn == 0 && aligned16(x);
-    g = geometry_for(VBH_OP_REDUCE, n, vec_ok ? vn : 1);
-    if (g.stream) {  // no per-element output: the row kernel streams any length
-      g.stream = false;
-      g.tpr = kMaxBlock;
-      g.block = kMaxBlock;
-    }
+    g = reduce_geometry(n, vec_ok ? vn : 1);
     if (int rc = check_grid(outer, g)) return rc;
   } else if ((outer * inner + 255) / 256 * 256 > kMaxWorkItems) {
     return fail(VBH_E_RANGE, "reduce: outer * inner too large");

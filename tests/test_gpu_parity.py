@@ -20,6 +20,7 @@ import pytest
 import torch
 
 from dslperfgap_amd import _lib
+from dslperfgap_amd.viperbench.argmax.hip_impl import argmax
 from dslperfgap_amd.viperbench.cross_entropy.hip_impl import cross_entropy_bwd, cross_entropy_fwd
 from dslperfgap_amd.viperbench.layer_norm.hip_impl import layer_norm
 from dslperfgap_amd.viperbench.log_softmax.hip_impl import log_softmax
@@ -325,6 +326,41 @@ def test_geometry_overrides(tpr, block, flags, cols):
         args = (0.1, 1.0, 0.01, -100, cols, 0, 1024, True, False)
         check_ce(cross_entropy_fwd(ld, lbd, *args), ref.cross_entropy_fwd(logits, labels, *args),
                  20, cols, 1024, False, what=tag)
+    finally:
+        for op in ops:
+            _lib.tune_override(op, 0, 0, 0)
+
+
+@pytest.mark.parametrize("block", [384, 960, 1024])
+def test_block_only_override_keeps_whole_row_groups(block):
+    """A workgroup size overridden without tpr: the heuristic tpr for 10000
+    columns (640 lanes fp32, 320 bf16/fp16 and 320 for the reductions) does not
+    divide 1024 or 960, so the size is rounded down to whole row groups (and up
+    to one group for 384)."""
+    g = _g(111)
+    cols = 10000
+    x = torch.randn(30, cols, generator=g)
+    w, b = torch.randn(cols, generator=g), torch.randn(cols, generator=g)
+    xb, wb = x.to(torch.bfloat16), w.to(torch.bfloat16)
+    logits = torch.randn(12, cols, generator=g)
+    labels = torch.randint(0, cols, (12,), generator=g)
+    xd, wd, bd, ld, lbd, xbd, wbd = cuda(x, w, b, logits, labels, xb, wb)
+    ops = [_lib.OP_LAYER_NORM, _lib.OP_RMS_NORM, _lib.OP_SOFTMAX, _lib.OP_LOGSUMEXP,
+           _lib.OP_CROSS_ENTROPY, _lib.OP_REDUCE]
+    tag = f"block={block}"
+    try:
+        for op in ops:
+            _lib.tune_override(op, 0, block, 0)
+        check(layer_norm(xd, wd, bd), ref.layer_norm(x, w, b), torch.float32, what=tag)
+        check(rms_norm(xbd, (cols,), wbd), ref.rms_norm(xb, (cols,), wb), torch.bfloat16,
+              what=tag)
+        check(softmax(xd), ref.softmax(x), torch.float32, what=tag)
+        check(logsumexp(xbd), ref.logsumexp(xb), torch.bfloat16, what=tag)
+        args = (0.0, 1.0, 0.0, -100, cols, 0, 16384, False, False)
+        check_ce(cross_entropy_fwd(ld, lbd, *args), ref.cross_entropy_fwd(logits, labels, *args),
+                 12, cols, 16384, False, what=tag)
+        assert torch.equal(argmax(xd, 1).cpu(), ref.argmax(x, 1)), tag
+        assert torch.equal(argmax(xbd, 1).cpu(), ref.argmax(xb, 1)), tag
     finally:
         for op in ops:
             _lib.tune_override(op, 0, 0, 0)
