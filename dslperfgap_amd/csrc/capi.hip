@@ -57,17 +57,28 @@ std::atomic<int> g_block[kNumOps];
 std::atomic<int> g_flags[kNumOps];
 
 // Built-in choices per op, from launch-shape sweeps on MI355X:
-//   vectors per lane before more lanes are added (pick_geometry): 2 for softmax
-//   and RMSNorm, 4 for LayerNorm (its two reductions per row favour fewer
-//   waves per row) and for the reductions that write one value per row
-//   (logsumexp, cross entropy, mean / max / argmax);
+//   vectors per lane before more lanes are added (pick_geometry): 2 for RMSNorm
+//   and fp32 softmax, 4 for 16-bit softmax (bf16 8192 columns: +8% over 2),
+//   4 for LayerNorm (its two reductions per row favour fewer waves per row) and
+//   for the reductions that write one value per row (logsumexp, cross entropy,
+//   mean / max / argmax), 8 for logsumexp and mean / max / argmax rows of more
+//   than 2048 vectors (1024 lanes x 4 -- one batch of loads per lane -- is the
+//   slow spot: fp32 16384-column logsumexp 6.1 TB/s, 512 x 8 6.9 TB/s);
 //   nontemporal row loads / stores for every op (rows are touched once);
-//   the persistent pipelined kernel for LayerNorm / RMSNorm rows that span 512
-//   or more lanes (few, wide rows: it keeps every CU streaming instead of
-//   running the grid in a handful of rounds); narrower rows run one row group
-//   per workgroup.
-constexpr int kItTarget[kNumOps] = {4, 2, 2, 4, 4, 4};
-constexpr int kPersistMinTpr = 512;
+//   the persistent pipelined kernel for LayerNorm rows that span 128 or more
+//   lanes and RMSNorm rows that span 512 or more (it keeps every CU streaming
+//   instead of running the grid in rounds: on MI355X, LayerNorm gains 3-9% at
+//   128 and 256 lanes -- bf16 4096 / 8192 and fp32 2048 / 4096 columns -- and
+//   loses 3-13% at 64 lanes); narrower rows run one row group per workgroup.
+constexpr int kItTarget[kNumOps][2] = {{4, 4}, {2, 2}, {2, 4}, {4, 4}, {4, 4}, {4, 4}};
+constexpr int64_t kLongRowVecs = 2048;
+
+// [op][0] for 4-byte (or unaligned scalar) access, [op][1] for 16-bit vectors
+int it_target(int op, int64_t nvec, int vec) {
+  if ((op == VBH_OP_LOGSUMEXP || op == VBH_OP_REDUCE) && nvec > kLongRowVecs) return 8;
+  return kItTarget[op][vec == 8 ? 1 : 0];
+}
+constexpr int kPersistMinTpr[kNumOps] = {128, 512, 0, 0, 0, 0};
 
 Geometry geometry_for(int op, int64_t cols, int vec) {
   const int over = g_flags[op].load();
@@ -77,8 +88,9 @@ Geometry geometry_for(int op, int64_t cols, int vec) {
   const bool norm = op == VBH_OP_LAYER_NORM || op == VBH_OP_RMS_NORM;
   if (norm && !(over & kFlagNoPersist)) flags |= kFlagPersist;
   Geometry g =
-      pick_geometry(cols, vec, kItTarget[op], g_tpr[op].load(), g_block[op].load(), flags);
-  if (g.persist && !(over & kFlagPersist) && g.tpr < kPersistMinTpr) g.persist = false;
+      pick_geometry(cols, vec, it_target(op, cols / vec, vec), g_tpr[op].load(),
+                    g_block[op].load(), flags);
+  if (g.persist && !(over & kFlagPersist) && g.tpr < kPersistMinTpr[op]) g.persist = false;
   return g;
 }
 
@@ -105,11 +117,10 @@ int pow2ceil(int64_t n) {
 int fit_block(int block, int tpr) { return block < tpr ? tpr : block / tpr * tpr; }
 
 // The reduction row kernel streams its row whatever the vectors per lane, so
-// its geometry has no register cap: about kItTarget vectors per lane, with
-// more lanes per row (a power of two up to 64, then whole waves up to 1024)
-// as the row grows.  Rows of more than 2048 vectors take 8 per lane: a
-// 1024-lane group with 4 (a single batch of loads per lane) streamed fp16 rows
-// of 4096 vectors at 4.8 TB/s on MI355X, 512 lanes x 8 at 6.5 TB/s.
+// its geometry has no register cap: it_target vectors per lane, with more
+// lanes per row (a power of two up to 64, then whole waves up to 1024) as the
+// row grows (fp16 rows of 4096 vectors: 1024 lanes x 4 at 4.8 TB/s, 512 x 8
+// at 6.5 TB/s).
 Geometry reduce_geometry(int64_t n, int vec) {
   Geometry g;
   g.v = vec;
@@ -117,7 +128,7 @@ Geometry reduce_geometry(int64_t n, int vec) {
   const int64_t nvec = n / vec;
   int tpr = g_tpr[VBH_OP_REDUCE].load();
   if (tpr <= 0) {
-    const int per_lane = nvec > 2048 ? 8 : kItTarget[VBH_OP_REDUCE];
+    const int per_lane = it_target(VBH_OP_REDUCE, nvec, vec);
     const int64_t lanes = (nvec + per_lane - 1) / per_lane;
     if (lanes <= kWave) {
       tpr = pow2ceil(lanes < 1 ? 1 : lanes);
