@@ -91,8 +91,12 @@ def gpu_identity() -> dict:
             "timestamp_utc": datetime.now(timezone.utc).isoformat(timespec="seconds")}
 
 
-def device_slug(name: str) -> str:
-    """Filesystem-safe GPU tag, as _harness.device_slug (experiments/_harness.py:53-57)."""
+def device_slug(name: str, arch: str = "") -> str:
+    """Filesystem-safe GPU tag, as _harness.device_slug (experiments/_harness.py:53-57).
+    Where the runtime reports only the generic "AMD Radeon Graphics" (no
+    marketing-name table on the host), the ISA name stands in for the model."""
+    if arch and "Radeon Graphics" in name:
+        name = f"AMD {arch}"
     return re.sub(r"[^A-Za-z0-9._-]+", "_", name).strip("_")
 
 
@@ -178,7 +182,7 @@ def main(argv=None) -> int:
         print(f"{kernel:<15}{dtype:<6}{t_lib:>10.4f}{t_opt:>10.4f}{row['E_lib_opt']:>10}"
               f"{row['roofline_frac_opt']:>10}{t_hbm:>10.4f}{row['roofline_frac_opt_hbm']:>10}",
               flush=True)
-    out = Path(args.out) if args.out else RESULTS / device_slug(meta["gpu_name"]) / \
+    out = Path(args.out) if args.out else RESULTS / device_slug(meta["gpu_name"], meta["sm"]) / \
         "cliff_roofline.csv"
     write_rows(out, rows, meta)
     print(f"results -> {out}", flush=True)

@@ -107,3 +107,22 @@ def test_cliff_entries_follow_kernel_configs():
     for k, shape in want.items():
         assert f"{shape[0]},{shape[1]}" in cliff_roofline.ENTRIES[k][2], k
     assert cliff_roofline.device_slug("AMD Instinct MI355X") == "AMD_Instinct_MI355X"
+    assert cliff_roofline.device_slug("AMD Radeon Graphics", "gfx950") == "AMD_gfx950"
+
+
+def test_committed_cliff_table_is_consistent():
+    """One hip row per family kernel; E_lib_opt and the roofline fraction follow
+    from the row's own times and the 8 TB/s MI355X figure."""
+    path = RESULTS / "AMD_gfx950" / "cliff_roofline.csv"
+    with open(path, newline="") as f:
+        reader = csv.DictReader(f)
+        assert reader.fieldnames[3:17] == CLIFF_COLUMNS
+        rows = list(reader)
+    assert sorted(r["kernel"] for r in rows) == sorted(cliff_roofline.ENTRIES)
+    for r in rows:
+        assert r["dsl"] == "hip" and r["sm"] == "gfx950"
+        t_lib, t_opt = float(r["t_lib_ms"]), float(r["t_opt_ms"])
+        assert float(r["E_lib_opt"]) == pytest.approx(t_lib / t_opt, rel=1e-3)
+        work = int(r["note"].split("essential bytes ")[1].split(";")[0])
+        assert float(r["roofline_frac_opt"]) == pytest.approx(work / (t_opt * 1e-3) / 8e12,
+                                                              abs=2e-4)
