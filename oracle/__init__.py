@@ -38,6 +38,11 @@ Pinning (what checks each function; see tests/test_oracle_pins.py):
                   closed form; ignored rows; class_start shift
   cross_entropy_bwd  ce_loops brute force; torch.autograd of
                   F.cross_entropy(+ z-loss term) for one block
+  mean_reduction  numpy fp64 over one and several dims, keepdim; the dtype
+                  argument casts before reducing (bf16 in, fp32 out)
+  max_reduction / argmax  hand-computed known answers (ties -> first index,
+                  NaN is the largest value, all -inf rows -> 0, +inf ties);
+                  numpy first-occurrence argmax over every dim
 The reference itself ships no golden vectors or fixtures for this path, and its
 Python was not imported or run: every function above is pinned by the checks
 listed, none is "parity unpinned".
