@@ -19,11 +19,14 @@ from dslperfgap_amd import _lib, _reduce  # noqa: E402
 def argmax(input_tensor, dim, keepdim=False):
     """Returns the indices of the maximum values across a specified dimension."""
     x = input_tensor
-    if x.numel() == 0:
-        raise IndexError("argmax(): Expected reduction dim to be specified for input.numel() == 0.")
     if dim is None:
+        if x.numel() == 0:
+            raise IndexError(
+                "argmax(): Expected reduction dim to be specified for input.numel() == 0.")
         _, idx = _reduce.reduce(x.reshape(-1), [0], False, _lib.REDUCE_ARGMAX, x.dtype, "argmax")
         return idx.reshape([1] * x.dim()) if keepdim else idx.reshape([])
     dims = _reduce.norm_dims(int(dim), x.dim(), "argmax")
+    if x.dim() > 0 and x.shape[dims[0]] == 0:  # other empty axes give an empty result
+        raise IndexError(f"argmax(): Expected reduction dim {dims[0]} to have non-zero size.")
     _, idx = _reduce.reduce(x, dims, keepdim, _lib.REDUCE_ARGMAX, x.dtype, "argmax")
     return idx

@@ -19,9 +19,11 @@ with logsumexp and cross_entropy byte models that the reference lacks
 (exp_cliff_roofline.py:263).
 
 The reference protocol reuses one input set, so a working set under the 256 MB
-Infinity Cache is partly served from it.  Two columns are appended: the median
-device time with inputs cycled through >= 2 GiB of HBM copies
-(``t_opt_hbm_ms``) and the roofline fraction from it (``roofline_frac_opt_hbm``).
+Infinity Cache is partly served from it.  Three columns are appended: the
+median device time with inputs cycled through >= 2 GiB of HBM copies
+(``t_opt_hbm_ms``), the roofline fraction from it (``roofline_frac_opt_hbm``),
+and the same achieved rate as a fraction of the stream-copy rate measured at
+the start of the run (``frac_of_measured_copy_hbm``; 4 GiB copy, read + write).
 
     python -m dslperfgap_amd.viperbench.cliff_roofline [--kernels a,b] [--out PATH]
 """
@@ -44,7 +46,8 @@ from dslperfgap_amd.workloads import to_device
 RESULTS = Path(__file__).resolve().parent / "results"
 FIELDS = ["kernel", "dsl", "dtype", "shape", "t_lib_ms", "t_naive_ms", "t_opt_ms",
           "E_lib_naive", "E_lib_opt", "cliff", "roofline_bound_type", "roofline_peak_assumed",
-          "roofline_frac_opt", "note", "t_opt_hbm_ms", "roofline_frac_opt_hbm"]
+          "roofline_frac_opt", "note", "t_opt_hbm_ms", "roofline_frac_opt_hbm",
+          "frac_of_measured_copy_hbm"]
 META = ["gpu_name", "sm", "timestamp_utc"]
 
 
@@ -118,7 +121,7 @@ def time_ref_protocol(fn, args, warmup: int = 15, reps: int = 50) -> float:
 
 
 def make_row(kernel: str, t_lib: float | None, t_opt: float, t_hbm: float | None,
-             work: int, peak: float, peak_note: str) -> dict:
+             work: int, peak: float, peak_note: str, copy_peak: float | None = None) -> dict:
     """One cliff_roofline row (times in ms, work in bytes, peak in bytes/s)."""
     _fn, dtype, shape, _make, lines = ENTRIES[kernel]
     frac = work / (t_opt * 1e-3) / peak
@@ -134,6 +137,8 @@ def make_row(kernel: str, t_lib: float | None, t_opt: float, t_hbm: float | None
         "roofline_frac_opt": round(frac, 4), "note": note,
         "t_opt_hbm_ms": round(t_hbm, 5) if t_hbm else "",
         "roofline_frac_opt_hbm": round(work / (t_hbm * 1e-3) / peak, 4) if t_hbm else "",
+        "frac_of_measured_copy_hbm":
+            round(work / (t_hbm * 1e-3) / copy_peak, 4) if t_hbm and copy_peak else "",
     }
 
 
@@ -162,9 +167,11 @@ def main(argv=None) -> int:
         print(peak_note, file=sys.stderr)
         return 2
     kernels = args.kernels.split(",") if args.kernels else list(ENTRIES)
+    copy_peak = harness.copy_peak("cuda:0")
+    print(f"measured stream-copy rate: {copy_peak / 1e9:.1f} GB/s", flush=True)
     rows = []
     print(f"{'kernel':<15}{'dtype':<6}{'t_lib':>10}{'t_opt':>10}{'E_lib_opt':>10}"
-          f"{'roof_opt':>10}{'t_hbm':>10}{'roof_hbm':>10}", flush=True)
+          f"{'roof_opt':>10}{'t_hbm':>10}{'roof_hbm':>10}{'of_copy':>9}", flush=True)
     for kernel in kernels:
         fn_name, dtype, _shape, make, _lines = ENTRIES[kernel]
         cpu_args = make()
@@ -177,10 +184,11 @@ def main(argv=None) -> int:
         del dev
         torch.cuda.empty_cache()
         t_hbm = device_time_us(hip, cpu_args, work) * 1e-3
-        row = make_row(kernel, t_lib, t_opt, t_hbm, work, peak, peak_note)
+        row = make_row(kernel, t_lib, t_opt, t_hbm, work, peak, peak_note, copy_peak)
         rows.append(row)
         print(f"{kernel:<15}{dtype:<6}{t_lib:>10.4f}{t_opt:>10.4f}{row['E_lib_opt']:>10}"
-              f"{row['roofline_frac_opt']:>10}{t_hbm:>10.4f}{row['roofline_frac_opt_hbm']:>10}",
+              f"{row['roofline_frac_opt']:>10}{t_hbm:>10.4f}{row['roofline_frac_opt_hbm']:>10}"
+              f"{row['frac_of_measured_copy_hbm']:>9}",
               flush=True)
     out = Path(args.out) if args.out else RESULTS / device_slug(meta["gpu_name"], meta["sm"]) / \
         "cliff_roofline.csv"

@@ -21,9 +21,9 @@ def max_reduction(input, dim, keepdim=False):
     """Computes max along a specified dimension, returning (values, indices)."""
     if not isinstance(input, torch.Tensor):
         raise TypeError('The input must be a torch.Tensor.')
-    if input.numel() == 0 or (input.dim() > 0 and input.shape[dim] == 0):
-        raise IndexError("max_reduction(): Expected reduction dim to have non-zero size")
     dims = _reduce.norm_dims(int(dim), input.dim(), "max_reduction")
+    if input.dim() > 0 and input.shape[dims[0]] == 0:  # other empty axes: empty result
+        raise IndexError(f"max(): Expected reduction dim {dims[0]} to have non-zero size.")
     vals, idx = _reduce.reduce(input, dims, keepdim, _lib.REDUCE_MAX, input.dtype,
                                "max_reduction")
     return (vals, idx)

@@ -123,6 +123,14 @@ def test_dims_dtype_and_degenerate():
            ref.mean_reduction(x, 1, False, torch.float16), "fp32 -> fp16 cast first")
     e = torch.empty(4, 0)
     _close(mean_reduction(e.to(DEV), 1), ref.mean_reduction(e, 1), "empty axis -> NaN")
+    z = torch.empty(0, 5)  # empty outer axis: empty results, no error
+    _same(argmax(z.to(DEV), 1), ref.argmax(z, 1), "empty outer argmax")
+    _same(argmax(z.to(DEV), 1, True), ref.argmax(z, 1, True), "empty outer argmax keepdim")
+    v, i = max_reduction(z.to(DEV), 1, True)
+    rv, ri = ref.max_reduction(z, 1, True)
+    _same(v, rv, "empty outer max values")
+    _same(i, ri, "empty outer max indices")
+    _close(mean_reduction(z.to(DEV), 1), ref.mean_reduction(z, 1), "empty outer mean")
     s = torch.tensor(1.5)
     _same(argmax(s.to(DEV), 0), ref.argmax(s, 0), "0-d argmax")
     _same(argmax(x.to(DEV), None), ref.argmax(x, None), "flattened argmax")

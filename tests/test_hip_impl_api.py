@@ -74,3 +74,19 @@ def test_ce_cpu_rejected():
     with pytest.raises(ValueError, match="GPU tensors"):
         mod.cross_entropy_fwd(torch.randn(4, 8), torch.zeros(4, dtype=torch.int64), 0.0, 1.0, 0.0,
                               -100, 8, 0, 8, False, False)
+
+
+def test_reductions_reject_an_empty_reduced_axis():
+    """torch.max / torch.argmax raise IndexError only when the reduced axis is
+    empty (an empty outer axis gives an empty result, tested on the GPU)."""
+    am, mx = _load("argmax"), _load("max_reduction")
+    e = torch.empty(4, 0)
+    for fn in (lambda: am.argmax(e, 1), lambda: mx.max_reduction(e, -1),
+               lambda: ref.argmax(e, 1), lambda: ref.max_reduction(e, -1)):
+        with pytest.raises(IndexError, match="non-zero size"):
+            fn()
+    for fn in (lambda: am.argmax(torch.empty(0, 3), None), lambda: ref.argmax(torch.empty(0, 3), None)):
+        with pytest.raises(IndexError, match="numel"):
+            fn()
+    with pytest.raises(IndexError, match="Dimension out of range"):
+        mx.max_reduction(torch.empty(2, 3), 2)
