@@ -2,8 +2,6 @@
 checks, raw pointers and the current HIP stream.  Nothing here computes."""
 from __future__ import annotations
 
-import contextlib
-
 import torch
 
 from . import _lib
@@ -52,11 +50,17 @@ def stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
 
-def device_guard(dev: torch.device):
-    """Make `dev` current for the launch; a no-op when it already is."""
-    if dev.index is None or dev.index == torch.cuda.current_device():
-        return contextlib.nullcontext()
-    return torch.cuda.device(dev)
+def launch(name: str, dev: torch.device, *args) -> None:
+    """Call entry point `name` with `args` followed by the handle of torch's
+    current stream on `dev` (every launching entry point takes the stream
+    last), with `dev` the current device during the call."""
+    cur = torch.cuda.current_device()
+    idx = cur if dev.index is None else dev.index
+    if idx == cur:
+        _lib.call(name, *args, stream(dev) if _raw_stream is None else _raw_stream(cur))
+        return
+    with torch.cuda.device(idx):
+        _lib.call(name, *args, stream(dev))
 
 
 def numel_prod(shape) -> int:

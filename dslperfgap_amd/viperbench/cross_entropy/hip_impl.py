@@ -27,7 +27,7 @@ if _ROOT not in sys.path:
 
 import torch  # noqa: E402
 
-from dslperfgap_amd import _bridge, _lib  # noqa: E402
+from dslperfgap_amd import _bridge  # noqa: E402
 
 
 def _labels(labels, n_rows, what):
@@ -65,13 +65,12 @@ def cross_entropy_fwd(
     lse = torch.empty((n_rows, n_cols), dtype=torch.float32, device=logits.device)
     z_loss = torch.empty((n_rows, n_cols), dtype=torch.float32, device=logits.device)
     row_stride = logits.stride(0) if n_rows > 1 else n_cols
-    with _bridge.device_guard(dev):
-        _lib.call("vbh_cross_entropy_fwd", _bridge.ptr(logits), _bridge.ptr(labels), dt,
-                  _bridge.LABEL_CODES[labels.dtype], _bridge.ptr(loss), _bridge.ptr(lse),
-                  _bridge.ptr(z_loss), n_rows, n_cols, row_stride, float(smoothing),
-                  float(logit_scale), float(lse_square_scale), int(ignored_index),
-                  int(total_classes), int(class_start_idx), int(BLOCK_SIZE),
-                  int(bool(HAS_SMOOTHING)), int(bool(SPLIT)), _bridge.stream(dev))
+    _bridge.launch("vbh_cross_entropy_fwd", dev, _bridge.ptr(logits), _bridge.ptr(labels), dt,
+                   _bridge.LABEL_CODES[labels.dtype], _bridge.ptr(loss), _bridge.ptr(lse),
+                   _bridge.ptr(z_loss), n_rows, n_cols, row_stride, float(smoothing),
+                   float(logit_scale), float(lse_square_scale), int(ignored_index),
+                   int(total_classes), int(class_start_idx), int(BLOCK_SIZE),
+                   int(bool(HAS_SMOOTHING)), int(bool(SPLIT)))
     return loss, lse, z_loss
 
 
@@ -95,13 +94,11 @@ def cross_entropy_bwd(
     if lse_flat.numel() < n_rows:
         raise ValueError(f"{what}: lse has {lse_flat.numel()} elements for {n_rows} rows")
     dlogits = torch.empty((n_rows, n_cols), dtype=logits.dtype, device=logits.device)
-    with _bridge.device_guard(dev):
-        _lib.call("vbh_cross_entropy_bwd", _bridge.ptr(dl), _bridge.ptr(logits),
-                  _bridge.ptr(lse_flat), _bridge.ptr(labels), _bridge.ptr(dlogits), dt,
-                  _bridge.LABEL_CODES[labels.dtype], n_rows, n_cols,
-                  logits.stride(0) if n_rows > 1 else n_cols, n_cols,
-                  dl.stride(0) if dl.numel() > 1 else 1, float(smoothing),
-                  float(logit_scale), float(lse_square_scale), int(ignored_index),
-                  int(total_classes), int(class_start_idx), int(bool(HAS_SMOOTHING)),
-                  _bridge.stream(dev))
+    _bridge.launch("vbh_cross_entropy_bwd", dev, _bridge.ptr(dl), _bridge.ptr(logits),
+                   _bridge.ptr(lse_flat), _bridge.ptr(labels), _bridge.ptr(dlogits), dt,
+                   _bridge.LABEL_CODES[labels.dtype], n_rows, n_cols,
+                   logits.stride(0) if n_rows > 1 else n_cols, n_cols,
+                   dl.stride(0) if dl.numel() > 1 else 1, float(smoothing),
+                   float(logit_scale), float(lse_square_scale), int(ignored_index),
+                   int(total_classes), int(class_start_idx), int(bool(HAS_SMOOTHING)))
     return dlogits

@@ -16,7 +16,7 @@ if _ROOT not in sys.path:  # loadable by file path, as ViperBench's harness load
 
 import torch  # noqa: E402
 
-from dslperfgap_amd import _bridge, _lib  # noqa: E402
+from dslperfgap_amd import _bridge  # noqa: E402
 
 
 def layer_norm(x, weight, bias, eps=1e-5):
@@ -48,7 +48,6 @@ def layer_norm(x, weight, bias, eps=1e-5):
     b = bias.contiguous() if bias is not None else None
     y = torch.empty_like(x)
     rows = x.numel() // cols if cols else 0
-    with _bridge.device_guard(dev):
-        _lib.call("vbh_layer_norm_fwd", _bridge.ptr(x), _bridge.ptr(w), _bridge.ptr(b),
-                  _bridge.ptr(y), rows, cols, float(eps), dt, wdt, _bridge.stream(dev))
+    _bridge.launch("vbh_layer_norm_fwd", dev, _bridge.ptr(x), _bridge.ptr(w), _bridge.ptr(b),
+                   _bridge.ptr(y), rows, cols, float(eps), dt, wdt)
     return y

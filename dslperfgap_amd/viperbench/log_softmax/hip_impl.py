@@ -20,7 +20,7 @@ if _ROOT not in sys.path:
 
 import torch  # noqa: E402
 
-from dslperfgap_amd import _bridge, _lib  # noqa: E402
+from dslperfgap_amd import _bridge  # noqa: E402
 
 
 def log_softmax(x, dim=-1, dtype=None):
@@ -43,15 +43,14 @@ def log_softmax(x, dim=-1, dtype=None):
     x = x.contiguous()
     y = torch.empty(x.shape, dtype=out_dtype, device=x.device)
     shape = list(x.shape) if x.dim() > 0 else [1]
-    with _bridge.device_guard(dev):
-        if d == ndim - 1:
-            cols = shape[-1]
-            rows = x.numel() // cols if cols else 0
-            _lib.call("vbh_softmax_fwd", _bridge.ptr(x), _bridge.ptr(y), rows, cols, idt, odt, 1,
-                      _bridge.stream(dev))
-        else:
-            outer = _bridge.numel_prod(shape[:d])
-            inner = _bridge.numel_prod(shape[d + 1:])
-            _lib.call("vbh_softmax_dim_fwd", _bridge.ptr(x), _bridge.ptr(y), outer, shape[d],
-                      inner, idt, odt, 1, _bridge.stream(dev))
+    if d == ndim - 1:
+        cols = shape[-1]
+        rows = x.numel() // cols if cols else 0
+        _bridge.launch("vbh_softmax_fwd", dev, _bridge.ptr(x), _bridge.ptr(y), rows, cols, idt,
+                       odt, 1)
+    else:
+        outer = _bridge.numel_prod(shape[:d])
+        inner = _bridge.numel_prod(shape[d + 1:])
+        _bridge.launch("vbh_softmax_dim_fwd", dev, _bridge.ptr(x), _bridge.ptr(y), outer,
+                       shape[d], inner, idt, odt, 1)
     return y

@@ -15,7 +15,7 @@ if _ROOT not in sys.path:
 
 import torch  # noqa: E402
 
-from dslperfgap_amd import _bridge, _lib  # noqa: E402
+from dslperfgap_amd import _bridge  # noqa: E402
 
 
 def logsumexp(x):
@@ -31,7 +31,5 @@ def logsumexp(x):
     cols = x.shape[-1]
     rows = _bridge.numel_prod(out_shape)
     y = torch.empty(out_shape, dtype=x.dtype, device=x.device)
-    with _bridge.device_guard(dev):
-        _lib.call("vbh_logsumexp_fwd", _bridge.ptr(x), _bridge.ptr(y), rows, cols, dt, dt,
-                  _bridge.stream(dev))
+    _bridge.launch("vbh_logsumexp_fwd", dev, _bridge.ptr(x), _bridge.ptr(y), rows, cols, dt, dt)
     return y

@@ -16,7 +16,7 @@ if _ROOT not in sys.path:
 
 import torch  # noqa: E402
 
-from dslperfgap_amd import _bridge, _lib  # noqa: E402
+from dslperfgap_amd import _bridge  # noqa: E402
 
 
 def rms_norm(x, normalized_shape, weight, eps=1e-5):
@@ -38,7 +38,6 @@ def rms_norm(x, normalized_shape, weight, eps=1e-5):
     x = x.contiguous()
     y = torch.empty_like(x)
     rows = x.numel() // cols if cols else 0
-    with _bridge.device_guard(dev):
-        _lib.call("vbh_rms_norm_fwd", _bridge.ptr(x), _bridge.ptr(w), _bridge.ptr(y), rows, cols,
-                  float(eps), dt, wdt, _bridge.stream(dev))
+    _bridge.launch("vbh_rms_norm_fwd", dev, _bridge.ptr(x), _bridge.ptr(w), _bridge.ptr(y), rows,
+                   cols, float(eps), dt, wdt)
     return y

@@ -14,7 +14,7 @@ if _ROOT not in sys.path:
 
 import torch  # noqa: E402
 
-from dslperfgap_amd import _bridge, _lib  # noqa: E402
+from dslperfgap_amd import _bridge  # noqa: E402
 
 
 def softmax(x):
@@ -25,7 +25,5 @@ def softmax(x):
     y = torch.empty_like(x)
     cols = x.shape[-1] if x.dim() > 0 else 1
     rows = x.numel() // cols if cols else 0
-    with _bridge.device_guard(dev):
-        _lib.call("vbh_softmax_fwd", _bridge.ptr(x), _bridge.ptr(y), rows, cols, dt, dt, 0,
-                  _bridge.stream(dev))
+    _bridge.launch("vbh_softmax_fwd", dev, _bridge.ptr(x), _bridge.ptr(y), rows, cols, dt, dt, 0)
     return y
