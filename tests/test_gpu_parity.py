@@ -331,6 +331,30 @@ def test_geometry_overrides(tpr, block, flags, cols):
             _lib.tune_override(op, 0, 0, 0)
 
 
+@pytest.mark.parametrize("rows", [7, 300, 3001])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_full_row_persistent_kernels(rows, dtype):
+    """16-bit rows whose width fills every lane (8192 columns: 1024 vectors =
+    256 lanes x 4 for LayerNorm, 512 x 2 for RMSNorm; 20480: 640 x 4) run the
+    unguarded persistent kernel.  Row counts below, near and above the resident
+    grid (last rounds partly empty), with and without bias, 16-bit and fp32
+    weights."""
+    g = _g(112)
+    for cols in (8192, 20480):
+        x = torch.randn(rows, cols, generator=g).to(dtype)
+        w32 = 1 + 0.1 * torch.randn(cols, generator=g)
+        b32 = 0.1 * torch.randn(cols, generator=g)
+        w, b = w32.to(dtype), b32.to(dtype)
+        xd, wd, bd, w32d, b32d = cuda(x, w, b, w32, b32)
+        tag = f"rows={rows} cols={cols} {dtype}"
+        check(layer_norm(xd, wd, bd), ref.layer_norm(x, w, b), dtype, what=tag)
+        check(layer_norm(xd, wd, None), ref.layer_norm(x, w, None), dtype, what=tag + " no bias")
+        check(layer_norm(xd, w32d, b32d), ref.layer_norm(x, w32, b32), dtype, what=tag + " fp32 w")
+        check(rms_norm(xd, (cols,), wd), ref.rms_norm(x, (cols,), w), dtype, what=tag)
+        check(rms_norm(xd, (cols,), w32d), ref.rms_norm(x, (cols,), w32), dtype,
+              what=tag + " fp32 w")
+
+
 @pytest.mark.parametrize("block", [384, 960, 1024])
 def test_block_only_override_keeps_whole_row_groups(block):
     """A workgroup size overridden without tpr: the heuristic tpr for 10000
