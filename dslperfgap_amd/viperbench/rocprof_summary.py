@@ -1,0 +1,330 @@
+"""Text summaries of rocprofv3 output for the HIP backend's kernels.
+
+Reads what ``rocprofv3 --kernel-trace --stats --output-format csv`` writes
+(``<prefix>_kernel_stats.csv``) and what ``rocprofv3 --pmc FETCH_SIZE`` /
+``--pmc WRITE_SIZE --output-format csv`` write (``<prefix>_counter_collection.csv``),
+maps kernel symbols to workloads, and reports per workload:
+
+* calls, average / min / max duration, achieved GB/s = algorithmic bytes /
+  average duration, and that rate over the copy kernel's rate in the same run;
+* FETCH_SIZE and WRITE_SIZE (KiB per dispatch, averaged over dispatches),
+  each scaled by what the counter reads for the 4 GiB copy kernel
+  (vbh_stream_copy: 4 GiB read and 4 GiB written per dispatch) in the same
+  run, and the ratio of that traffic to the algorithmic bytes -- one read and
+  one write of every byte shows as 1.00.
+
+Algorithmic bytes follow the essential-work rule of
+experiments/exp_cliff_roofline.py:229-263 (``harness.essential_work``, which
+adds logsumexp and cross-entropy byte models), evaluated on meta tensors.
+
+Presets:
+  configs    the five measured configs of ``bench.py --all`` (C1-C5)
+  reference  the family at the reference's large shapes (cliff_roofline.py)
+
+    python -m dslperfgap_amd.viperbench.rocprof_summary configs \\
+        --trace D/trace/all_kernel_stats.csv --fetch D/fetch/all_counter_collection.csv \\
+        --write D/write/all_counter_collection.csv --out-dir profiles
+
+    python -m dslperfgap_amd.viperbench.rocprof_summary headline \\
+        --trace D/c2trace/c2_kernel_stats.csv --bench-line D/c2_bench.jsonl --out-dir profiles
+
+``headline`` summarises the trace of bench.py's default run (C2) next to the
+line bench.py printed in the same run, whose per-launch event time the
+trace's average duration must agree with.
+"""
+from __future__ import annotations
+
+import argparse
+import collections
+import csv
+import re
+import sys
+from pathlib import Path
+
+import torch
+
+from dslperfgap_amd import harness
+from dslperfgap_amd.workloads import WORKLOADS
+
+COPY = "stream_copy_4GiB"
+COPY_BYTES = 2 * (4 << 30)         # read + written by one 4 GiB copy dispatch
+COPY_KIB_EACH_WAY = (4 << 30) // 1024
+
+# workload -> symbol patterns (demangled or mangled; rocprofv3 prints either)
+CONFIG_KERNELS = [
+    ("C1_layer_norm", r"layer_norm_rows<float, float, 4, 4, true>|layer_norm_rowsIffLi4ELi4ELb1E"),
+    ("C2_rms_norm", r"rms_norm_rowsIDF16bDF16bLi8ELi2ELb1E"),
+    ("C3_log_softmax", r"softmax_rows<float, float, 4, 2, true, true>"),
+    ("C3_softmax", r"softmax_rows<float, float, 4, 2, false, true>"),
+    ("C3_logsumexp", r"logsumexp_rows<float, float, 4, 4, true>"),
+    ("C4_cross_entropy", r"ce_fwd_rows<float, 4, 8, true>"),
+    ("C5_layer_norm", r"layer_norm_pipeIDF16bDF16bLi8ELi4ELb1E"),
+    (COPY, r"copy_kernel\("),
+]
+REFERENCE_KERNELS = [
+    ("layer_norm", r"layer_norm_pipeIDF16bDF16bLi8ELi4ELb1E"),
+    ("rms_norm", r"rms_norm_pipeIDF16_DF16_Li8ELi2ELb1E"),
+    ("softmax", r"softmax_rowsIDF16_DF16_Li8ELi4ELb0ELb1E"),
+    ("log_softmax", r"softmax_rowsIDF16_DF16_Li8ELi4ELb1ELb1E"),
+    ("logsumexp", r"logsumexp_rows<float, float, 4, 8, true>"),
+    ("cross_entropy", r"ce_fwd_rows<float, 4, 4, true>"),
+    ("argmax", r"reduce_rowsIDF16_DF16_Li8ELi2E"),
+    ("max_reduction", r"reduce_rowsIDF16_DF16_Li8ELi1E"),
+    ("mean_reduction", r"reduce_rows<float, float, 4, 0>"),
+    (COPY, r"copy_kernel\("),
+]
+
+
+def _meta(shape, dtype=torch.float32):
+    return torch.empty(shape, dtype=dtype, device="meta")
+
+
+def reference_bytes() -> dict:
+    """Essential bytes of the reference's large shapes (AKO4ALL/prepare_kernel.py
+    KERNEL_CONFIGS, as timed by cliff_roofline.py)."""
+    bf, hf = torch.bfloat16, torch.float16
+    sq, wide = (8192, 8192), (8192, 32768)
+    ew = harness.essential_work
+    return {
+        "layer_norm": ew("layer_norm", [_meta(sq, bf), _meta((8192,), bf), _meta((8192,), bf)]),
+        "rms_norm": ew("rms_norm", [_meta(sq, hf), (8192,), _meta((8192,), hf)]),
+        "softmax": ew("softmax", [_meta((4096, 32768), hf)]),
+        "log_softmax": ew("log_softmax", [_meta((4096, 32768), hf)]),
+        "logsumexp": ew("logsumexp", [_meta((8192, 16384))]),
+        "cross_entropy": ew("cross_entropy", [_meta((4096, 32768)), _meta((4096,), torch.int64),
+                                              0.0, 1.0, 0.0, -100, 32768, 0, 1024, False, False]),
+        "argmax": ew("argmax", [_meta(wide, hf), 1]),
+        "max_reduction": ew("max_reduction", [_meta(wide, hf), 1]),
+        "mean_reduction": ew("mean_reduction", [_meta(wide), 1]),
+        COPY: COPY_BYTES,
+    }
+
+
+def config_bytes() -> dict:
+    out = {k: w.bytes_per_launch for k, w in WORKLOADS.items()}
+    out[COPY] = COPY_BYTES
+    return out
+
+
+def classify(name: str, kernels) -> str | None:
+    for key, rx in kernels:
+        if re.search(rx, name):
+            return key
+    return None
+
+
+def read_stats(path, kernels) -> dict:
+    """{workload: (symbol, calls, avg_ns, min_ns, max_ns)} from a kernel_stats.csv."""
+    out = {}
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            key = classify(r["Name"], kernels)
+            if key:
+                out[key] = (r["Name"], int(r["Calls"]), float(r["AverageNs"]), float(r["MinNs"]),
+                            float(r["MaxNs"]))
+    return out
+
+
+def read_counter(path, kernels) -> dict:
+    """{workload: (mean counter value per dispatch, dispatches)} from a counter_collection.csv."""
+    acc = collections.defaultdict(list)
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            key = classify(r["Kernel_Name"], kernels)
+            if key:
+                acc[key].append(float(r["Counter_Value"]))
+    return {k: (sum(v) / len(v), len(v)) for k, v in acc.items()}
+
+
+def trace_table(stats: dict, alg: dict, order) -> list[dict]:
+    copy_rate = alg[COPY] / stats[COPY][2] if COPY in stats else None
+    rows = []
+    for key in order:
+        if key not in stats:
+            continue
+        name, calls, avg, mn, mx = stats[key]
+        gbs = alg[key] / avg
+        rows.append(dict(workload=key, kernel=name, calls=calls, avg_ns=avg, min_ns=mn,
+                         max_ns=mx, alg_bytes=alg[key], gbps=gbs,
+                         of_copy=gbs / copy_rate if copy_rate else float("nan")))
+    return rows
+
+
+def traffic_table(fetch: dict, write: dict, alg: dict, order):
+    """(rows, fetch scale, write scale); scales from the copy kernel of the same runs."""
+    fs = COPY_KIB_EACH_WAY / fetch[COPY][0]
+    ws = COPY_KIB_EACH_WAY / write[COPY][0]
+    rows = []
+    for key in order:
+        if key not in fetch or key not in write:
+            continue
+        f_kib, n = fetch[key]
+        w_kib, _ = write[key]
+        traffic = (f_kib * fs + w_kib * ws) * 1024
+        rows.append(dict(workload=key, dispatches=n, fetch_kib=f_kib, write_kib=w_kib,
+                         traffic=traffic, alg_bytes=alg[key], ratio=traffic / alg[key]))
+    return rows, fs, ws
+
+
+def format_trace(rows) -> str:
+    out = [f"{'workload':<18}{'calls':>7}{'avg_ns':>11}{'min_ns':>9}{'max_ns':>9}{'alg_bytes':>12}"
+           f"{'GB/s':>8}{'of_copy':>8}  kernel"]
+    for r in rows:
+        out.append(f"{r['workload']:<18}{r['calls']:>7}{r['avg_ns']:>11.0f}{r['min_ns']:>9.0f}"
+                   f"{r['max_ns']:>9.0f}{r['alg_bytes']:>12}{r['gbps']:>8.0f}{r['of_copy']:>8.3f}"
+                   f"  {r['kernel'][:100]}")
+    return "\n".join(out) + "\n"
+
+
+def format_traffic(rows, fs, ws, machine_lines: bool) -> str:
+    out = [f"FETCH_SIZE reads {COPY_KIB_EACH_WAY / fs:,.1f} KiB per 4 GiB copy -> fetch scale "
+           f"{fs:.4f}",
+           f"WRITE_SIZE reads {COPY_KIB_EACH_WAY / ws:,.1f} KiB per 4 GiB copy -> write scale "
+           f"{ws:.5f}",
+           "traffic = (FETCH_SIZE * fetch scale + WRITE_SIZE * write scale) * 1024 bytes", "",
+           f"{'workload':<18}{'dispatches':>11}{'FETCH_KiB':>12}{'WRITE_KiB':>12}{'traffic_B':>13}"
+           f"{'alg_B':>13}{'ratio':>8}"]
+    for r in rows:
+        out.append(f"{r['workload']:<18}{r['dispatches']:>11}{r['fetch_kib']:>12.1f}"
+                   f"{r['write_kib']:>12.1f}{r['traffic']:>13.0f}{r['alg_bytes']:>13}"
+                   f"{r['ratio']:>8.4f}")
+    if machine_lines:
+        out += ["", "Machine-readable (bench.py reads these lines):"]
+        out += [f"TRAFFIC {r['workload']} bytes_per_launch={r['traffic']:.0f} "
+                f"fetch_kib={r['fetch_kib']:.1f} write_kib={r['write_kib']:.1f}"
+                for r in rows if r["workload"] != COPY]
+    return "\n".join(out) + "\n"
+
+
+PRESETS = {
+    "configs": dict(
+        kernels=CONFIG_KERNELS, alg=config_bytes, machine=True,
+        files=("row_kernels_all_configs_trace.txt", "row_kernels_all_configs_hbm_traffic.txt"),
+        what="every measured workload (C1-C5, bench.py --all)",
+        trace_cmd="python3 -u bench.py --all --no-cpu",
+        pmc_cmd="python3 -u bench.py --all --no-cpu --steps 50",
+        source_note=("Calls include the 0.5 s warm-up, the warm-up launches and the 1000 timed\n"
+                     "launches of bench.py; every input cycles through >= 2 GiB of HBM copies.")),
+    "reference": dict(
+        kernels=REFERENCE_KERNELS, alg=reference_bytes, machine=False,
+        files=("reference_shapes_kernels_trace.txt", "reference_shapes_hbm_traffic.txt"),
+        what="the family at the reference's large shapes (AKO4ALL/prepare_kernel.py KERNEL_CONFIGS)",
+        trace_cmd="python3 -u -m dslperfgap_amd.viperbench.cliff_roofline --out RUN/cliff_traced.csv",
+        pmc_cmd=("python3 -u -m dslperfgap_amd.viperbench.cliff_roofline --reps 10 --warmup 3 "
+                 "--out RUN/cliff_COUNTER.csv"),
+        source_note=("65 calls per kernel reuse one input set (the reference protocol); the rest\n"
+                     "cycle through >= 2 GiB of HBM copies, so the averages are HBM-bound launches.")),
+}
+
+
+def _dir_prefix(path, suffix: str) -> tuple[str, str]:
+    """(output directory, -o prefix) of a rocprofv3 csv file named <prefix><suffix>."""
+    p = Path(path)
+    name = p.name
+    return str(p.parent), name[:-len(suffix)] if name.endswith(suffix) else name
+
+
+def render(preset: str, trace, fetch, write) -> tuple[str, str]:
+    """The trace summary and the traffic summary, headed by the commands that
+    wrote the input files (directories and prefixes taken from their paths)."""
+    p = PRESETS[preset]
+    kernels, alg = p["kernels"], p["alg"]()
+    order = [k for k, _ in kernels]
+    stats = read_stats(trace, kernels)
+    tr = trace_table(stats, alg, order)
+    tdir, tpre = _dir_prefix(trace, "_kernel_stats.csv")
+    run_dir = str(Path(tdir).parent)
+    cmd = p["trace_cmd"].replace("RUN", run_dir)
+    head = (f"rocprofv3 kernel trace -- {p['what']} (MI355X, gfx950)\n\n"
+            f"Command (from the repository root, after `cd /tmp && export TMPDIR=/tmp`):\n"
+            f"  rocprofv3 --kernel-trace --stats --output-format csv -d {tdir} -o {tpre} -- \\\n"
+            f"      {cmd}\n"
+            f"Summary: python -m dslperfgap_amd.viperbench.rocprof_summary {preset} ...\n\n"
+            f"{p['source_note']}\n"
+            f"achieved = algorithmic bytes / AverageNs (ns); of_copy = achieved / the 4 GiB copy\n"
+            f"kernel's rate in the same run.\n\n")
+    trace_txt = head + format_trace(tr)
+    rows, fs, ws = traffic_table(read_counter(fetch, kernels), read_counter(write, kernels), alg,
+                                 order)
+    pmc = []
+    for c, path in (("FETCH_SIZE", fetch), ("WRITE_SIZE", write)):
+        d, pre = _dir_prefix(path, "_counter_collection.csv")
+        pmc.append(f"  timeout -s KILL 400 rocprofv3 --pmc {c} --output-format csv -d {d} -o {pre} -- \\\n"
+                   f"      {p['pmc_cmd'].replace('RUN', run_dir).replace('COUNTER', c)}")
+    pmc = "\n".join(pmc)
+    head = (f"rocprofv3 HBM traffic counters -- {p['what']} (MI355X, gfx950)\n\n"
+            f"Commands (from the repository root, after `cd /tmp && export TMPDIR=/tmp`), one\n"
+            f"counter per run:\n{pmc}\n"
+            f"Summary: python -m dslperfgap_amd.viperbench.rocprof_summary {preset} ...\n\n"
+            f"Counter values are KiB per dispatch, averaged over every dispatch of the kernel,\n"
+            f"scaled by what each counter reads for the 4 GiB copy kernel of the same runs.\n\n")
+    return trace_txt, head + format_traffic(rows, fs, ws, p["machine"])
+
+
+HEADLINE_FILE = "rms_norm_rows_C2_trace.txt"
+
+
+def render_headline(trace, bench_line) -> str:
+    """C2's kernel (and the copy kernel) from the trace of `bench.py --no-cpu`,
+    with bench.py's own line from the same run."""
+    import json
+
+    tdir, tpre = _dir_prefix(trace, "_kernel_stats.csv")
+    with open(trace, newline="") as f:
+        rows = [r for r in csv.DictReader(f)
+                if re.search(r"rms_norm_rows|copy_kernel\(", r["Name"])]
+    line = json.loads(Path(bench_line).read_text().strip().splitlines()[-1])
+    alg = WORKLOADS["C2_rms_norm"].bytes_per_launch
+    out = [f"rocprofv3 kernel trace -- headline workload C2 (RMSNorm bf16 [8192, 4096], eps 1e-6)", "",
+           "Command (from the repository root, after `cd /tmp && export TMPDIR=/tmp`):",
+           f"  rocprofv3 --kernel-trace --stats --output-format csv -d {tdir} -o {tpre} -- \\",
+           "      python3 -u bench.py --no-cpu",
+           "Summary: python -m dslperfgap_amd.viperbench.rocprof_summary headline ...", "",
+           "bench.py's line in the same run reports latency_us (device events over the 1000",
+           "back-to-back timed launches / 1000); the trace average covers every dispatch of",
+           "the kernel (warm-up included).", "",
+           f"{'calls':>7}{'avg_ns':>11}{'min_ns':>9}{'max_ns':>9}{'stddev':>9}{'GB/s':>8}  kernel"]
+    for r in rows:
+        avg = float(r["AverageNs"])
+        b = alg if "rms_norm" in r["Name"] else COPY_BYTES
+        out.append(f"{int(r['Calls']):>7}{avg:>11.0f}{float(r['MinNs']):>9.0f}"
+                   f"{float(r['MaxNs']):>9.0f}{float(r['StdDev']):>9.0f}{b / avg:>8.0f}"
+                   f"  {r['Name'][:100]}")
+    out += ["", f"bench.py line of the traced run: value {line['value']} GB/s, "
+                f"latency_us {line['latency_us']}",
+            f"GB/s from the trace = {alg:,} B / avg_ns"]
+    return "\n".join(out) + "\n"
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("preset", choices=sorted(PRESETS) + ["headline"])
+    ap.add_argument("--trace", required=True, help="<prefix>_kernel_stats.csv")
+    ap.add_argument("--fetch", help="FETCH_SIZE <prefix>_counter_collection.csv")
+    ap.add_argument("--write", help="WRITE_SIZE <prefix>_counter_collection.csv")
+    ap.add_argument("--bench-line", help="headline: the JSON line bench.py printed in the run")
+    ap.add_argument("--out-dir", default=None, help="write the summaries here (else print)")
+    args = ap.parse_args(argv)
+    if args.preset == "headline":
+        if not args.bench_line:
+            ap.error("headline needs --bench-line")
+        txt = render_headline(args.trace, args.bench_line)
+        if args.out_dir:
+            Path(args.out_dir, HEADLINE_FILE).write_text(txt)
+        else:
+            sys.stdout.write(txt)
+        return 0
+    if not (args.fetch and args.write):
+        ap.error(f"{args.preset} needs --fetch and --write")
+    trace_txt, traffic_txt = render(args.preset, args.trace, args.fetch, args.write)
+    if args.out_dir:
+        names = PRESETS[args.preset]["files"]
+        Path(args.out_dir, names[0]).write_text(trace_txt)
+        Path(args.out_dir, names[1]).write_text(traffic_txt)
+    else:
+        sys.stdout.write(trace_txt + "\n" + traffic_txt)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,102 @@
+"""rocprofv3 summaries (CPU tier): the arithmetic of
+dslperfgap_amd/viperbench/rocprof_summary.py on small synthetic CSV files in
+rocprofv3's column layout, and the committed summaries that bench.py reads.
+
+* achieved GB/s = algorithmic bytes / AverageNs, of_copy against the 4 GiB copy
+  kernel of the same run;
+* traffic = (FETCH_SIZE * fetch scale + WRITE_SIZE * write scale) * 1024 with
+  the scales set by what the counters read for the copy kernel (4 GiB each way);
+* the headers name the directories and prefixes the inputs came from;
+* bench.py's roofline.traffic parser reads every config from the committed file.
+"""
+import csv
+import importlib.util
+from pathlib import Path
+
+import pytest
+
+from dslperfgap_amd.viperbench import rocprof_summary as rs
+from dslperfgap_amd.workloads import WORKLOADS
+
+ROOT = Path(__file__).resolve().parents[1]
+C2 = "_ZN3vbh12_GLOBAL__N_113rms_norm_rowsIDF16bDF16bLi8ELi2ELb1EEEvPKT_PKT0_PS2_liif"
+COPYK = "vbh::(anonymous namespace)::copy_kernel(unsigned int __vector(4) const*, unsigned int __vector(4)*, long)"
+OTHER = "void at::native::reduce_kernel<512, 1>(...)"
+
+
+def _write(path, header, rows):
+    path.parent.mkdir(parents=True, exist_ok=True)
+    with open(path, "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(header)
+        w.writerows(rows)
+    return path
+
+
+def _fixture(tmp_path):
+    stats = _write(tmp_path / "run" / "trace" / "all_kernel_stats.csv",
+                   ["Name", "Calls", "TotalDurationNs", "AverageNs", "Percentage", "MinNs", "MaxNs",
+                    "StdDev"],
+                   [[C2, 10, 240000, 24000, 1, 23000, 25000, 100],
+                    [COPYK, 2, 2600000, 1300000, 1, 1290000, 1310000, 10],
+                    [OTHER, 5, 50, 10, 0, 9, 11, 1]])
+    hdr = ["Correlation_Id", "Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"]
+    fetch = _write(tmp_path / "run" / "fetch" / "all_counter_collection.csv", hdr,
+                   [[1, 1, C2, "FETCH_SIZE", 32768.0], [2, 2, C2, "FETCH_SIZE", 32770.0],
+                    [3, 3, COPYK, "FETCH_SIZE", 2097152.0], [4, 4, OTHER, "FETCH_SIZE", 7.0]])
+    write = _write(tmp_path / "run" / "write" / "all_counter_collection.csv", hdr,
+                   [[1, 1, C2, "WRITE_SIZE", 65536.0], [2, 2, C2, "WRITE_SIZE", 65536.0],
+                    [3, 3, COPYK, "WRITE_SIZE", 4194304.0]])
+    return stats, fetch, write
+
+
+def test_trace_and_traffic_arithmetic(tmp_path):
+    stats, fetch, write = _fixture(tmp_path)
+    alg = rs.config_bytes()
+    order = [k for k, _ in rs.CONFIG_KERNELS]
+    tr = {r["workload"]: r for r in rs.trace_table(rs.read_stats(stats, rs.CONFIG_KERNELS), alg,
+                                                     order)}
+    assert set(tr) == {"C2_rms_norm", rs.COPY}
+    c2 = tr["C2_rms_norm"]
+    assert c2["gbps"] == pytest.approx(134_225_920 / 24000)
+    assert c2["of_copy"] == pytest.approx((134_225_920 / 24000) / (8 * 2**30 / 1_300_000))
+    rows, fs, ws = rs.traffic_table(rs.read_counter(fetch, rs.CONFIG_KERNELS),
+                                    rs.read_counter(write, rs.CONFIG_KERNELS), alg, order)
+    assert fs == pytest.approx(2.0) and ws == pytest.approx(1.0)  # copy reads 2 GiB / 4 GiB
+    t = {r["workload"]: r for r in rows}["C2_rms_norm"]
+    assert t["dispatches"] == 2 and t["fetch_kib"] == pytest.approx(32769.0)
+    assert t["traffic"] == pytest.approx((32769.0 * 2 + 65536.0) * 1024)
+    assert t["ratio"] == pytest.approx(t["traffic"] / 134_225_920)
+
+
+def test_rendered_headers_and_machine_lines(tmp_path):
+    stats, fetch, write = _fixture(tmp_path)
+    trace_txt, traffic_txt = rs.render("configs", stats, fetch, write)
+    assert f"-d {stats.parent} -o all -- " in trace_txt
+    assert f"--pmc FETCH_SIZE --output-format csv -d {fetch.parent} -o all" in traffic_txt
+    assert f"--pmc WRITE_SIZE --output-format csv -d {write.parent} -o all" in traffic_txt
+    line = [l for l in traffic_txt.splitlines() if l.startswith("TRAFFIC C2_rms_norm")][0]
+    assert f"bytes_per_launch={(32769.0 * 2 + 65536.0) * 1024:.0f}" in line
+    assert not any("stream_copy" in l for l in traffic_txt.splitlines() if l.startswith("TRAFFIC"))
+
+
+def test_reference_bytes_match_the_cliff_models():
+    b = rs.reference_bytes()
+    assert b["layer_norm"] == 2 * 8192 * 8192 * 2 + 2 * 8192 * 2
+    assert b["rms_norm"] == 2 * 8192 * 8192 * 2 + 8192 * 2
+    assert b["softmax"] == b["log_softmax"] == 2 * 4096 * 32768 * 2
+    assert b["logsumexp"] == 8192 * 16384 * 4 + 8192 * 4
+    assert b["cross_entropy"] == 4096 * 32768 * 4 + 4096 * 8 + 3 * 4 * 4096 * 32
+    assert b["argmax"] == 8192 * 32768 * 2 + 8192 * 8
+    assert b["max_reduction"] == 8192 * 32768 * 2 + 8192 * (8 + 2)
+    assert b["mean_reduction"] == 8192 * 32768 * 4 + 8192 * 4
+
+
+def test_bench_reads_traffic_of_every_config_from_the_committed_summary():
+    spec = importlib.util.spec_from_file_location("bench_mod", ROOT / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    for key, w in WORKLOADS.items():
+        t = bench.measured_traffic(key)
+        assert t is not None, key
+        assert 0.99 < t / w.bytes_per_launch < 1.01, (key, t)
