@@ -112,6 +112,7 @@ def call(name: str, *args) -> None:
 
 # vbh_tune_override flag bits (VBH_TUNE_*)
 TUNE_PERSIST, TUNE_NO_PERSIST, TUNE_NONTEMPORAL, TUNE_TEMPORAL = 1, 2, 4, 8
+TUNE_WRITE_THROUGH, TUNE_NO_WRITE_THROUGH = 16, 32
 
 
 def tune_override(op: int, tpr: int = 0, block: int = 0, flags: int = 0) -> None:

@@ -130,7 +130,7 @@ constexpr int pipe_cap() {
 // register-resident kernels: one row group per row
 // ---------------------------------------------------------------------------
 
-template <typename T, typename TW, int V, int IT, bool NT>
+template <typename T, typename TW, int V, int IT, int SP>
 __global__ __launch_bounds__(kMaxBlock) void layer_norm_rows(
     const T* __restrict__ x, const TW* __restrict__ w, const TW* __restrict__ b,
     T* __restrict__ y, int64_t rows, int cols, int tpr, float eps) {
@@ -139,12 +139,14 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_rows(
   __shared__ float lds[2][kMaxWaves];
   const int nvec = cols / V;
   const int g = threadIdx.x % tpr;
-  int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / tpr) + threadIdx.x / tpr;
+  const int rpb = blockDim.x / tpr;
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * rpb;
+  int64_t row = first + threadIdx.x / tpr;
   const bool live = row < rows;
   if (!live) row = rows - 1;
 
   RT xr[IT];
-  load_raw_row<T, V, IT, NT>(x + row * cols, nvec, g, tpr, xr);
+  load_raw_row<T, V, IT, SP != kStoreCached>(x + row * cols, nvec, g, tpr, xr);
   constexpr bool kEarly = kEarlyLN<TW, V, IT>;
   RW wr[kEarly ? IT : 1], br[kEarly ? IT : 1];
   if constexpr (kEarly) {
@@ -161,7 +163,9 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_rows(
   if (!live) return;
   reload_barrier<T, V, IT>(xr);
 
+  const OutWindow<T, SP> out(y + first * cols, std::min<int64_t>(rpb, rows - first) * cols);
   T* yr = y + row * cols;
+  const int yoff = static_cast<int>(row - first) * cols;
 #pragma unroll
   for (int i = 0; i < IT; ++i) {
     const int j = i * tpr + g;
@@ -179,12 +183,12 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_rows(
       for (int k = 0; k < V; ++k)
         o[k] = (raw_at<T, V>(xr[i], k) - mean) * rstd * raw_at<TW, V>(wv, k) +
                raw_at<TW, V>(bv, k);
-      store_raw<T, V, NT>(yr + static_cast<int64_t>(j) * V, o);
+      out.template store<V>(yr + static_cast<int64_t>(j) * V, yoff + j * V, o);
     }
   }
 }
 
-template <typename T, typename TW, int V, int IT, bool NT>
+template <typename T, typename TW, int V, int IT, int SP>
 __global__ __launch_bounds__(kMaxBlock) void rms_norm_rows(
     const T* __restrict__ x, const TW* __restrict__ w, T* __restrict__ y, int64_t rows,
     int cols, int tpr, float eps) {
@@ -193,12 +197,14 @@ __global__ __launch_bounds__(kMaxBlock) void rms_norm_rows(
   __shared__ float lds[kMaxWaves];
   const int nvec = cols / V;
   const int g = threadIdx.x % tpr;
-  int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / tpr) + threadIdx.x / tpr;
+  const int rpb = blockDim.x / tpr;
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * rpb;
+  int64_t row = first + threadIdx.x / tpr;
   const bool live = row < rows;
   if (!live) row = rows - 1;
 
   RT xr[IT];
-  load_raw_row<T, V, IT, NT>(x + row * cols, nvec, g, tpr, xr);
+  load_raw_row<T, V, IT, SP != kStoreCached>(x + row * cols, nvec, g, tpr, xr);
   constexpr bool kEarly = kEarlyRMS<TW, V, IT>;
   RW wr[kEarly ? IT : 1];
   if constexpr (kEarly) load_raw_row<TW, V, IT, false>(w, nvec, g, tpr, wr);
@@ -208,7 +214,9 @@ __global__ __launch_bounds__(kMaxBlock) void rms_norm_rows(
   if (!live) return;
   reload_barrier<T, V, IT>(xr);
 
+  const OutWindow<T, SP> out(y + first * cols, std::min<int64_t>(rpb, rows - first) * cols);
   T* yr = y + row * cols;
+  const int yoff = static_cast<int>(row - first) * cols;
 #pragma unroll
   for (int i = 0; i < IT; ++i) {
     const int j = i * tpr + g;
@@ -219,7 +227,7 @@ __global__ __launch_bounds__(kMaxBlock) void rms_norm_rows(
       float o[V];
 #pragma unroll
       for (int k = 0; k < V; ++k) o[k] = (raw_at<T, V>(xr[i], k) * rinv) * raw_at<TW, V>(wv, k);
-      store_raw<T, V, NT>(yr + static_cast<int64_t>(j) * V, o);
+      out.template store<V>(yr + static_cast<int64_t>(j) * V, yoff + j * V, o);
     }
   }
 }
@@ -242,7 +250,7 @@ __global__ __launch_bounds__(kMaxBlock) void rms_norm_rows(
 // row's stores included.  Unguarded, the wait can leave the stores in flight.
 // ---------------------------------------------------------------------------
 
-template <typename T, typename TW, int V, int IT, bool NT, bool FULL>
+template <typename T, typename TW, int V, int IT, int SP, bool FULL>
 __global__ __launch_bounds__(kMaxBlock) void layer_norm_pipe(
     const T* __restrict__ x, const TW* __restrict__ w, const TW* __restrict__ b,
     T* __restrict__ y, int64_t rows, int cols, int tpr, float eps) {
@@ -254,6 +262,7 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_pipe(
   const int rpb = blockDim.x / tpr;
   const int grp = threadIdx.x / tpr;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * rpb;
+  constexpr bool kNT = SP != kStoreCached;
 
   RW wr[IT], br[IT];
   load_raw_row<TW, V, IT, false, FULL>(w, nvec, g, tpr, wr);
@@ -268,20 +277,20 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_pipe(
   // load helper whose guards are all false (which schedules better for fp32
   // rows than plain register zeroing); FULL never reaches the first branch.
   if (base + grp < rows) {
-    load_raw_row<T, V, IT, NT, FULL>(x + (base + grp) * cols, nvec, g, tpr, cur);
+    load_raw_row<T, V, IT, kNT, FULL>(x + (base + grp) * cols, nvec, g, tpr, cur);
   } else {
     if constexpr (FULL) zero_row<T, V, IT>(cur);
-    else load_raw_row<T, V, IT, NT>(x, 0, g, tpr, cur);
+    else load_raw_row<T, V, IT, kNT>(x, 0, g, tpr, cur);
   }
   int par = 0;
   for (; base < rows; base += stride) {
     const int64_t row = base + grp;
     const int64_t next = row + stride;
     if (next < rows) {
-      load_raw_row<T, V, IT, NT, FULL>(x + next * cols, nvec, g, tpr, nxt);
+      load_raw_row<T, V, IT, kNT, FULL>(x + next * cols, nvec, g, tpr, nxt);
     } else {
       if constexpr (FULL) zero_row<T, V, IT>(nxt);
-      else load_raw_row<T, V, IT, NT>(x, 0, g, tpr, nxt);
+      else load_raw_row<T, V, IT, kNT>(x, 0, g, tpr, nxt);
     }
 
     const float mean = group_allreduce<Sum>(lane_sum<T, V, IT>(cur), tpr, lds[par][0]) /
@@ -292,7 +301,9 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_pipe(
     const float rstd = 1.0f / sqrtf(m2 / static_cast<float>(cols) + eps);
     reload_barrier<T, V, IT>(cur);
     if (FULL || row < rows) {
+      const OutWindow<T, SP> out(y + base * cols, std::min<int64_t>(rpb, rows - base) * cols);
       T* yr = y + row * cols;
+      const int yoff = grp * cols;
 #pragma unroll
       for (int i = 0; i < IT; ++i) {
         const int j = i * tpr + g;
@@ -302,7 +313,7 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_pipe(
           for (int k = 0; k < V; ++k)
             o[k] = (raw_at<T, V>(cur[i], k) - mean) * rstd * raw_at<TW, V>(wr[i], k) +
                    raw_at<TW, V>(br[i], k);
-          store_raw<T, V, NT>(yr + static_cast<int64_t>(j) * V, o);
+          out.template store<V>(yr + static_cast<int64_t>(j) * V, yoff + j * V, o);
         }
       }
     }
@@ -312,7 +323,7 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_pipe(
   }
 }
 
-template <typename T, typename TW, int V, int IT, bool NT, bool FULL>
+template <typename T, typename TW, int V, int IT, int SP, bool FULL>
 __global__ __launch_bounds__(kMaxBlock) void rms_norm_pipe(
     const T* __restrict__ x, const TW* __restrict__ w, T* __restrict__ y, int64_t rows,
     int cols, int tpr, float eps) {
@@ -324,6 +335,7 @@ __global__ __launch_bounds__(kMaxBlock) void rms_norm_pipe(
   const int rpb = blockDim.x / tpr;
   const int grp = threadIdx.x / tpr;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * rpb;
+  constexpr bool kNT = SP != kStoreCached;
 
   RW wr[IT];
   load_raw_row<TW, V, IT, false, FULL>(w, nvec, g, tpr, wr);
@@ -333,27 +345,29 @@ __global__ __launch_bounds__(kMaxBlock) void rms_norm_pipe(
   // load helper whose guards are all false (which schedules better for fp32
   // rows than plain register zeroing); FULL never reaches the first branch.
   if (base + grp < rows) {
-    load_raw_row<T, V, IT, NT, FULL>(x + (base + grp) * cols, nvec, g, tpr, cur);
+    load_raw_row<T, V, IT, kNT, FULL>(x + (base + grp) * cols, nvec, g, tpr, cur);
   } else {
     if constexpr (FULL) zero_row<T, V, IT>(cur);
-    else load_raw_row<T, V, IT, NT>(x, 0, g, tpr, cur);
+    else load_raw_row<T, V, IT, kNT>(x, 0, g, tpr, cur);
   }
   int par = 0;
   for (; base < rows; base += stride) {
     const int64_t row = base + grp;
     const int64_t next = row + stride;
     if (next < rows) {
-      load_raw_row<T, V, IT, NT, FULL>(x + next * cols, nvec, g, tpr, nxt);
+      load_raw_row<T, V, IT, kNT, FULL>(x + next * cols, nvec, g, tpr, nxt);
     } else {
       if constexpr (FULL) zero_row<T, V, IT>(nxt);
-      else load_raw_row<T, V, IT, NT>(x, 0, g, tpr, nxt);
+      else load_raw_row<T, V, IT, kNT>(x, 0, g, tpr, nxt);
     }
 
     const float ss = group_allreduce<Sum>(lane_sumsq<T, V, IT>(cur), tpr, lds[par]);
     const float rinv = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
     reload_barrier<T, V, IT>(cur);
     if (FULL || row < rows) {
+      const OutWindow<T, SP> out(y + base * cols, std::min<int64_t>(rpb, rows - base) * cols);
       T* yr = y + row * cols;
+      const int yoff = grp * cols;
 #pragma unroll
       for (int i = 0; i < IT; ++i) {
         const int j = i * tpr + g;
@@ -362,7 +376,7 @@ __global__ __launch_bounds__(kMaxBlock) void rms_norm_pipe(
 #pragma unroll
           for (int k = 0; k < V; ++k)
             o[k] = (raw_at<T, V>(cur[i], k) * rinv) * raw_at<TW, V>(wr[i], k);
-          store_raw<T, V, NT>(yr + static_cast<int64_t>(j) * V, o);
+          out.template store<V>(yr + static_cast<int64_t>(j) * V, yoff + j * V, o);
         }
       }
     }
@@ -471,6 +485,13 @@ bool dispatch_weight_type(int dt, int wdt, Fn&& fn) {
 template <typename T>
 constexpr bool kPipeFullType = sizeof(T) == 2;
 
+// The guarded persistent kernels (rows that do not fill every lane) keep
+// their output stores in the L2: the 16-bit LayerNorm one sits at the
+// 128-VGPR cap of a 1024-lane workgroup and the write-through addressing
+// would make it spill.
+template <int SP>
+constexpr int kGuardedPipeSP = SP == kStoreThrough ? kStoreStream : SP;
+
 template <typename T>
 bool pipe_full(const Geometry& g, int64_t nvec, int it) {
   return kPipeFullType<T> && g.v > 1 && g.block == g.tpr &&
@@ -514,24 +535,22 @@ hipError_t launch_layer_norm(const void* x, const void* w, const void* b, void* 
         dispatch_maxit(g.maxit, [&](auto mc) {
           constexpr int M = decltype(mc)::value;
           if constexpr (M <= lane_cap(V)) {
-            auto body = [&](auto nt) {
-              constexpr bool NT = decltype(nt)::value;
+            dispatch_store_policy<V>(g, [&](auto sp) {
+              constexpr int SP = decltype(sp)::value;
               constexpr int PC = pipe_cap<T, TW, V, 2>();
               constexpr int MP = M <= PC ? M : PC;
               auto pipe_k = pipe_full<T>(g, cols / V, MP)
-                                ? layer_norm_pipe<T, TW, V, MP, NT, V != 1 && kPipeFullType<T>>
-                                : layer_norm_pipe<T, TW, V, MP, NT, false>;
+                                ? layer_norm_pipe<T, TW, V, MP, SP, V != 1 && kPipeFullType<T>>
+                                : layer_norm_pipe<T, TW, V, MP, kGuardedPipeSP<SP>, false>;
               err = launch_rows_or_pipe(
-                  layer_norm_rows<T, TW, V, M, NT>, pipe_k,
+                  layer_norm_rows<T, TW, V, M, SP>, pipe_k,
                   g.persist && M <= PC, rows, g, [&](auto kern, int64_t grid) {
                     hipLaunchKernelGGL(kern, dim3(grid), dim3(g.block), 0, s,
                                        static_cast<const T*>(x), static_cast<const TW*>(w),
                                        static_cast<const TW*>(b), static_cast<T*>(y), rows,
                                        cols, g.tpr, eps);
                   });
-            };
-            if (g.nt) body(std::true_type{});
-            else body(std::false_type{});
+            });
           }
         });
       };
@@ -562,23 +581,21 @@ hipError_t launch_rms_norm(const void* x, const void* w, void* y, int64_t rows, 
         dispatch_maxit(g.maxit, [&](auto mc) {
           constexpr int M = decltype(mc)::value;
           if constexpr (M <= lane_cap(V)) {
-            auto body = [&](auto nt) {
-              constexpr bool NT = decltype(nt)::value;
+            dispatch_store_policy<V>(g, [&](auto sp) {
+              constexpr int SP = decltype(sp)::value;
               constexpr int PC = pipe_cap<T, TW, V, 1>();
               constexpr int MP = M <= PC ? M : PC;
               auto pipe_k = pipe_full<T>(g, cols / V, MP)
-                                ? rms_norm_pipe<T, TW, V, MP, NT, V != 1 && kPipeFullType<T>>
-                                : rms_norm_pipe<T, TW, V, MP, NT, false>;
+                                ? rms_norm_pipe<T, TW, V, MP, SP, V != 1 && kPipeFullType<T>>
+                                : rms_norm_pipe<T, TW, V, MP, kGuardedPipeSP<SP>, false>;
               err = launch_rows_or_pipe(
-                  rms_norm_rows<T, TW, V, M, NT>, pipe_k,
+                  rms_norm_rows<T, TW, V, M, SP>, pipe_k,
                   g.persist && M <= PC, rows, g, [&](auto kern, int64_t grid) {
                     hipLaunchKernelGGL(kern, dim3(grid), dim3(g.block), 0, s,
                                        static_cast<const T*>(x), static_cast<const TW*>(w),
                                        static_cast<T*>(y), rows, cols, g.tpr, eps);
                   });
-            };
-            if (g.nt) body(std::true_type{});
-            else body(std::false_type{});
+            });
           }
         });
       };

@@ -14,6 +14,8 @@
 // ViperBench/log_softmax/pytorch_impl.py:4-8 (F.log_softmax(x, dim, dtype)),
 // ViperBench/logsumexp/pytorch_impl.py:3-5 (torch.logsumexp, dim=-1: the max
 // used for the shift is replaced by 0 when it is infinite).
+#include <algorithm>
+
 #include "vbh_device.h"
 #include "vbh_launch.h"
 
@@ -71,7 +73,7 @@ __device__ __forceinline__ float lane_sum_exp(const typename Raw<T, V>::type (&x
   return a[0];
 }
 
-template <typename Ti, typename To, int V, int IT, bool LOG, bool NT>
+template <typename Ti, typename To, int V, int IT, bool LOG, int SP>
 __global__ __launch_bounds__(kMaxBlock) void softmax_rows(const Ti* __restrict__ x,
                                                           To* __restrict__ y, int64_t rows,
                                                           int cols, int tpr) {
@@ -79,12 +81,14 @@ __global__ __launch_bounds__(kMaxBlock) void softmax_rows(const Ti* __restrict__
   __shared__ float lds[2][kMaxWaves];
   const int nvec = cols / V;
   const int g = threadIdx.x % tpr;
-  int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / tpr) + threadIdx.x / tpr;
+  const int rpb = blockDim.x / tpr;
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * rpb;
+  int64_t row = first + threadIdx.x / tpr;
   const bool live = row < rows;
   if (!live) row = rows - 1;
 
   RT xr[IT];
-  load_raw_row<Ti, V, IT, NT>(x + row * cols, nvec, g, tpr, xr);
+  load_raw_row<Ti, V, IT, SP != kStoreCached>(x + row * cols, nvec, g, tpr, xr);
   const float m = group_allreduce<Max>(lane_max<Ti, V, IT>(xr, nvec, g, tpr), tpr, lds[0]);
   reload_barrier<Ti, V, IT>(xr);
   const float s =
@@ -92,7 +96,9 @@ __global__ __launch_bounds__(kMaxBlock) void softmax_rows(const Ti* __restrict__
   if (!live) return;
   reload_barrier<Ti, V, IT>(xr);
 
+  const OutWindow<To, SP> out(y + first * cols, std::min<int64_t>(rpb, rows - first) * cols);
   To* yr = y + row * cols;
+  const int yoff = static_cast<int>(row - first) * cols;
   const float ls = LOG ? fast_log(s) : 0.f;
   const float r = LOG ? 0.f : 1.0f / s;
 #pragma unroll
@@ -105,7 +111,7 @@ __global__ __launch_bounds__(kMaxBlock) void softmax_rows(const Ti* __restrict__
         const float d = raw_at<Ti, V>(xr[i], k) - m;
         o[k] = LOG ? d - ls : fast_exp(d) * r;
       }
-      store_raw<To, V, NT>(yr + static_cast<int64_t>(j) * V, o);
+      out.template store<V>(yr + static_cast<int64_t>(j) * V, yoff + j * V, o);
     }
   }
 }
@@ -293,14 +299,12 @@ hipError_t launch_softmax(const void* x, void* y, int64_t rows, int cols, int id
       dispatch_maxit(g.maxit, [&](auto mc) {
         constexpr int M = decltype(mc)::value;
         if constexpr (M <= lane_cap(V)) {
-          if (g.nt)
-            hipLaunchKernelGGL((softmax_rows<Ti, To, V, M, LOG, true>), dim3(grid_for(rows, g)),
+          dispatch_store_policy<V>(g, [&](auto sp) {
+            constexpr int SP = decltype(sp)::value;
+            hipLaunchKernelGGL((softmax_rows<Ti, To, V, M, LOG, SP>), dim3(grid_for(rows, g)),
                                dim3(g.block), 0, s, static_cast<const Ti*>(x),
                                static_cast<To*>(y), rows, cols, g.tpr);
-          else
-            hipLaunchKernelGGL((softmax_rows<Ti, To, V, M, LOG, false>), dim3(grid_for(rows, g)),
-                               dim3(g.block), 0, s, static_cast<const Ti*>(x),
-                               static_cast<To*>(y), rows, cols, g.tpr);
+          });
           err = hipGetLastError();
         }
       });

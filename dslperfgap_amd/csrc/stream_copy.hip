@@ -1,7 +1,9 @@
 // Device-to-device copy used to measure the sustainable HBM rate of one GPU.
 // Each 256-lane workgroup moves one contiguous 4 KiB tile (one 16-byte access
-// per lane) with nontemporal hints, so reads and writes stream through the
-// caches; the grid covers the buffer once.
+// per lane); the grid covers the buffer once.  Loads are nontemporal; stores
+// are nontemporal and written through the L2 at device scope (the row kernels'
+// kStoreThrough policy), the fastest store form measured on MI355X for a 4 GiB
+// copy: 6657 GB/s against 6467 with nontemporal stores kept in the L2.
 #include "vbh_device.h"
 #include "vbh_launch.h"
 
@@ -10,11 +12,21 @@ namespace vbh {
 namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(256) void copy_kernel(const u32x4* __restrict__ src,
                                                    u32x4* __restrict__ dst, int64_t n) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * blockDim.x;
+  const int64_t i = first + threadIdx.x;
+  // the workgroup's tile [first, first + tile) is the store window (its range
+  // check also drops any store past the end of the buffer)
+  const int64_t tile = n - first < blockDim.x ? n - first : blockDim.x;
+  const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(
+      dst + first, static_cast<short>(0), static_cast<int>(tile * sizeof(u32x4)), kRawBufferWord3);
+  if (i < n)
+    __builtin_amdgcn_raw_buffer_store_b128(
+        __builtin_bit_cast(i32x4, __builtin_nontemporal_load(src + i)), out,
+        static_cast<int>(threadIdx.x * sizeof(u32x4)), 0, kCacheNtSc1);
 }
 
 }  // namespace

@@ -9,6 +9,8 @@
 #include <type_traits>
 #include <utility>
 
+#include "vbh_device.h"
+
 namespace vbh {
 
 enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2, kI32 = 3, kI64 = 4 };
@@ -24,6 +26,8 @@ enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2, kI32 = 3, kI64 = 4 };
 //          capacity, each row group loops over rows, keeps per-column vectors
 //          (weight, bias) in registers and prefetches its next row
 //   nt     nontemporal hints on the streamed row loads / output stores
+//   wt     16-byte output stores also written through the L2 (kStoreThrough;
+//          only with nt, and only where the kernel has 16-byte output rows)
 struct Geometry {
   int v = 1;
   int tpr = 64;
@@ -32,6 +36,7 @@ struct Geometry {
   bool stream = false;
   bool persist = false;
   bool nt = false;
+  bool wt = false;
 };
 
 // vbh_tune_override flag bits
@@ -39,6 +44,9 @@ constexpr int kFlagPersist = 1;
 constexpr int kFlagNoPersist = 2;
 constexpr int kFlagNontemporal = 4;
 constexpr int kFlagTemporal = 8;
+constexpr int kFlagWriteThrough = 16;
+constexpr int kFlagNoWriteThrough = 32;
+constexpr int kFlagAll = 63;
 
 // The persistent kernels keep up to this many 16-byte vectors per lane for each
 // of: current row, next row, and every per-column vector (their register cap
@@ -96,6 +104,15 @@ bool dispatch_maxit(int maxit, Fn&& fn) {
     case 32: fn(std::integral_constant<int, 32>{}); return true;
     default: return false;
   }
+}
+
+// Store policy of a launch with V-element accesses (StorePolicy in
+// vbh_device.h): write-through needs 16-byte vector rows.
+template <int V, typename Fn>
+void dispatch_store_policy(const Geometry& g, Fn&& fn) {
+  if (!g.nt) fn(std::integral_constant<int, kStoreCached>{});
+  else if (V > 1 && g.wt) fn(std::integral_constant<int, kStoreThrough>{});
+  else fn(std::integral_constant<int, kStoreStream>{});
 }
 
 inline int64_t grid_for(int64_t rows, const Geometry& g) {

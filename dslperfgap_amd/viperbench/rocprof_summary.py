@@ -50,22 +50,24 @@ COPY = "stream_copy_4GiB"
 COPY_BYTES = 2 * (4 << 30)         # read + written by one 4 GiB copy dispatch
 COPY_KIB_EACH_WAY = (4 << 30) // 1024
 
-# workload -> symbol patterns (demangled or mangled; rocprofv3 prints either)
+# workload -> symbol patterns (demangled or mangled; rocprofv3 prints either).
+# The row kernels carry their output store policy as an int template argument
+# (0 cached, 1 nontemporal, 2 write-through), matched as any digit.
 CONFIG_KERNELS = [
-    ("C1_layer_norm", r"layer_norm_rows<float, float, 4, 4, true>|layer_norm_rowsIffLi4ELi4ELb1E"),
-    ("C2_rms_norm", r"rms_norm_rowsIDF16bDF16bLi8ELi2ELb1E"),
-    ("C3_log_softmax", r"softmax_rows<float, float, 4, 2, true, true>"),
-    ("C3_softmax", r"softmax_rows<float, float, 4, 2, false, true>"),
+    ("C1_layer_norm", r"layer_norm_rows<float, float, 4, 4, \d>|layer_norm_rowsIffLi4ELi4ELi\dE"),
+    ("C2_rms_norm", r"rms_norm_rowsIDF16bDF16bLi8ELi2ELi\dE"),
+    ("C3_log_softmax", r"softmax_rows<float, float, 4, 2, true, \d>"),
+    ("C3_softmax", r"softmax_rows<float, float, 4, 2, false, \d>"),
     ("C3_logsumexp", r"logsumexp_rows<float, float, 4, 4, true>"),
     ("C4_cross_entropy", r"ce_fwd_rows<float, 4, 8, true>"),
-    ("C5_layer_norm", r"layer_norm_pipeIDF16bDF16bLi8ELi4ELb1E"),
+    ("C5_layer_norm", r"layer_norm_pipeIDF16bDF16bLi8ELi4ELi\dELb1E"),
     (COPY, r"copy_kernel\("),
 ]
 REFERENCE_KERNELS = [
-    ("layer_norm", r"layer_norm_pipeIDF16bDF16bLi8ELi4ELb1E"),
-    ("rms_norm", r"rms_norm_pipeIDF16_DF16_Li8ELi2ELb1E"),
-    ("softmax", r"softmax_rowsIDF16_DF16_Li8ELi4ELb0ELb1E"),
-    ("log_softmax", r"softmax_rowsIDF16_DF16_Li8ELi4ELb1ELb1E"),
+    ("layer_norm", r"layer_norm_pipeIDF16bDF16bLi8ELi4ELi\dELb1E"),
+    ("rms_norm", r"rms_norm_pipeIDF16_DF16_Li8ELi2ELi\dELb1E"),
+    ("softmax", r"softmax_rowsIDF16_DF16_Li8ELi4ELb0ELi\dE"),
+    ("log_softmax", r"softmax_rowsIDF16_DF16_Li8ELi4ELb1ELi\dE"),
     ("logsumexp", r"logsumexp_rows<float, float, 4, 8, true>"),
     ("cross_entropy", r"ce_fwd_rows<float, 4, 4, true>"),
     ("argmax", r"reduce_rowsIDF16_DF16_Li8ELi2E"),

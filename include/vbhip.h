@@ -164,6 +164,9 @@ int vbh_stream_copy(const void* src, void* dst, int64_t bytes, void* stream);
 #define VBH_TUNE_NO_PERSIST 2   /* force one row group per workgroup            */
 #define VBH_TUNE_NONTEMPORAL 4  /* force nontemporal row loads / output stores  */
 #define VBH_TUNE_TEMPORAL 8     /* force plain row loads / output stores        */
+#define VBH_TUNE_WRITE_THROUGH 16    /* nontemporal 16-byte output stores also
+                                        written through the L2 (device scope) */
+#define VBH_TUNE_NO_WRITE_THROUGH 32 /* keep output stores in the L2            */
 int vbh_tune_override(int op, int tpr, int block, int flags);
 
 #ifdef __cplusplus

@@ -296,11 +296,18 @@ GEOMETRIES = [(1, 64), (4, 256), (16, 128), (64, 64), (128, 512), (192, 384), (2
               (320, 960), (512, 1024), (640, 640), (1024, 1024)]
 
 
+WT = _lib.TUNE_WRITE_THROUGH
+
+
 @pytest.mark.parametrize("flags", [0, _lib.TUNE_PERSIST | _lib.TUNE_NONTEMPORAL,
-                                   _lib.TUNE_NONTEMPORAL])
+                                   _lib.TUNE_NONTEMPORAL, _lib.TUNE_PERSIST | WT, WT,
+                                   _lib.TUNE_NO_WRITE_THROUGH])
 @pytest.mark.parametrize("tpr,block", GEOMETRIES)
-@pytest.mark.parametrize("cols", [200, 3000])
+@pytest.mark.parametrize("cols", [200, 1001, 3000])
 def test_geometry_overrides(tpr, block, flags, cols):
+    """Every group size, kernel choice and store policy gives the oracle's
+    answer; 1001 columns take the scalar (unaligned) path, where write-through
+    falls back to nontemporal stores."""
     g = _g(110)
     x = torch.randn(50, cols, generator=g)
     w, b = torch.randn(cols, generator=g), torch.randn(cols, generator=g)
@@ -331,9 +338,10 @@ def test_geometry_overrides(tpr, block, flags, cols):
             _lib.tune_override(op, 0, 0, 0)
 
 
+@pytest.mark.parametrize("flags", [0, WT, _lib.TUNE_NO_WRITE_THROUGH])
 @pytest.mark.parametrize("rows", [7, 300, 3001])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_full_row_persistent_kernels(rows, dtype):
+def test_full_row_persistent_kernels(rows, dtype, flags):
     """16-bit rows whose width fills every lane (8192 columns: 1024 vectors =
     256 lanes x 4 for LayerNorm, 512 x 2 for RMSNorm; 20480: 640 x 4) run the
     unguarded persistent kernel.  Row counts below, near and above the resident
@@ -346,13 +354,21 @@ def test_full_row_persistent_kernels(rows, dtype):
         b32 = 0.1 * torch.randn(cols, generator=g)
         w, b = w32.to(dtype), b32.to(dtype)
         xd, wd, bd, w32d, b32d = cuda(x, w, b, w32, b32)
-        tag = f"rows={rows} cols={cols} {dtype}"
-        check(layer_norm(xd, wd, bd), ref.layer_norm(x, w, b), dtype, what=tag)
-        check(layer_norm(xd, wd, None), ref.layer_norm(x, w, None), dtype, what=tag + " no bias")
-        check(layer_norm(xd, w32d, b32d), ref.layer_norm(x, w32, b32), dtype, what=tag + " fp32 w")
-        check(rms_norm(xd, (cols,), wd), ref.rms_norm(x, (cols,), w), dtype, what=tag)
-        check(rms_norm(xd, (cols,), w32d), ref.rms_norm(x, (cols,), w32), dtype,
-              what=tag + " fp32 w")
+        tag = f"rows={rows} cols={cols} {dtype} flags={flags}"
+        try:
+            for op in (_lib.OP_LAYER_NORM, _lib.OP_RMS_NORM):
+                _lib.tune_override(op, 0, 0, flags)
+            check(layer_norm(xd, wd, bd), ref.layer_norm(x, w, b), dtype, what=tag)
+            check(layer_norm(xd, wd, None), ref.layer_norm(x, w, None), dtype,
+                  what=tag + " no bias")
+            check(layer_norm(xd, w32d, b32d), ref.layer_norm(x, w32, b32), dtype,
+                  what=tag + " fp32 w")
+            check(rms_norm(xd, (cols,), wd), ref.rms_norm(x, (cols,), w), dtype, what=tag)
+            check(rms_norm(xd, (cols,), w32d), ref.rms_norm(x, (cols,), w32), dtype,
+                  what=tag + " fp32 w")
+        finally:
+            for op in (_lib.OP_LAYER_NORM, _lib.OP_RMS_NORM):
+                _lib.tune_override(op, 0, 0, 0)
 
 
 @pytest.mark.parametrize("block", [384, 960, 1024])
@@ -498,3 +514,20 @@ def test_golden_fixtures(kernel):
                 got = {"softmax": softmax, "logsumexp": logsumexp}[kernel](*cuda(x))
             want = torch.from_numpy(np.asarray(c["expected"])).to(dt)
             check(got, want, dt, what=f"{kernel}/{name}")
+
+
+# ---------------------------------------------------------------------------
+# the measured-peak yardstick: the stream copy must copy
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("nbytes", [16, 4080, 4096, 4112, (1 << 20) + 48, 3 << 24])
+def test_stream_copy_copies(nbytes):
+    """Every byte arrives, for whole and partial 4 KiB tiles; the bytes just
+    past the copied range keep their old value."""
+    g = _g(120)
+    src = torch.randint(0, 256, (nbytes,), generator=g, dtype=torch.uint8).to(DEV)
+    dst = torch.full((nbytes + 4096,), 7, dtype=torch.uint8, device=DEV)
+    stream = torch.cuda.current_stream().cuda_stream
+    _lib.call("vbh_stream_copy", src.data_ptr(), dst.data_ptr(), nbytes, stream)
+    torch.cuda.synchronize()
+    assert torch.equal(dst[:nbytes].cpu(), src.cpu())
+    assert bool((dst[nbytes:] == 7).all())

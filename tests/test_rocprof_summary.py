@@ -19,7 +19,7 @@ from dslperfgap_amd.viperbench import rocprof_summary as rs
 from dslperfgap_amd.workloads import WORKLOADS
 
 ROOT = Path(__file__).resolve().parents[1]
-C2 = "_ZN3vbh12_GLOBAL__N_113rms_norm_rowsIDF16bDF16bLi8ELi2ELb1EEEvPKT_PKT0_PS2_liif"
+C2 = "_ZN3vbh12_GLOBAL__N_113rms_norm_rowsIDF16bDF16bLi8ELi2ELi2EEEvPKT_PKT0_PS2_liif"
 COPYK = "vbh::(anonymous namespace)::copy_kernel(unsigned int __vector(4) const*, unsigned int __vector(4)*, long)"
 OTHER = "void at::native::reduce_kernel<512, 1>(...)"
 
