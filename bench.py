@@ -74,7 +74,7 @@ def cpu_baseline(w, cpu_args, budget_s: float) -> dict:
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     fn = getattr(ref, w.fn)
-    warm = 1 if w.fn == "cross_entropy_fwd" else 3
+    warm = 1 if w.fn.startswith("cross_entropy") else 3
     for _ in range(warm):
         fn(*cpu_args)
     # timed calls until `budget_s` seconds of CPU work (at least 3 calls)

@@ -444,8 +444,13 @@ int vbh_cross_entropy_bwd(const void* dloss, const void* logits, const void* lse
   if (n_rows == 0 || n_cols == 0) return 0;
   if (!dloss || !logits || !lse || !labels || !dlogits)
     return fail(VBH_E_INVALID, "cross_entropy_bwd: null pointer");
-  if (n_rows * 256 > kMaxWorkItems) return fail(VBH_E_RANGE, "cross_entropy_bwd: too many rows");
   const int vn = 16 / elt_size(logits_dtype);
+  const bool vec_ok = n_cols % vn == 0 && logits_row_stride % vn == 0 &&
+                      dlogits_row_stride % vn == 0 && aligned16(logits) && aligned16(dlogits);
+  const int64_t tiles = (n_cols / (vec_ok ? vn : 1) + kCeBwdLanes - 1) / kCeBwdLanes;
+  if (n_rows > kMaxWorkItems / (tiles * kCeBwdLanes))
+    return fail(VBH_E_RANGE, "cross_entropy_bwd: %lld x %lld elements exceed one launch",
+                static_cast<long long>(n_rows), static_cast<long long>(n_cols));
   CeBwdArgs a;
   a.dloss = static_cast<const float*>(dloss);
   a.logits = logits;
@@ -466,10 +471,15 @@ int vbh_cross_entropy_bwd(const void* dloss, const void* logits, const void* lse
   a.total_classes = static_cast<float>(total_classes);
   a.class_start = class_start_idx;
   a.has_smoothing = has_smoothing != 0;
-  a.vec = (n_cols % vn == 0 && logits_row_stride % vn == 0 && dlogits_row_stride % vn == 0 &&
-           aligned16(logits) && aligned16(dlogits))
-              ? vn
-              : 1;
+  a.vec = vec_ok ? vn : 1;
+  // store policy: the cross-entropy op's tune flags, else nontemporal, and
+  // written through the L2 from kWriteThroughMinBytes of dlogits
+  const int over = g_flags[VBH_OP_CROSS_ENTROPY].load();
+  a.nt = !(over & kFlagTemporal);
+  bool wt = n_rows * n_cols * elt_size(logits_dtype) >= kWriteThroughMinBytes;
+  if (over & kFlagWriteThrough) wt = true;
+  if (over & kFlagNoWriteThrough) wt = false;
+  a.wt = a.nt && wt;
   return hip_status(launch_cross_entropy_bwd(a, static_cast<hipStream_t>(stream)),
                     "cross_entropy_bwd launch");
 }

@@ -236,14 +236,21 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_stream(
            static_cast<int64_t>(cb) * n_rows + row);
 }
 
-// Backward: one workgroup per row, elementwise over the row.
-template <typename T, int V>
-__global__ __launch_bounds__(256) void ce_bwd_rows(
+// Backward: elementwise over the rows.  One 256-lane workgroup per tile of
+// 256 vectors of one row (one 16-byte vector per lane, the shape of the copy
+// kernel that sets the measured peak); the row's label, dloss and lse are
+// read once per workgroup.
+constexpr int kBwdLanes = kCeBwdLanes;
+
+template <typename T, int V, int SP>
+__global__ __launch_bounds__(kBwdLanes) void ce_bwd_tiles(
     const float* __restrict__ dloss, const T* __restrict__ logits,
     const float* __restrict__ lse, const void* __restrict__ labels, int label_i64,
-    T* __restrict__ dlogits, int n_cols, int64_t ld_in, int64_t ld_out,
-    int64_t dloss_stride, CeScalars c) {
-  const int64_t row = blockIdx.x;
+    T* __restrict__ dlogits, int n_cols, uint32_t tiles_per_row, int64_t ld_in,
+    int64_t ld_out, int64_t dloss_stride, CeScalars c) {
+  const uint32_t row32 = blockIdx.x / tiles_per_row;
+  const int j0 = static_cast<int>(blockIdx.x - row32 * tiles_per_row) * kBwdLanes;
+  const int64_t row = row32;
   const int64_t label = read_label(labels, label_i64, row);
   const float dl = label != c.ignored_index ? dloss[row * dloss_stride] : 0.f;
   const float lse_r = lse[row];
@@ -253,22 +260,25 @@ __global__ __launch_bounds__(256) void ce_bwd_rows(
   const float zfac = c.two_lse_square_scale * lse_r;
   const float smooth_neg = c.has_smoothing ? c.smooth_negative : 0.f;
   const float hit = c.has_smoothing ? c.one_minus_smoothing : 1.0f;
-  const T* lr = logits + row * ld_in;
-  T* dr = dlogits + row * ld_out;
   const int nvec = n_cols / V;
-  for (int j = threadIdx.x; j < nvec; j += blockDim.x) {
-    float v[V], o[V];
-    load_f32<T, V>(lr + static_cast<int64_t>(j) * V, v);
+  const int tile = nvec - j0 < kBwdLanes ? nvec - j0 : kBwdLanes;
+  T* dr = dlogits + row * ld_out;
+  const OutWindow<T, SP> out(dr + static_cast<int64_t>(j0) * V, static_cast<int64_t>(tile) * V);
+  const int j = j0 + static_cast<int>(threadIdx.x);
+  if (j < nvec) {
+    const auto r = load_raw<T, V, SP != kStoreCached>(logits + row * ld_in +
+                                                      static_cast<int64_t>(j) * V);
+    float o[V];
 #pragma unroll
     for (int k = 0; k < V; ++k) {
-      float p = fast_exp(v[k] * c.logit_scale - lse_r);
+      float p = fast_exp(raw_at<T, V>(r, k) * c.logit_scale - lse_r);
       p = p + zfac * p;
       const int64_t col = static_cast<int64_t>(j) * V + k;
       if (col == adj) p = p - hit;
       if (c.has_smoothing) p = p - smooth_neg;
       o[k] = scale * p;
     }
-    store_from_f32<T, V>(dr + static_cast<int64_t>(j) * V, o);
+    out.template store<V>(dr + static_cast<int64_t>(j) * V, static_cast<int>(threadIdx.x) * V, o);
   }
 }
 
@@ -319,15 +329,24 @@ hipError_t launch_cross_entropy_bwd(const CeBwdArgs& a, hipStream_t s) {
   const CeScalars c =
       make_scalars(a.smoothing, a.logit_scale, a.lse_square_scale, a.total_classes,
                    a.ignored_index, a.class_start, a.has_smoothing, 0);
+  Geometry g;
+  g.nt = a.nt != 0;
+  g.wt = a.wt != 0;
   dispatch_float_type(a.logits_dt, [&](auto tt) {
     using T = typename decltype(tt)::type;
     constexpr int VN = Vec<T>::n;
     auto go = [&](auto vc) {
       constexpr int V = decltype(vc)::value;
-      hipLaunchKernelGGL((ce_bwd_rows<T, V>), dim3(a.n_rows), dim3(256), 0, s, a.dloss,
-                         static_cast<const T*>(a.logits), a.lse, a.labels, a.label_i64,
-                         static_cast<T*>(a.dlogits), a.n_cols, a.ld_logits, a.ld_dlogits,
-                         a.dloss_stride, c);
+      const int64_t nvec = a.n_cols / V;
+      const int64_t tiles = (nvec + kBwdLanes - 1) / kBwdLanes;
+      dispatch_store_policy<V>(g, [&](auto sp) {
+        constexpr int SP = decltype(sp)::value;
+        hipLaunchKernelGGL((ce_bwd_tiles<T, V, SP>), dim3(a.n_rows * tiles), dim3(kBwdLanes),
+                           0, s, a.dloss, static_cast<const T*>(a.logits), a.lse, a.labels,
+                           a.label_i64, static_cast<T*>(a.dlogits), a.n_cols,
+                           static_cast<uint32_t>(tiles), a.ld_logits, a.ld_dlogits,
+                           a.dloss_stride, c);
+      });
       err = hipGetLastError();
     };
     if (a.vec == 1) go(std::integral_constant<int, 1>{});

@@ -182,7 +182,11 @@ struct CeBwdArgs {
   int64_t class_start;
   int has_smoothing;
   int vec;
+  int nt;  // nontemporal logits loads / dlogits stores
+  int wt;  // dlogits stores also written through the L2 (with nt, 16-byte rows)
 };
+// One workgroup of this many lanes per tile of as many vectors of one row.
+constexpr int kCeBwdLanes = 256;
 hipError_t launch_cross_entropy_bwd(const CeBwdArgs& a, hipStream_t s);
 
 hipError_t launch_reduce(const void* x, void* vals, int64_t* idx, int64_t outer, int n,

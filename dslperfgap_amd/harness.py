@@ -65,6 +65,11 @@ def essential_work(kernel: str, inputs) -> int:
     if kernel == "logsumexp":
         n = x.shape[-1] if x.dim() else 1
         return el(x) + (x.numel() // max(n, 1)) * x.element_size()
+    if kernel == "cross_entropy_bwd":
+        # dloss, logits, lse, labels -> dlogits (same shape and dtype as logits)
+        dloss, logits, lse, labels = inputs[:4]
+        rows = logits.shape[0]
+        return 2 * el(logits) + el(labels) + rows * lse.element_size() + rows * dloss.element_size()
     if kernel == "cross_entropy":
         logits, labels, bs = inputs[0], inputs[1], int(inputs[8])
         rows, cols = logits.shape
@@ -247,7 +252,7 @@ def make_rotation(w: Workload, cpu_args: tuple, device, min_footprint: int = 2 <
     dev = torch.device(device)
     stream = _bridge.stream(dev)
     ins, outs = [], []
-    x0 = cpu_args[0]
+    x0 = cpu_args[1] if w.fn == "cross_entropy_bwd" else cpu_args[0]
     for _ in range(copies):
         ins.append(tuple(a.to(dev) if isinstance(a, torch.Tensor) else a for a in cpu_args))
     p = _bridge.ptr
@@ -261,6 +266,9 @@ def make_rotation(w: Workload, cpu_args: tuple, device, min_footprint: int = 2 <
         for _ in range(copies):
             outs.append(tuple(torch.empty(x0.shape, dtype=torch.float32, device=dev)
                               for _ in range(3)))
+    elif w.fn == "cross_entropy_bwd":
+        for _ in range(copies):
+            outs.append(torch.empty(x0.shape, dtype=x0.dtype, device=dev))
     rows = x0.numel() // x0.shape[-1]
     cols = x0.shape[-1]
     dt = _float_code(x0)
@@ -305,6 +313,16 @@ def make_rotation(w: Workload, cpu_args: tuple, device, min_footprint: int = 2 <
             call("vbh_cross_entropy_fwd", a[0], a[1], dt, ldt, a[2], a[3], a[4], rows, cols, cols,
                  float(sm), float(scale), float(lss), int(ign), int(total), int(start), int(bs),
                  int(has_sm), int(split), stream)
+    elif w.fn == "cross_entropy_bwd":
+        (_, _, _, labels, sm, scale, lss, ign, total, start, _bs, has_sm) = cpu_args
+        ldt = _bridge.LABEL_CODES[labels.dtype]
+        argv = [(p(i[0]), p(i[1]), p(i[2]), p(i[3]), p(o)) for i, o in zip(ins, outs)]
+
+        def launch(k):
+            a = argv[k % copies]
+            call("vbh_cross_entropy_bwd", a[0], a[1], a[2], a[3], a[4], dt, ldt, rows, cols, cols,
+                 cols, 1, float(sm), float(scale), float(lss), int(ign), int(total), int(start),
+                 int(has_sm), stream)
     else:
         raise KeyError(w.fn)
     return Rotation(w, copies, launch, outs, ins)

@@ -67,6 +67,8 @@ def cases(include_configs=True):
     out = [(c.kernel, c.size, c.fn, c.desc, c.make, c.is_slow) for c in REFERENCE_CASES]
     if include_configs:
         for w in WORKLOADS.values():
+            if w.fn == "cross_entropy_bwd":
+                continue  # the reference's benchmark has no backward rows
             out.append((w.kernel, w.key, w.fn, w.desc, w.make, w.fn == "cross_entropy_fwd"))
     return out
 

@@ -60,6 +60,7 @@ CONFIG_KERNELS = [
     ("C3_softmax", r"softmax_rows<float, float, 4, 2, false, \d>"),
     ("C3_logsumexp", r"logsumexp_rows<float, float, 4, 4, true>"),
     ("C4_cross_entropy", r"ce_fwd_rows<float, 4, 8, true>"),
+    ("C4_cross_entropy_bwd", r"ce_bwd_tiles<float, 4, \d>|ce_bwd_tilesIfLi4ELi\dE"),
     ("C5_layer_norm", r"layer_norm_pipeIDF16bDF16bLi8ELi4ELi\dELb1E"),
     (COPY, r"copy_kernel\("),
 ]

@@ -67,6 +67,16 @@ def make_c4():
     return (logits, labels, 0.0, 1.0, 0.0, -100, 32000, 0, 32768, False, False)
 
 
+def make_c4_bwd():
+    """cross_entropy_bwd at C4's shape: the forward's logits and labels, the
+    per-row lse of its single column block, and dloss = 1 / n_rows (the
+    gradient of the mean of the row losses)."""
+    logits, labels = make_c4()[:2]
+    lse = torch.logsumexp(logits, dim=1)
+    dloss = torch.full((logits.shape[0],), 1.0 / logits.shape[0])
+    return (dloss, logits, lse, labels, 0.0, 1.0, 0.0, -100, 32000, 0, 32768, False)
+
+
 def make_c5():
     g = _gen(4)
     x = torch.randn(2048, 20480, generator=g).to(torch.bfloat16)
@@ -101,6 +111,10 @@ WORKLOADS = {
                  "cross_entropy fwd fp32 logits[8192,32000]~N(0,2), int64 targets, "
                  "BLOCK_SIZE=32768 (one block per row), mean of the 8192 row losses",
                  make_c4, 8192 * 32000 * 4 + 8192 * 8 + 3 * 8192 * 4, "f32"),
+        Workload("C4_cross_entropy_bwd", "cross_entropy", "cross_entropy_bwd",
+                 "cross_entropy bwd fp32 logits[8192,32000] (C4's inputs), lse of the forward, "
+                 "dloss = 1/8192 per row (gradient of the mean), dlogits fp32",
+                 make_c4_bwd, 2 * 8192 * 32000 * 4 + 8192 * 8 + 8192 * 4 + 8192 * 4, "f32"),
         Workload("C5_layer_norm", "layer_norm", "layer_norm",
                  "LayerNorm fwd bf16 x[2048,20480], w~N(1,0.1), b~N(0,0.1), eps=1e-5",
                  make_c5, _rw(2048, 20480, 2, 2 * 20480 * 2), "bf16"),

@@ -159,6 +159,7 @@ def _run(w, args):
     mod = {
         "layer_norm": layer_norm, "rms_norm": rms_norm, "softmax": softmax,
         "log_softmax": log_softmax, "logsumexp": logsumexp, "cross_entropy_fwd": cross_entropy_fwd,
+        "cross_entropy_bwd": cross_entropy_bwd,
     }
     return mod[w.fn](*args)
 
@@ -180,6 +181,14 @@ def test_measured_configs_full_size(key):
         assert abs(hip_mean - ref_mean) <= 1e-4 * abs(ref_mean), (hip_mean, ref_mean)
         lib = torch.nn.functional.cross_entropy(args[0].double(), args[1]).item()
         assert abs(hip_mean - lib) <= 1e-4 * abs(lib), (hip_mean, lib)
+    elif w.fn == "cross_entropy_bwd":
+        # dloss = 1/n_rows scales every entry; compare at the fp32 bar after
+        # undoing it (an absolute 1e-5 would pass anything at this scale)
+        n_rows = args[1].shape[0]
+        check(got * n_rows, want * n_rows, torch.float32, STRICT, key)
+        # size-independent: softmax minus the one-hot label sums to zero per row
+        s = got.double().sum(-1) * n_rows
+        assert s.abs().max().item() < 1e-4
     else:
         check(got, want, want.dtype, STRICT, key)
     if w.fn == "softmax":  # size-independent property: every row sums to one
@@ -470,6 +479,33 @@ def test_cross_entropy_bwd(smoothing, lss, dtype):
     got = cross_entropy_bwd(*cuda(dloss, logits, lse, labels), *args)
     want = ref.cross_entropy_bwd(dloss, logits, lse, labels, *args)
     check(got, want, dtype, what="ce bwd")
+
+
+@pytest.mark.parametrize("flags", [0, _lib.TUNE_WRITE_THROUGH, _lib.TUNE_TEMPORAL])
+@pytest.mark.parametrize("cols,dtype,ldt", [(1001, torch.float32, torch.int64),
+                                            (4096, torch.float32, torch.int32),
+                                            (4104, torch.bfloat16, torch.int64),
+                                            (255, torch.float16, torch.int32)])
+def test_cross_entropy_bwd_tiles(cols, dtype, ldt, flags):
+    """The tiled backward: scalar rows (1001, 255 columns), whole and partial
+    256-vector tiles, int32 / int64 labels, ignored rows, a class_start shift
+    that puts some labels outside the shard, and every store policy."""
+    g = _g(121)
+    rows = 37
+    logits = (2 * torch.randn(rows, cols, generator=g)).to(dtype)
+    labels = torch.randint(0, cols + 50, (rows,), generator=g).to(ldt)
+    labels[5] = -100
+    dloss = torch.rand(rows, generator=g)
+    lse = torch.logsumexp(logits.float(), dim=1)
+    args = (0.05, 1.0, 0.02, -100, cols, 25, 8192, True)
+    try:
+        _lib.tune_override(_lib.OP_CROSS_ENTROPY, 0, 0, flags)
+        got = cross_entropy_bwd(*cuda(dloss, logits, lse, labels), *args)
+    finally:
+        _lib.tune_override(_lib.OP_CROSS_ENTROPY, 0, 0, 0)
+    want = ref.cross_entropy_bwd(dloss, logits, lse, labels, *args)
+    check(got, want, dtype, what=f"ce bwd cols={cols} {dtype} flags={flags}")
+    assert bool((got[5] == 0).all())
 
 
 # ---------------------------------------------------------------------------
