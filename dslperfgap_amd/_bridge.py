@@ -50,11 +50,16 @@ def stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
 
+# torch's raw current-device accessor (torch.cuda.current_device adds a
+# lazy-init check per call; a GPU tensor argument has already initialised it)
+_raw_device = getattr(torch._C, "_cuda_getDevice", None) or torch.cuda.current_device
+
+
 def launch(name: str, dev: torch.device, *args) -> None:
     """Call entry point `name` with `args` followed by the handle of torch's
     current stream on `dev` (every launching entry point takes the stream
     last), with `dev` the current device during the call."""
-    cur = torch.cuda.current_device()
+    cur = _raw_device()
     idx = cur if dev.index is None else dev.index
     if idx == cur:
         _lib.call(name, *args, stream(dev) if _raw_stream is None else _raw_stream(cur))

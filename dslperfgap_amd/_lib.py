@@ -1,11 +1,17 @@
-"""ctypes binding of libvbhip.so (declarations in include/vbhip.h).
+"""Bindings of libvbhip.so (declarations in include/vbhip.h).
 
 The library is loaded after ``import torch`` so that it binds to the HIP
 runtime torch already holds (both carry the soname libamdhip64.so.7), which
 makes torch's stream handles valid for the library's launches.
 
-There is no fallback: if the library is missing, :func:`lib` raises
-``ImportError`` naming the build command.
+Two bindings of the same C ABI: ctypes (every entry point; also checks the ABI
+version and the exported symbols), and the CPython module ``_vbhfast`` built
+from csrc/vbhfast.c, whose METH_FASTCALL functions the launching entry points
+go through because its argument conversion costs about 0.1 us per call
+against ctypes' 0.7 us.
+
+There is no non-HIP fallback: if the library or the binding module is
+missing, :func:`lib` raises ``ImportError`` naming the build command.
 """
 from __future__ import annotations
 
@@ -59,6 +65,14 @@ SIGNATURES = {
 }
 
 
+# entry points _vbhfast binds (every launching one)
+FAST_ENTRY_POINTS = (
+    "vbh_layer_norm_fwd", "vbh_rms_norm_fwd", "vbh_softmax_fwd", "vbh_softmax_dim_fwd",
+    "vbh_logsumexp_fwd", "vbh_cross_entropy_fwd", "vbh_cross_entropy_bwd", "vbh_reduce_fwd",
+    "vbh_stream_copy",
+)
+
+
 class VbhError(RuntimeError):
     """A nonzero status from libvbhip (argument error < 0, hipError_t > 0)."""
 
@@ -91,7 +105,16 @@ def lib() -> ctypes.CDLL:
             version = handle.vbh_abi_version()
             if version != ABI_VERSION:
                 raise ImportError(f"{LIB_PATH} has ABI {version}, expected {ABI_VERSION}")
+            try:
+                from . import _vbhfast
+            except ImportError as e:
+                raise ImportError(f"the CPython binding of {LIB_PATH.name} is missing or stale "
+                                  f"({e}): build it with `python -m dslperfgap_amd.build`") from e
+            if _vbhfast.ABI_VERSION != ABI_VERSION:
+                raise ImportError(f"_vbhfast has ABI {_vbhfast.ABI_VERSION}, expected {ABI_VERSION}")
             _fns.update({name: getattr(handle, name) for name in SIGNATURES})
+            # launching entry points through the fast binding
+            _fns.update({name: getattr(_vbhfast, name) for name in FAST_ENTRY_POINTS})
             _lib = handle
     return _lib
 

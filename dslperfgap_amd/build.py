@@ -1,8 +1,10 @@
 """Build libvbhip.so (the gfx950 HIP kernels + C ABI) in-tree.
 
 Every ``csrc/*.hip`` file is compiled with hipcc for gfx950 only, in parallel,
-into ``_build/``, then linked into ``dslperfgap_amd/libvbhip.so``.  The library
-is rebuilt on every call (the caller asked for a build).
+into ``_build/``, then linked into ``dslperfgap_amd/libvbhip.so``.  The CPython
+binding of its launching entry points (``csrc/vbhfast.c``) is then compiled
+with the host C compiler into ``dslperfgap_amd/_vbhfast*.so``, linked against
+that library.  Both are rebuilt on every call (the caller asked for a build).
 
 Usage: ``python -m dslperfgap_amd.build`` or ``build()`` from Python.
 """
@@ -12,6 +14,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
@@ -19,6 +22,7 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 BUILD_DIR = PKG_DIR / "_build"
 LIB_PATH = PKG_DIR / "libvbhip.so"
+FAST_PATH = PKG_DIR / ("_vbhfast" + sysconfig.get_config_var("EXT_SUFFIX"))
 REPO_ROOT = PKG_DIR.parent
 
 ARCH = "gfx950"
@@ -73,9 +77,29 @@ def build(verbose: bool = True) -> Path:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, LIB_PATH)
+    build_fast()
     if verbose:
-        print(f"built {LIB_PATH} from {len(sources)} sources", file=sys.stderr)
+        print(f"built {LIB_PATH} from {len(sources)} sources, and {FAST_PATH.name}",
+              file=sys.stderr)
     return LIB_PATH
+
+
+def build_fast() -> Path:
+    """Compile the CPython binding (csrc/vbhfast.c) against the built library;
+    the loader finds libvbhip.so next to it ($ORIGIN)."""
+    cc = os.environ.get("CC") or shutil.which("gcc") or shutil.which("cc")
+    if not cc:
+        raise RuntimeError("no host C compiler (gcc) found for the CPython binding")
+    tmp = FAST_PATH.with_suffix(".so.tmp")
+    cmd = [cc, "-O2", "-shared", "-fPIC", "-Wall", "-Werror",
+           f"-I{sysconfig.get_paths()['include']}", f"-I{REPO_ROOT / 'include'}",
+           str(CSRC / "vbhfast.c"), "-o", str(tmp), f"-L{PKG_DIR}", "-lvbhip",
+           "-Wl,-rpath,$ORIGIN"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"building {FAST_PATH.name} failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, FAST_PATH)
+    return FAST_PATH
 
 
 if __name__ == "__main__":

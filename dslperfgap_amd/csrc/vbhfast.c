@@ -1,0 +1,116 @@
+/* CPython binding of the launching entry points of libvbhip.so (include/vbhip.h).
+ *
+ * The same C ABI as the ctypes binding in _lib.py, called through
+ * METH_FASTCALL functions that convert their arguments directly: about 0.1 us
+ * per call where ctypes' argument conversion takes about 0.7 us, which is a
+ * visible share of a small kernel's 2-3 us host path.  Each function takes
+ * the entry point's arguments in the header's order (device pointers as
+ * Python ints or None, sizes as ints, scalars as floats, the stream handle
+ * last) and returns its status code; the GIL is released around the call, as
+ * ctypes does.  No torch types are involved.
+ */
+#define PY_SSIZE_T_CLEAN
+#include <Python.h>
+#include <stdint.h>
+
+#include "vbhip.h"
+
+typedef union {
+  void* p;
+  long long q;
+  double f;
+} arg_t;
+
+/* Parse `n` arguments by `fmt`: 'p' pointer (int or None), 'q' integer,
+ * 'f' float.  Returns 0, or -1 with a Python exception set. */
+static int parse(PyObject* const* args, Py_ssize_t n, const char* fmt, arg_t* out) {
+  Py_ssize_t want = (Py_ssize_t)strlen(fmt);
+  if (n != want) {
+    PyErr_Format(PyExc_TypeError, "expected %zd arguments, got %zd", want, n);
+    return -1;
+  }
+  for (Py_ssize_t i = 0; i < n; ++i) {
+    PyObject* o = args[i];
+    switch (fmt[i]) {
+      case 'p':
+        if (o == Py_None) {
+          out[i].p = NULL;
+        } else {
+          out[i].p = PyLong_AsVoidPtr(o);
+          if (out[i].p == NULL && PyErr_Occurred()) return -1;
+        }
+        break;
+      case 'q':
+        out[i].q = PyLong_AsLongLong(o);
+        if (out[i].q == -1 && PyErr_Occurred()) return -1;
+        break;
+      case 'f':
+        out[i].f = PyFloat_AsDouble(o);
+        if (out[i].f == -1.0 && PyErr_Occurred()) return -1;
+        break;
+      default:
+        PyErr_SetString(PyExc_SystemError, "bad argument format");
+        return -1;
+    }
+  }
+  return 0;
+}
+
+#define P(k) (a[k].p)
+#define Q(k) ((int64_t)a[k].q)
+#define I(k) ((int)a[k].q)
+#define F(k) ((float)a[k].f)
+
+#define ENTRY(name, fmt, call)                                                   \
+  static PyObject* py_##name(PyObject* self, PyObject* const* args, Py_ssize_t n) { \
+    arg_t a[24];                                                                 \
+    int rc;                                                                      \
+    (void)self;                                                                  \
+    if (parse(args, n, fmt, a) < 0) return NULL;                                 \
+    Py_BEGIN_ALLOW_THREADS rc = call;                                            \
+    Py_END_ALLOW_THREADS return PyLong_FromLong(rc);                             \
+  }
+
+ENTRY(vbh_layer_norm_fwd, "ppppqqfqqp",
+      vbh_layer_norm_fwd(P(0), P(1), P(2), P(3), Q(4), Q(5), F(6), I(7), I(8), P(9)))
+ENTRY(vbh_rms_norm_fwd, "pppqqfqqp",
+      vbh_rms_norm_fwd(P(0), P(1), P(2), Q(3), Q(4), F(5), I(6), I(7), P(8)))
+ENTRY(vbh_softmax_fwd, "ppqqqqqp",
+      vbh_softmax_fwd(P(0), P(1), Q(2), Q(3), I(4), I(5), I(6), P(7)))
+ENTRY(vbh_softmax_dim_fwd, "ppqqqqqqp",
+      vbh_softmax_dim_fwd(P(0), P(1), Q(2), Q(3), Q(4), I(5), I(6), I(7), P(8)))
+ENTRY(vbh_logsumexp_fwd, "ppqqqqp",
+      vbh_logsumexp_fwd(P(0), P(1), Q(2), Q(3), I(4), I(5), P(6)))
+ENTRY(vbh_cross_entropy_fwd, "ppqqpppqqqfffqqqqqqp",
+      vbh_cross_entropy_fwd(P(0), P(1), I(2), I(3), P(4), P(5), P(6), Q(7), Q(8), Q(9), F(10),
+                            F(11), F(12), Q(13), Q(14), Q(15), Q(16), I(17), I(18), P(19)))
+ENTRY(vbh_cross_entropy_bwd, "pppppqqqqqqqfffqqqqp",
+      vbh_cross_entropy_bwd(P(0), P(1), P(2), P(3), P(4), I(5), I(6), Q(7), Q(8), Q(9), Q(10),
+                            Q(11), F(12), F(13), F(14), Q(15), Q(16), Q(17), I(18), P(19)))
+ENTRY(vbh_reduce_fwd, "pppqqqqqqp",
+      vbh_reduce_fwd(P(0), P(1), P(2), Q(3), Q(4), Q(5), I(6), I(7), I(8), P(9)))
+ENTRY(vbh_stream_copy, "ppqp", vbh_stream_copy(P(0), P(1), Q(2), P(3)))
+
+#define METHOD(name) {#name, (PyCFunction)(void (*)(void))py_##name, METH_FASTCALL, NULL}
+
+static PyMethodDef methods[] = {
+    METHOD(vbh_layer_norm_fwd),    METHOD(vbh_rms_norm_fwd),   METHOD(vbh_softmax_fwd),
+    METHOD(vbh_softmax_dim_fwd),   METHOD(vbh_logsumexp_fwd),  METHOD(vbh_cross_entropy_fwd),
+    METHOD(vbh_cross_entropy_bwd), METHOD(vbh_reduce_fwd),     METHOD(vbh_stream_copy),
+    {NULL, NULL, 0, NULL},
+};
+
+static struct PyModuleDef module = {
+    PyModuleDef_HEAD_INIT, "_vbhfast",
+    "CPython binding of the launching entry points of libvbhip.so", -1, methods,
+};
+
+PyMODINIT_FUNC PyInit__vbhfast(void) {
+  PyObject* m = PyModule_Create(&module);
+  if (m == NULL) return NULL;
+  if (PyModule_AddIntConstant(m, "ABI_VERSION", vbh_abi_version()) < 0) {
+    Py_DECREF(m);
+    return NULL;
+  }
+  return m;
+}

@@ -97,3 +97,57 @@ def test_missing_library_is_loud(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "_lib", None)
     with pytest.raises(ImportError, match="no non-HIP fallback"):
         _lib.lib()
+
+
+# ---------------------------------------------------------------------------
+# the CPython binding (_vbhfast) of the launching entry points
+# ---------------------------------------------------------------------------
+def _fast():
+    _lib.lib()
+    from dslperfgap_amd import _vbhfast
+    return _vbhfast
+
+
+def test_fast_binding_covers_every_launching_entry_point():
+    """Every entry point that takes a stream is bound by _vbhfast, with the
+    header's arity, and launches go through it."""
+    fast = _fast()
+    decls = _declared()
+    launching = {n for n, (_, args) in _lib.SIGNATURES.items()
+                 if args and args[-1] is ctypes.c_void_p and n != "vbh_tune_override"}
+    assert launching == set(_lib.FAST_ENTRY_POINTS)
+    assert fast.ABI_VERSION == _lib.ABI_VERSION
+    for name in _lib.FAST_ENTRY_POINTS:
+        fn = getattr(fast, name)
+        assert _lib._fns[name] is fn
+        with pytest.raises(TypeError, match=f"expected {decls[name]} arguments"):
+            fn(*([0] * (decls[name] - 1)))
+
+
+def test_fast_and_ctypes_bindings_agree_on_argument_errors():
+    """The same call through both bindings gives the same status and message."""
+    fast = _fast()
+    handle = _lib.lib()
+    cases = [
+        ("vbh_softmax_fwd", (16, 16, -1, 4, 0, 0, 0, None)),
+        ("vbh_softmax_fwd", (16, 16, 4, 4, 0, 0, 2, None)),
+        ("vbh_layer_norm_fwd", (16, 16, 16, 16, 4, 4, 1e-5, 7, 7, None)),
+        ("vbh_reduce_fwd", (16, 16, 16, 1, 8, 1, 0, 0, 3, None)),
+        ("vbh_stream_copy", (16, 16, 15, None)),
+        ("vbh_cross_entropy_bwd", (16, 16, 16, 16, 16, 0, 9, 2, 4, 4, 4, 1, 0.0, 1.0, 0.0,
+                                   -100, 4, 0, 0, None)),
+    ]
+    for name, args in cases:
+        rc_fast = getattr(fast, name)(*args)
+        msg_fast = _lib.last_error()
+        rc_ct = getattr(handle, name)(*args)
+        assert rc_fast == rc_ct < 0, (name, rc_fast, rc_ct)
+        assert msg_fast == _lib.last_error(), name
+
+
+def test_fast_binding_rejects_bad_argument_types():
+    fast = _fast()
+    with pytest.raises(TypeError):
+        fast.vbh_stream_copy(16, 16, 1.5, None)       # size must be an int
+    with pytest.raises(TypeError):
+        fast.vbh_stream_copy("16", 16, 16, None)      # pointer must be an int or None
