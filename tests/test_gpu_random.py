@@ -1,0 +1,188 @@
+"""GPU parity on seeded random cases: shapes, ranks, dtypes, strides and
+arguments drawn per case index, every result checked against the oracle.
+
+Each case draws from its own generator (seed 5000 + family offset + index),
+so a failing case is reproduced by its test id alone.  Tolerances are the
+reference's loose per-dtype set (ViperBench/test_utils.py:12-25, loose_tol):
+fp32 2e-5, fp16 2e-3, bf16 2e-2 for atol and rtol; max values and all indices
+must match exactly (ViperBench/argmax/test.py:38-42).
+"""
+import random
+
+import pytest
+import torch
+
+from dslperfgap_amd.viperbench.argmax.hip_impl import argmax
+from dslperfgap_amd.viperbench.cross_entropy.hip_impl import cross_entropy_bwd, cross_entropy_fwd
+from dslperfgap_amd.viperbench.layer_norm.hip_impl import layer_norm
+from dslperfgap_amd.viperbench.log_softmax.hip_impl import log_softmax
+from dslperfgap_amd.viperbench.logsumexp.hip_impl import logsumexp
+from dslperfgap_amd.viperbench.max_reduction.hip_impl import max_reduction
+from dslperfgap_amd.viperbench.mean_reduction.hip_impl import mean_reduction
+from dslperfgap_amd.viperbench.rms_norm.hip_impl import rms_norm
+from dslperfgap_amd.viperbench.softmax.hip_impl import softmax
+from oracle import pytorch_impl as ref
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+TOL = {torch.float32: 2e-5, torch.float16: 2e-3, torch.bfloat16: 2e-2}
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+N_CASES = 60
+
+
+def _rng(family: int, i: int) -> random.Random:
+    return random.Random(5000 + 1000 * family + i)
+
+
+def _tensor(r: random.Random, shape, dtype, contiguous=None):
+    """N(mu, sigma) values of `dtype`; a non-contiguous view (a transposed or
+    strided slice of a larger tensor) when the draw says so."""
+    g = torch.Generator().manual_seed(r.randrange(1 << 30))
+    mu, sigma = r.choice([0.0, 0.0, 3.0, -50.0]), r.choice([0.05, 1.0, 1.0, 4.0])
+    if contiguous is None:
+        contiguous = r.random() < 0.6
+    if contiguous or len(shape) < 2:
+        return (mu + sigma * torch.randn(shape, generator=g)).to(dtype)
+    if r.random() < 0.5:  # transposed storage of the last two dims
+        base = mu + sigma * torch.randn(*shape[:-2], shape[-1], shape[-2], generator=g)
+        return base.to(dtype).transpose(-1, -2)
+    base = mu + sigma * torch.randn(*shape[:-1], 2 * shape[-1] + 1, generator=g)
+    return base.to(dtype)[..., 1::2]  # every other column: stride 2, odd offset
+
+
+def _shape(r: random.Random, min_ndim=1, max_ndim=3, last=None):
+    ndim = r.randint(min_ndim, max_ndim)
+    dims = [r.choice([1, 2, 3, 7, 16, 33, 64, 100]) for _ in range(ndim - 1)]
+    if last is None:
+        last = r.choice([1, 5, 8, 64, 100, 255, 256, 1000, 1024, 2050, 4096, 8200, 20480])
+    return tuple(dims + [last])
+
+
+def _close(got, want, dtype, what):
+    assert got.device.type == "cuda", what
+    assert got.shape == want.shape and got.dtype == want.dtype, (what, got.shape, want.shape,
+                                                                 got.dtype, want.dtype)
+    tol = TOL[dtype]
+    g, w = got.float().cpu(), want.float()
+    if not torch.allclose(g, w, atol=tol, rtol=tol, equal_nan=True):
+        err = (g - w).abs().nan_to_num(0.0).max().item()
+        raise AssertionError(f"{what}: max_err={err:.3e} tol={tol}")
+
+
+def _same(got, want, what):
+    g = got.cpu()
+    assert g.shape == want.shape and g.dtype == want.dtype, (what, g.shape, want.shape)
+    if g.is_floating_point():
+        assert torch.equal(g.isnan(), want.isnan()), what
+        assert torch.equal(g[~g.isnan()], want[~want.isnan()]), what
+    else:
+        assert torch.equal(g, want), what
+
+
+@pytest.mark.parametrize("i", range(N_CASES))
+def test_random_norms(i):
+    r = _rng(0, i)
+    dtype = r.choice(DTYPES)
+    k = r.choice([1, 1, 1, 2])  # normalized over the last k dims
+    shape = _shape(r, min_ndim=k, max_ndim=k + 2)
+    norm = shape[len(shape) - k:]
+    x = _tensor(r, shape, dtype)
+    wdt = dtype if r.random() < 0.7 else torch.float32
+    g = torch.Generator().manual_seed(r.randrange(1 << 30))
+    w = (1 + 0.1 * torch.randn(norm, generator=g)).to(wdt)
+    b = (0.1 * torch.randn(norm, generator=g)).to(wdt) if r.random() < 0.8 else None
+    tag = f"case {i}: {tuple(shape)} {dtype} w {wdt} bias {b is not None} contig {x.is_contiguous()}"
+    print(f"[gpu] norms {tag}", flush=True)
+    xd, wd = x.to(DEV), w.to(DEV)
+    bd = b.to(DEV) if b is not None else None
+    _close(layer_norm(xd, wd, bd), ref.layer_norm(x, w, b), dtype, "layer_norm " + tag)
+    eps = r.choice([1e-5, 1e-6])
+    _close(rms_norm(xd, norm, wd, eps), ref.rms_norm(x, norm, w, eps), dtype, "rms_norm " + tag)
+
+
+@pytest.mark.parametrize("i", range(N_CASES))
+def test_random_softmax_family(i):
+    r = _rng(1, i)
+    dtype = r.choice(DTYPES)
+    shape = _shape(r, 1, 4)
+    x = _tensor(r, shape, dtype)
+    dim = r.randrange(-len(shape), len(shape))
+    out_dt = torch.float32 if dtype != torch.float32 and r.random() < 0.4 else None
+    tag = f"case {i}: {tuple(shape)} {dtype} dim {dim} dtype {out_dt} contig {x.is_contiguous()}"
+    print(f"[gpu] softmax family {tag}", flush=True)
+    xd = x.to(DEV)
+    _close(softmax(xd), ref.softmax(x), dtype, "softmax " + tag)
+    _close(log_softmax(xd, dim, out_dt), ref.log_softmax(x, dim, out_dt), out_dt or dtype,
+           "log_softmax " + tag)
+    _close(logsumexp(xd), ref.logsumexp(x), dtype, "logsumexp " + tag)
+
+
+@pytest.mark.parametrize("i", range(N_CASES))
+def test_random_reductions(i):
+    r = _rng(2, i)
+    dtype = r.choice(DTYPES)
+    shape = _shape(r, 1, 4, last=r.choice([1, 3, 64, 100, 1000, 4096, 9000]))
+    x = _tensor(r, shape, dtype)
+    if r.random() < 0.2:  # ties and special values
+        flat = x.reshape(-1) if x.is_contiguous() else None
+        if flat is not None and flat.numel() > 3:
+            flat[r.randrange(flat.numel())] = float("nan") if r.random() < 0.5 else float("inf")
+            flat[r.randrange(flat.numel())] = flat[r.randrange(flat.numel())]
+    nd = len(shape)
+    dim = r.randrange(-nd, nd)
+    keep = r.random() < 0.5
+    tag = f"case {i}: {tuple(shape)} {dtype} dim {dim} keepdim {keep} contig {x.is_contiguous()}"
+    print(f"[gpu] reductions {tag}", flush=True)
+    xd = x.to(DEV)
+    v, ix = max_reduction(xd, dim, keep)
+    rv, rix = ref.max_reduction(x, dim, keep)
+    _same(v, rv, "max values " + tag)
+    _same(ix, rix, "max indices " + tag)
+    _same(argmax(xd, dim, keep), ref.argmax(x, dim, keep), "argmax " + tag)
+    if r.random() < 0.3:
+        _same(argmax(xd, None, keep), ref.argmax(x, None, keep), "argmax flat " + tag)
+    dims = sorted(r.sample(range(nd), r.randint(1, nd)))
+    mdt = torch.float32 if dtype != torch.float32 and r.random() < 0.4 else None
+    _close(mean_reduction(xd, dims, keep, mdt), ref.mean_reduction(x, dims, keep, mdt),
+           mdt or dtype, f"mean dims {dims} dtype {mdt} " + tag)
+
+
+@pytest.mark.parametrize("i", range(N_CASES))
+def test_random_cross_entropy(i):
+    r = _rng(3, i)
+    rows = r.choice([1, 3, 17, 64, 200])
+    cols = r.choice([2, 7, 100, 1000, 4096, 32000])
+    bs = r.choice([2 ** k for k in range(1, 16)] + [65536])
+    ldt = r.choice([torch.int32, torch.int64])
+    g = torch.Generator().manual_seed(r.randrange(1 << 30))
+    logits = (r.choice([1.0, 2.0, 8.0]) * torch.randn(rows, cols, generator=g))
+    start = r.choice([0, 0, cols // 3])
+    labels = torch.randint(0, cols + start, (rows,), generator=g).to(ldt)
+    if rows > 2:
+        labels[r.randrange(rows)] = -100
+    smoothing = r.choice([0.0, 0.0, 0.1])
+    split = r.random() < 0.3
+    params = dict(smoothing=smoothing, logit_scale=r.choice([1.0, 0.5, 1.7]),
+                  lse_square_scale=r.choice([0.0, 1e-4]), ignored_index=-100,
+                  total_classes=cols + start, class_start_idx=start, BLOCK_SIZE=bs,
+                  HAS_SMOOTHING=smoothing > 0, SPLIT=split)
+    tag = f"case {i}: {rows}x{cols} {ldt} {params}"
+    print(f"[gpu] cross entropy {tag}", flush=True)
+    got = cross_entropy_fwd(logits.to(DEV), labels.to(DEV), **params)
+    want = ref.cross_entropy_fwd(logits, labels, **params)
+    n = rows * -(-cols // bs)
+    for k, (t, w) in enumerate(zip(got, want)):
+        if k == 2 and split:
+            continue
+        _close(t.reshape(-1)[:n], w.reshape(-1)[:n], torch.float32, f"fwd[{k}] " + tag)
+    # backward with the forward's per-row lse when one block covers the row
+    if bs >= cols and not split:
+        dloss = torch.rand(rows, generator=g)
+        lse = want[1].reshape(-1)[:rows]
+        bargs = (smoothing, params["logit_scale"], params["lse_square_scale"], -100,
+                 cols + start, start, bs, smoothing > 0)
+        _close(cross_entropy_bwd(dloss.to(DEV), logits.to(DEV), lse.to(DEV), labels.to(DEV),
+                                 *bargs),
+               ref.cross_entropy_bwd(dloss, logits, lse, labels, *bargs), torch.float32,
+               "bwd " + tag)
