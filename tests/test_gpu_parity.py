@@ -567,3 +567,58 @@ def test_stream_copy_copies(nbytes):
     torch.cuda.synchronize()
     assert torch.equal(dst[:nbytes].cpu(), src.cpu())
     assert bool((dst[nbytes:] == 7).all())
+
+
+# ---------------------------------------------------------------------------
+# concurrency: the library is stateless and the bindings release the GIL
+# ---------------------------------------------------------------------------
+def test_threads_on_their_own_streams():
+    """Four host threads, each on its own torch stream, launching a mix of the
+    kernels 25 times; every result equals the single-threaded one."""
+    import threading
+
+    g = _g(130)
+    x = torch.randn(300, 2050, generator=g).to(DEV)
+    xb = torch.randn(64, 8192, generator=g).to(torch.bfloat16).to(DEV)
+    w, b = torch.randn(2050, generator=g).to(DEV), torch.randn(2050, generator=g).to(DEV)
+    wb = torch.randn(8192, generator=g).to(torch.bfloat16).to(DEV)
+    logits = torch.randn(40, 5000, generator=g).to(DEV)
+    labels = torch.randint(0, 5000, (40,), generator=g).to(DEV)
+    ce_args = (0.0, 1.0, 0.0, -100, 5000, 0, 2048, False, False)
+    jobs = [
+        lambda: layer_norm(x, w, b),
+        lambda: rms_norm(xb, (8192,), wb, 1e-6),
+        lambda: softmax(x),
+        lambda: log_softmax(xb, 0),
+        lambda: logsumexp(x),
+        lambda: argmax(x, 1),
+        # only the n_rows * ceil(n_cols / BLOCK_SIZE) block-major entries are
+        # written (the rest of the torch.empty output is undefined)
+        lambda: cross_entropy_fwd(logits, labels, *ce_args)[1].reshape(-1)[:40 * 3],
+    ]
+    expected = [j().clone() for j in jobs]
+    torch.cuda.synchronize()
+    errors = []
+
+    def worker(tid):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                outs = []
+                for it in range(25):
+                    k = (tid + it) % len(jobs)
+                    outs.append((k, jobs[k]()))
+                s.synchronize()
+            for k, o in outs:
+                if not torch.equal(o, expected[k]):
+                    errors.append(f"thread {tid}: job {k} differs")
+        except Exception as e:  # surfaced below
+            errors.append(f"thread {tid}: {e!r}")
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not any(t.is_alive() for t in threads), "a worker thread did not finish"
+    assert not errors, errors
