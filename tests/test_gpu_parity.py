@@ -667,3 +667,33 @@ def test_hip_graph_capture_and_replay():
         torch.cuda.synchronize()
         for k, (o, e) in enumerate(zip(outs, want)):
             assert torch.equal(o, e), f"replay {rep}: output {k} differs from eager"
+
+
+# ---------------------------------------------------------------------------
+# vocab-parallel cross entropy, every shard on this one GPU
+# ---------------------------------------------------------------------------
+def test_vocab_parallel_cross_entropy_at_c4():
+    """C4's logits [8192, 32000] as 8 vocab shards of 4000 columns, each run at
+    its per-GPU shape as a row-strided view with class_start_idx = g * 4000 and
+    SPLIT (loss = -logit in the owning shard).  Merging the shards' lse with a
+    logsumexp (what one all-reduce of 8192 x 2 floats would do across GPUs)
+    and adding the SPLIT losses gives torch's cross entropy of the full rows,
+    within 1e-4 relative; the mean loss as well."""
+    w = WORKLOADS["C4_cross_entropy"]
+    logits, labels = w.make()[:2]
+    ld, lbd = cuda(logits, labels)
+    rows, cols = logits.shape
+    shards, width = 8, cols // 8
+    lse_parts, loss_sum = [], torch.zeros(rows, dtype=torch.float64, device=DEV)
+    for gidx in range(shards):
+        view = ld[:, gidx * width:(gidx + 1) * width]  # stride(0) = 32000
+        loss, lse, _ = cross_entropy_fwd(view, lbd, 0.0, 1.0, 0.0, -100, cols, gidx * width,
+                                         4096, False, True)
+        lse_parts.append(lse.reshape(-1)[:rows].double())
+        loss_sum += loss.reshape(-1)[:rows].double()
+    lse_all = torch.logsumexp(torch.stack(lse_parts), dim=0)
+    merged = (lse_all + loss_sum).cpu()
+    want = torch.nn.functional.cross_entropy(logits.double(), labels, reduction="none")
+    rel = ((merged - want).abs() / want.abs().clamp_min(1e-6)).max().item()
+    assert rel < 1e-4, rel
+    assert abs(merged.mean().item() - want.mean().item()) <= 1e-4 * abs(want.mean().item())
