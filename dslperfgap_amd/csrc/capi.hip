@@ -63,7 +63,8 @@ std::atomic<int> g_flags[kNumOps];
 //   for the reductions that write one value per row (logsumexp, cross entropy,
 //   mean / max / argmax), 8 for logsumexp and mean / max / argmax rows of more
 //   than 2048 vectors (1024 lanes x 4 -- one batch of loads per lane -- is the
-//   slow spot: fp32 16384-column logsumexp 6.1 TB/s, 512 x 8 6.9 TB/s);
+//   slow spot: fp32 16384-column logsumexp 6.1 TB/s, 512 x 8 6.9 TB/s) and
+//   earlier still on 16-byte rows (it_target);
 //   nontemporal row loads / stores for every op (rows are touched once);
 //   the persistent pipelined kernel for LayerNorm rows that span 128 or more
 //   lanes and RMSNorm rows that span 512 or more (it keeps every CU streaming
@@ -72,9 +73,21 @@ std::atomic<int> g_flags[kNumOps];
 //   loses 3-13% at 64 lanes); narrower rows run one row group per workgroup.
 constexpr int kItTarget[kNumOps][2] = {{4, 4}, {2, 2}, {2, 4}, {4, 4}, {4, 4}, {4, 4}};
 constexpr int64_t kLongRowVecs = 2048;
+constexpr int64_t kMidRowVecs = 256;
 
-// [op][0] for 4-byte (or unaligned scalar) access, [op][1] for 16-bit vectors
+// [op][0] for 4-byte (or unaligned scalar) access, [op][1] for 16-bit vectors.
+// The read-only row reductions take 8 vectors per lane earlier on 16-byte rows
+// (MI355X sweep over 512-16384 columns, 256 MB per launch): cross entropy at
+// every width (fp32 +6 to +18%, bf16 +12 to +22% over 4), 16-bit logsumexp
+// above 256 vectors (+7% at 500, +12% at 2048), fp32 mean / max / argmax above
+// 256 vectors (+2 to +4%) and their 16-bit rows above 1024 vectors (+13% at
+// 2048); fp32 logsumexp keeps 4 up to 2048 vectors (within 1% either way).
 int it_target(int op, int64_t nvec, int vec) {
+  if (vec > 1) {
+    if (op == VBH_OP_CROSS_ENTROPY) return 8;
+    if (op == VBH_OP_LOGSUMEXP && vec == 8 && nvec > kMidRowVecs) return 8;
+    if (op == VBH_OP_REDUCE && nvec > (vec == 8 ? int64_t(1024) : kMidRowVecs)) return 8;
+  }
   if ((op == VBH_OP_LOGSUMEXP || op == VBH_OP_REDUCE) && nvec > kLongRowVecs) return 8;
   return kItTarget[op][vec == 8 ? 1 : 0];
 }
