@@ -124,6 +124,14 @@ def last_error() -> str:
     return msg.decode() if msg else ""
 
 
+def entry(name: str):
+    """The bound function of entry point `name` (loads the library on first use).
+    It returns the entry point's status; :func:`call` raises on a nonzero one."""
+    if _lib is None:
+        lib()
+    return _fns[name]
+
+
 def call(name: str, *args) -> None:
     """Call entry point `name`; raise VbhError on a nonzero status."""
     if _lib is None:

@@ -31,8 +31,8 @@ def norm_dims(dim, ndim: int, what: str) -> list[int]:
 
 @functools.lru_cache(maxsize=1024)
 def plan(shape: tuple, dims: tuple, keepdim: bool, zero_d: bool) -> tuple:
-    """(outer, n, inner, permutation or None, output shape) of a reduction over
-    the sorted `dims` of a tensor of `shape`.  Adjacent dims collapse into one
+    """(outer, n, inner, permutation or None, output shape, output strides) of
+    a reduction over the sorted `dims` of a tensor of `shape`.  Adjacent dims collapse into one
     axis of the contiguous [outer, n, inner] view; otherwise the reduced dims are
     moved last (one extra copy pass)."""
     if dims[-1] - dims[0] == len(dims) - 1:
@@ -52,7 +52,7 @@ def plan(shape: tuple, dims: tuple, keepdim: bool, zero_d: bool) -> tuple:
         out_shape = tuple(1 if d in dims else s for d, s in enumerate(shape))
     else:
         out_shape = tuple(s for d, s in enumerate(shape) if d not in dims)
-    return outer, n, inner, perm, out_shape
+    return outer, n, inner, perm, out_shape, _bridge.contiguous_strides(out_shape)
 
 
 def reduce(x: torch.Tensor, dims: list[int], keepdim: bool, op: int, out_dtype, what: str):
@@ -62,14 +62,17 @@ def reduce(x: torch.Tensor, dims: list[int], keepdim: bool, op: int, out_dtype, 
     odt = _bridge.FLOAT_CODES[out_dtype]
     zero_d = x.dim() == 0
     shape = (1,) if zero_d else tuple(x.shape)
-    outer, n, inner, perm, out_shape = plan(shape, tuple(dims), bool(keepdim), zero_d)
+    outer, n, inner, perm, out_shape, out_strides = plan(shape, tuple(dims), bool(keepdim),
+                                                          zero_d)
     xc = x.reshape(shape) if zero_d else x
     if perm is not None:
         xc = xc.permute(perm)
     if not xc.is_contiguous():
         xc = xc.contiguous()
-    vals = None if op == _lib.REDUCE_ARGMAX else x.new_empty(out_shape, dtype=out_dtype)
-    idx = None if op == _lib.REDUCE_MEAN else x.new_empty(out_shape, dtype=torch.int64)
+    vals = None if op == _lib.REDUCE_ARGMAX else x.new_empty_strided(out_shape, out_strides,
+                                                                       dtype=out_dtype)
+    idx = None if op == _lib.REDUCE_MEAN else x.new_empty_strided(out_shape, out_strides,
+                                                                 dtype=torch.int64)
     if outer * inner == 0:
         return vals, idx
     _bridge.launch("vbh_reduce_fwd", dev, _bridge.ptr(xc), _bridge.ptr(vals), _bridge.ptr(idx),

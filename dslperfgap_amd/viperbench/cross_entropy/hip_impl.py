@@ -61,9 +61,9 @@ def cross_entropy_fwd(
     n_rows, n_cols = logits.shape
     labels = _labels(labels, n_rows, what)
     dt = _bridge.float_code(logits, what)
-    loss = torch.empty((n_rows, n_cols), dtype=torch.float32, device=logits.device)
-    lse = torch.empty((n_rows, n_cols), dtype=torch.float32, device=logits.device)
-    z_loss = torch.empty((n_rows, n_cols), dtype=torch.float32, device=logits.device)
+    loss = _bridge.empty(logits, (n_rows, n_cols), torch.float32)
+    lse = _bridge.empty(logits, (n_rows, n_cols), torch.float32)
+    z_loss = _bridge.empty(logits, (n_rows, n_cols), torch.float32)
     row_stride = logits.stride(0) if n_rows > 1 else n_cols
     _bridge.launch("vbh_cross_entropy_fwd", dev, _bridge.ptr(logits), _bridge.ptr(labels), dt,
                    _bridge.LABEL_CODES[labels.dtype], _bridge.ptr(loss), _bridge.ptr(lse),
@@ -93,7 +93,7 @@ def cross_entropy_bwd(
     lse_flat = lse.reshape(-1).to(torch.float32).contiguous()
     if lse_flat.numel() < n_rows:
         raise ValueError(f"{what}: lse has {lse_flat.numel()} elements for {n_rows} rows")
-    dlogits = torch.empty((n_rows, n_cols), dtype=logits.dtype, device=logits.device)
+    dlogits = _bridge.empty(logits, (n_rows, n_cols))
     _bridge.launch("vbh_cross_entropy_bwd", dev, _bridge.ptr(dl), _bridge.ptr(logits),
                    _bridge.ptr(lse_flat), _bridge.ptr(labels), _bridge.ptr(dlogits), dt,
                    _bridge.LABEL_CODES[labels.dtype], n_rows, n_cols,

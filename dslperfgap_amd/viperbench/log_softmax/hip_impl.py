@@ -41,7 +41,7 @@ def log_softmax(x, dim=-1, dtype=None):
                          f"{ndim - 1}], but got {dim})")
     d = dim % ndim
     x = x.contiguous()
-    y = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    y = torch.empty_like(x) if out_dtype == x.dtype else torch.empty_like(x, dtype=out_dtype)
     shape = list(x.shape) if x.dim() > 0 else [1]
     if d == ndim - 1:
         cols = shape[-1]

@@ -30,6 +30,6 @@ def logsumexp(x):
     x = x.contiguous()
     cols = x.shape[-1]
     rows = _bridge.numel_prod(out_shape)
-    y = torch.empty(out_shape, dtype=x.dtype, device=x.device)
+    y = _bridge.empty(x, out_shape)
     _bridge.launch("vbh_logsumexp_fwd", dev, _bridge.ptr(x), _bridge.ptr(y), rows, cols, dt, dt)
     return y
