@@ -93,6 +93,37 @@ int it_target(int op, int64_t nvec, int vec) {
 }
 constexpr int kPersistMinTpr[kNumOps] = {128, 512, 0, 0, 0, 0};
 
+// Small launches are bound by latency, not bandwidth: with too few lanes the
+// grid leaves CUs idle and each lane's chain of loads is long.  While a launch
+// would have fewer than kFillLanes lanes (256 per CU), the vectors per lane
+// are halved, down to 2 and as long as a row still fits one wave (a row group
+// over several waves adds an LDS exchange and a barrier).  MI355X, kernel time
+// per launch from HIP-graph replays at the reference's small shapes: LayerNorm
+// bf16 512 x 1024 3.26 -> 2.76 us, softmax fp16 512 x 1024 3.23 -> 2.62,
+// log_softmax 3.06 -> 2.51, cross entropy fp32 256 x 1024 (256-column blocks)
+// 3.63 -> 2.93, argmax fp16 1024 x 1024 3.07 -> 2.85.
+constexpr int64_t kFillLanes = 65536;
+
+int pow2ceil(int64_t n) {
+  int p = 1;
+  while (p < n) p <<= 1;
+  return p;
+}
+
+int row_group_lanes(int64_t nvec, int it) {
+  const int64_t lanes = (nvec + it - 1) / it;
+  if (lanes <= kWave) return pow2ceil(lanes < 1 ? 1 : lanes);
+  return static_cast<int>((lanes + kWave - 1) / kWave) * kWave;
+}
+
+// `units`: row groups one launch runs (rows, or row x column-block segments).
+int fill_it(int it, int64_t nvec, int64_t units) {
+  while (it > 2 && units * row_group_lanes(nvec, it) < kFillLanes &&
+         (nvec + it / 2 - 1) / (it / 2) <= kWave)
+    it /= 2;
+  return it;
+}
+
 // Write-through output stores (kStoreThrough) by default for the kernels that
 // write a full-size output (LayerNorm, RMSNorm, softmax / log_softmax) once
 // one launch writes at least this much.  Measured on MI355X against
@@ -101,17 +132,17 @@ constexpr int kPersistMinTpr[kNumOps] = {128, 512, 0, 0, 0, 0};
 // 4096 x 1024 (16 MiB out) -0.2%, RMSNorm bf16 1024 x 4096 (8 MiB out) -2.5%.
 constexpr int64_t kWriteThroughMinBytes = int64_t(32) << 20;
 
-// `out_bytes`: bytes one launch writes.
-Geometry geometry_for(int op, int64_t cols, int vec, int64_t out_bytes = 0) {
+// `units`: row groups of the launch (see fill_it); `out_bytes`: bytes it writes.
+Geometry geometry_for(int op, int64_t cols, int vec, int64_t units, int64_t out_bytes = 0) {
   const int over = g_flags[op].load();
   int flags = kFlagNontemporal;
   if (over & kFlagNontemporal) flags |= kFlagNontemporal;
   if (over & kFlagTemporal) flags &= ~kFlagNontemporal;
   const bool norm = op == VBH_OP_LAYER_NORM || op == VBH_OP_RMS_NORM;
   if (norm && !(over & kFlagNoPersist)) flags |= kFlagPersist;
-  Geometry g =
-      pick_geometry(cols, vec, it_target(op, cols / vec, vec), g_tpr[op].load(),
-                    g_block[op].load(), flags);
+  const int64_t nvec = cols / vec;
+  Geometry g = pick_geometry(cols, vec, fill_it(it_target(op, nvec, vec), nvec, units),
+                             g_tpr[op].load(), g_block[op].load(), flags);
   if (g.persist && !(over & kFlagPersist) && g.tpr < kPersistMinTpr[op]) g.persist = false;
   const bool full_output =
       op == VBH_OP_LAYER_NORM || op == VBH_OP_RMS_NORM || op == VBH_OP_SOFTMAX;
@@ -133,12 +164,6 @@ int check_grid(int64_t units, const Geometry& g) {
   return 0;
 }
 
-int pow2ceil(int64_t n) {
-  int p = 1;
-  while (p < n) p <<= 1;
-  return p;
-}
-
 // A workgroup holds whole row groups: a requested size is rounded down to a
 // multiple of tpr (and is at least tpr).  A tpr alone may come from the
 // heuristic while the size comes from vbh_tune_override.
@@ -149,14 +174,14 @@ int fit_block(int block, int tpr) { return block < tpr ? tpr : block / tpr * tpr
 // lanes per row (a power of two up to 64, then whole waves up to 1024) as the
 // row grows (fp16 rows of 4096 vectors: 1024 lanes x 4 at 4.8 TB/s, 512 x 8
 // at 6.5 TB/s).
-Geometry reduce_geometry(int64_t n, int vec) {
+Geometry reduce_geometry(int64_t n, int vec, int64_t units) {
   Geometry g;
   g.v = vec;
   g.nt = true;
   const int64_t nvec = n / vec;
   int tpr = g_tpr[VBH_OP_REDUCE].load();
   if (tpr <= 0) {
-    const int per_lane = it_target(VBH_OP_REDUCE, nvec, vec);
+    const int per_lane = fill_it(it_target(VBH_OP_REDUCE, nvec, vec), nvec, units);
     const int64_t lanes = (nvec + per_lane - 1) / per_lane;
     if (lanes <= kWave) {
       tpr = pow2ceil(lanes < 1 ? 1 : lanes);
@@ -296,7 +321,8 @@ int vbh_layer_norm_fwd(const void* x, const void* w, const void* b, void* y, int
   const bool vec_ok = cols % vn == 0 && aligned16(x) && aligned16(y) && aligned16(w) &&
                       (b == nullptr || aligned16(b));
   const Geometry g =
-      geometry_for(VBH_OP_LAYER_NORM, cols, vec_ok ? vn : 1, rows * cols * elt_size(dtype));
+      geometry_for(VBH_OP_LAYER_NORM, cols, vec_ok ? vn : 1, rows,
+                   rows * cols * elt_size(dtype));
   if (int rc = check_grid(rows, g)) return rc;
   return hip_status(launch_layer_norm(x, w, b, y, rows, static_cast<int>(cols), eps, dtype,
                                       w_dtype, g, static_cast<hipStream_t>(stream)),
@@ -317,7 +343,8 @@ int vbh_rms_norm_fwd(const void* x, const void* w, void* y, int64_t rows, int64_
   const int vn = 16 / elt_size(dtype);
   const bool vec_ok = cols % vn == 0 && aligned16(x) && aligned16(y) && aligned16(w);
   const Geometry g =
-      geometry_for(VBH_OP_RMS_NORM, cols, vec_ok ? vn : 1, rows * cols * elt_size(dtype));
+      geometry_for(VBH_OP_RMS_NORM, cols, vec_ok ? vn : 1, rows,
+                   rows * cols * elt_size(dtype));
   if (int rc = check_grid(rows, g)) return rc;
   return hip_status(launch_rms_norm(x, w, y, rows, static_cast<int>(cols), eps, dtype,
                                     w_dtype, g, static_cast<hipStream_t>(stream)),
@@ -343,7 +370,7 @@ int vbh_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols, int in_d
   if (!x || !y) return fail(VBH_E_INVALID, "softmax: null pointer");
   const int vn = 16 / elt_size(in_dtype);
   const bool vec_ok = cols % vn == 0 && aligned16(x) && aligned16(y);
-  const Geometry g = geometry_for(VBH_OP_SOFTMAX, cols, vec_ok ? vn : 1,
+  const Geometry g = geometry_for(VBH_OP_SOFTMAX, cols, vec_ok ? vn : 1, rows,
                                   rows * cols * elt_size(out_dtype));
   if (int rc = check_grid(rows, g)) return rc;
   return hip_status(launch_softmax(x, y, rows, static_cast<int>(cols), in_dtype, out_dtype,
@@ -382,7 +409,7 @@ int vbh_logsumexp_fwd(const void* x, void* y, int64_t rows, int64_t cols, int in
   if ((!x && cols > 0) || !y) return fail(VBH_E_INVALID, "logsumexp: null pointer");
   const int vn = 16 / elt_size(in_dtype);
   const bool vec_ok = cols % vn == 0 && aligned16(x);
-  const Geometry g = geometry_for(VBH_OP_LOGSUMEXP, cols, vec_ok ? vn : 1);
+  const Geometry g = geometry_for(VBH_OP_LOGSUMEXP, cols, vec_ok ? vn : 1, rows);
   if (int rc = check_grid(rows, g)) return rc;
   return hip_status(launch_logsumexp(x, y, rows, static_cast<int>(cols), in_dtype, out_dtype,
                                      g, static_cast<hipStream_t>(stream)),
@@ -412,7 +439,7 @@ int vbh_cross_entropy_fwd(const void* logits, const void* labels, int logits_dty
   const int vn = 16 / elt_size(logits_dtype);
   const bool vec_ok =
       n_cols % vn == 0 && bs % vn == 0 && row_stride % vn == 0 && aligned16(logits);
-  const Geometry g = geometry_for(VBH_OP_CROSS_ENTROPY, bs, vec_ok ? vn : 1);
+  const Geometry g = geometry_for(VBH_OP_CROSS_ENTROPY, bs, vec_ok ? vn : 1, n_rows * ncb);
   if (int rc = check_grid(n_rows * ncb, g)) return rc;
   CeArgs a;
   a.logits = logits;
@@ -515,7 +542,7 @@ int vbh_reduce_fwd(const void* x, void* values, void* indices, int64_t outer, in
   if (inner == 1) {
     const int vn = 16 / elt_size(in_dtype);
     const bool vec_ok = n % vn == 0 && aligned16(x);
-    g = reduce_geometry(n, vec_ok ? vn : 1);
+    g = reduce_geometry(n, vec_ok ? vn : 1, outer);
     if (int rc = check_grid(outer, g)) return rc;
   } else if ((outer * inner + 255) / 256 * 256 > kMaxWorkItems) {
     return fail(VBH_E_RANGE, "reduce: outer * inner too large");
