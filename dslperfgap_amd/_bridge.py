@@ -55,6 +55,8 @@ def contiguous_strides(shape) -> tuple:
     n = len(shape)
     if n == 1:
         return (1,)
+    if n == 2:
+        return (max(int(shape[1]), 1), 1)
     st = [1] * n
     for i in range(n - 2, -1, -1):
         st[i] = st[i + 1] * max(int(shape[i + 1]), 1)
@@ -65,7 +67,7 @@ def empty(like: torch.Tensor, shape, dtype: torch.dtype | None = None) -> torch.
     """A new contiguous tensor of `shape` on `like`'s device, of `dtype` (default:
     `like`'s)."""
     st = contiguous_strides(shape)
-    if dtype is None or dtype == like.dtype:
+    if dtype is None or dtype is like.dtype:
         return like.new_empty_strided(shape, st)
     return like.new_empty_strided(shape, st, dtype=dtype)
 

@@ -43,7 +43,8 @@ def _labels(labels, n_rows, what):
 def _logits(logits, what):
     if logits.dim() != 2:
         raise ValueError(f"{what}: logits must be 2-D [n_rows, n_cols], got {list(logits.shape)}")
-    if logits.stride(1) != 1 or logits.stride(0) < logits.shape[1]:
+    st = logits.stride()
+    if st[1] != 1 or st[0] < logits.shape[1]:
         logits = logits.contiguous()
     return logits
 

@@ -27,7 +27,7 @@ def rms_norm(x, normalized_shape, weight, eps=1e-5):
         raise RuntimeError(f"rms_norm: normalized_shape {tuple(normalized_shape)} has more dims "
                            f"than input {list(x.shape)}")
     dt = _bridge.float_code(x, "rms_norm")
-    cols = _bridge.numel_prod(x.shape[x.dim() - k:])
+    cols = x.shape[-1] if k == 1 else _bridge.numel_prod(x.shape[x.dim() - k:])
     if weight.numel() != cols:
         raise RuntimeError(f"rms_norm: weight has {weight.numel()} elements, the normalized "
                            f"dims hold {cols}")
