@@ -11,6 +11,7 @@
  */
 #define PY_SSIZE_T_CLEAN
 #include <Python.h>
+#include <limits.h>
 #include <stdint.h>
 
 #include "vbhip.h"
@@ -21,8 +22,10 @@ typedef union {
   double f;
 } arg_t;
 
-/* Parse `n` arguments by `fmt`: 'p' pointer (int or None), 'q' integer,
- * 'f' float.  Returns 0, or -1 with a Python exception set. */
+/* Parse `n` arguments by `fmt`: 'p' pointer (int or None), 'q' 64-bit
+ * integer, 'i' integer in the range of a C int (anything else raises
+ * OverflowError rather than wrapping), 'f' float.  Returns 0, or -1 with a
+ * Python exception set. */
 static int parse(PyObject* const* args, Py_ssize_t n, const char* fmt, arg_t* out) {
   Py_ssize_t want = (Py_ssize_t)strlen(fmt);
   if (n != want) {
@@ -41,8 +44,14 @@ static int parse(PyObject* const* args, Py_ssize_t n, const char* fmt, arg_t* ou
         }
         break;
       case 'q':
+      case 'i':
         out[i].q = PyLong_AsLongLong(o);
         if (out[i].q == -1 && PyErr_Occurred()) return -1;
+        if (fmt[i] == 'i' && (out[i].q < INT_MIN || out[i].q > INT_MAX)) {
+          PyErr_Format(PyExc_OverflowError, "argument %zd: %lld does not fit a C int", i,
+                       out[i].q);
+          return -1;
+        }
         break;
       case 'f':
         out[i].f = PyFloat_AsDouble(o);
@@ -62,32 +71,33 @@ static int parse(PyObject* const* args, Py_ssize_t n, const char* fmt, arg_t* ou
 #define F(k) ((float)a[k].f)
 
 #define ENTRY(name, fmt, call)                                                   \
+  static const char fmt_##name[] = fmt;                                          \
   static PyObject* py_##name(PyObject* self, PyObject* const* args, Py_ssize_t n) { \
     arg_t a[24];                                                                 \
     int rc;                                                                      \
     (void)self;                                                                  \
-    if (parse(args, n, fmt, a) < 0) return NULL;                                 \
+    if (parse(args, n, fmt_##name, a) < 0) return NULL;                          \
     Py_BEGIN_ALLOW_THREADS rc = call;                                            \
     Py_END_ALLOW_THREADS return PyLong_FromLong(rc);                             \
   }
 
-ENTRY(vbh_layer_norm_fwd, "ppppqqfqqp",
+ENTRY(vbh_layer_norm_fwd, "ppppqqfiip",
       vbh_layer_norm_fwd(P(0), P(1), P(2), P(3), Q(4), Q(5), F(6), I(7), I(8), P(9)))
-ENTRY(vbh_rms_norm_fwd, "pppqqfqqp",
+ENTRY(vbh_rms_norm_fwd, "pppqqfiip",
       vbh_rms_norm_fwd(P(0), P(1), P(2), Q(3), Q(4), F(5), I(6), I(7), P(8)))
-ENTRY(vbh_softmax_fwd, "ppqqqqqp",
+ENTRY(vbh_softmax_fwd, "ppqqiiip",
       vbh_softmax_fwd(P(0), P(1), Q(2), Q(3), I(4), I(5), I(6), P(7)))
-ENTRY(vbh_softmax_dim_fwd, "ppqqqqqqp",
+ENTRY(vbh_softmax_dim_fwd, "ppqqqiiip",
       vbh_softmax_dim_fwd(P(0), P(1), Q(2), Q(3), Q(4), I(5), I(6), I(7), P(8)))
-ENTRY(vbh_logsumexp_fwd, "ppqqqqp",
+ENTRY(vbh_logsumexp_fwd, "ppqqiip",
       vbh_logsumexp_fwd(P(0), P(1), Q(2), Q(3), I(4), I(5), P(6)))
-ENTRY(vbh_cross_entropy_fwd, "ppqqpppqqqfffqqqqqqp",
+ENTRY(vbh_cross_entropy_fwd, "ppiipppqqqfffqqqqiip",
       vbh_cross_entropy_fwd(P(0), P(1), I(2), I(3), P(4), P(5), P(6), Q(7), Q(8), Q(9), F(10),
                             F(11), F(12), Q(13), Q(14), Q(15), Q(16), I(17), I(18), P(19)))
-ENTRY(vbh_cross_entropy_bwd, "pppppqqqqqqqfffqqqqp",
+ENTRY(vbh_cross_entropy_bwd, "pppppiiqqqqqfffqqqip",
       vbh_cross_entropy_bwd(P(0), P(1), P(2), P(3), P(4), I(5), I(6), Q(7), Q(8), Q(9), Q(10),
                             Q(11), F(12), F(13), F(14), Q(15), Q(16), Q(17), I(18), P(19)))
-ENTRY(vbh_reduce_fwd, "pppqqqqqqp",
+ENTRY(vbh_reduce_fwd, "pppqqqiiip",
       vbh_reduce_fwd(P(0), P(1), P(2), Q(3), Q(4), Q(5), I(6), I(7), I(8), P(9)))
 ENTRY(vbh_stream_copy, "ppqp", vbh_stream_copy(P(0), P(1), Q(2), P(3)))
 
@@ -105,10 +115,45 @@ static struct PyModuleDef module = {
     "CPython binding of the launching entry points of libvbhip.so", -1, methods,
 };
 
+/* FORMATS: entry point name -> its argument format string, so that callers
+ * can check the binding against their own declaration of the header. */
+static int add_formats(PyObject* m) {
+  static const struct {
+    const char* name;
+    const char* fmt;
+  } table[] = {
+      {"vbh_layer_norm_fwd", fmt_vbh_layer_norm_fwd},
+      {"vbh_rms_norm_fwd", fmt_vbh_rms_norm_fwd},
+      {"vbh_softmax_fwd", fmt_vbh_softmax_fwd},
+      {"vbh_softmax_dim_fwd", fmt_vbh_softmax_dim_fwd},
+      {"vbh_logsumexp_fwd", fmt_vbh_logsumexp_fwd},
+      {"vbh_cross_entropy_fwd", fmt_vbh_cross_entropy_fwd},
+      {"vbh_cross_entropy_bwd", fmt_vbh_cross_entropy_bwd},
+      {"vbh_reduce_fwd", fmt_vbh_reduce_fwd},
+      {"vbh_stream_copy", fmt_vbh_stream_copy},
+  };
+  PyObject* d = PyDict_New();
+  if (d == NULL) return -1;
+  for (size_t i = 0; i < sizeof(table) / sizeof(table[0]); ++i) {
+    PyObject* v = PyUnicode_FromString(table[i].fmt);
+    if (v == NULL || PyDict_SetItemString(d, table[i].name, v) < 0) {
+      Py_XDECREF(v);
+      Py_DECREF(d);
+      return -1;
+    }
+    Py_DECREF(v);
+  }
+  if (PyModule_AddObject(m, "FORMATS", d) < 0) {
+    Py_DECREF(d);
+    return -1;
+  }
+  return 0;
+}
+
 PyMODINIT_FUNC PyInit__vbhfast(void) {
   PyObject* m = PyModule_Create(&module);
   if (m == NULL) return NULL;
-  if (PyModule_AddIntConstant(m, "ABI_VERSION", vbh_abi_version()) < 0) {
+  if (PyModule_AddIntConstant(m, "ABI_VERSION", vbh_abi_version()) < 0 || add_formats(m) < 0) {
     Py_DECREF(m);
     return NULL;
   }

@@ -151,3 +151,25 @@ def test_fast_binding_rejects_bad_argument_types():
         fast.vbh_stream_copy(16, 16, 1.5, None)       # size must be an int
     with pytest.raises(TypeError):
         fast.vbh_stream_copy("16", 16, 16, None)      # pointer must be an int or None
+
+
+def test_fast_binding_formats_match_the_ctypes_signatures():
+    """Each _vbhfast entry point converts its arguments as the ctypes
+    declaration of the same header entry does (pointer, int64, int, float)."""
+    fast = _fast()
+    code = {ctypes.c_void_p: "p", ctypes.c_int64: "q", ctypes.c_int: "i", ctypes.c_float: "f"}
+    assert set(fast.FORMATS) == set(_lib.FAST_ENTRY_POINTS)
+    for name in _lib.FAST_ENTRY_POINTS:
+        want = "".join(code[a] for a in _lib.SIGNATURES[name][1])
+        assert fast.FORMATS[name] == want, name
+
+
+def test_fast_binding_rejects_ints_outside_c_int():
+    """An int parameter (a dtype code here) out of C int range raises instead of
+    wrapping round to another value; nothing is called (and the other
+    arguments would be rejected by the library if anything were)."""
+    fast = _fast()
+    with pytest.raises(OverflowError, match="does not fit a C int"):
+        fast.vbh_softmax_fwd(16, 16, -1, 4, 1 << 32, 0, 0, None)
+    with pytest.raises(OverflowError):
+        fast.vbh_reduce_fwd(16, 16, 16, 1, 8, 1, 0, 0, -(1 << 31) - 1, None)
