@@ -110,6 +110,13 @@ int pow2ceil(int64_t n) {
   return p;
 }
 
+// a * b for sizes (a, b >= 0), saturated at INT64_MAX: products of caller
+// sizes are formed before the range checks that reject them.
+int64_t mul_sat(int64_t a, int64_t b) {
+  int64_t r;
+  return __builtin_mul_overflow(a, b, &r) ? INT64_MAX : r;
+}
+
 int row_group_lanes(int64_t nvec, int it) {
   const int64_t lanes = (nvec + it - 1) / it;
   if (lanes <= kWave) return pow2ceil(lanes < 1 ? 1 : lanes);
@@ -118,7 +125,7 @@ int row_group_lanes(int64_t nvec, int it) {
 
 // `units`: row groups one launch runs (rows, or row x column-block segments).
 int fill_it(int it, int64_t nvec, int64_t units) {
-  while (it > 2 && units * row_group_lanes(nvec, it) < kFillLanes &&
+  while (it > 2 && mul_sat(units, row_group_lanes(nvec, it)) < kFillLanes &&
          (nvec + it / 2 - 1) / (it / 2) <= kWave)
     it /= 2;
   return it;
@@ -157,6 +164,10 @@ constexpr int64_t kMaxCols = (int64_t(1) << 31) - 1;
 constexpr int64_t kMaxWorkItems = (int64_t(1) << 32) - 1;
 
 int check_grid(int64_t units, const Geometry& g) {
+  // every unit takes at least one lane
+  if (units > kMaxWorkItems)
+    return fail(VBH_E_RANGE, "launch of %lld rows exceeds 2^32 work-items",
+                static_cast<long long>(units));
   const int64_t grid = g.stream ? units : grid_for(units, g);
   if (grid * g.block > kMaxWorkItems)
     return fail(VBH_E_RANGE, "launch of %lld workgroups x %d lanes exceeds 2^32 work-items",
@@ -322,7 +333,7 @@ int vbh_layer_norm_fwd(const void* x, const void* w, const void* b, void* y, int
                       (b == nullptr || aligned16(b));
   const Geometry g =
       geometry_for(VBH_OP_LAYER_NORM, cols, vec_ok ? vn : 1, rows,
-                   rows * cols * elt_size(dtype));
+                   mul_sat(mul_sat(rows, cols), elt_size(dtype)));
   if (int rc = check_grid(rows, g)) return rc;
   return hip_status(launch_layer_norm(x, w, b, y, rows, static_cast<int>(cols), eps, dtype,
                                       w_dtype, g, static_cast<hipStream_t>(stream)),
@@ -344,7 +355,7 @@ int vbh_rms_norm_fwd(const void* x, const void* w, void* y, int64_t rows, int64_
   const bool vec_ok = cols % vn == 0 && aligned16(x) && aligned16(y) && aligned16(w);
   const Geometry g =
       geometry_for(VBH_OP_RMS_NORM, cols, vec_ok ? vn : 1, rows,
-                   rows * cols * elt_size(dtype));
+                   mul_sat(mul_sat(rows, cols), elt_size(dtype)));
   if (int rc = check_grid(rows, g)) return rc;
   return hip_status(launch_rms_norm(x, w, y, rows, static_cast<int>(cols), eps, dtype,
                                     w_dtype, g, static_cast<hipStream_t>(stream)),
@@ -371,7 +382,7 @@ int vbh_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols, int in_d
   const int vn = 16 / elt_size(in_dtype);
   const bool vec_ok = cols % vn == 0 && aligned16(x) && aligned16(y);
   const Geometry g = geometry_for(VBH_OP_SOFTMAX, cols, vec_ok ? vn : 1, rows,
-                                  rows * cols * elt_size(out_dtype));
+                                  mul_sat(mul_sat(rows, cols), elt_size(out_dtype)));
   if (int rc = check_grid(rows, g)) return rc;
   return hip_status(launch_softmax(x, y, rows, static_cast<int>(cols), in_dtype, out_dtype,
                                    log_mode, g, static_cast<hipStream_t>(stream)),
@@ -389,7 +400,7 @@ int vbh_softmax_dim_fwd(const void* x, void* y, int64_t outer, int64_t n, int64_
   if (n > kMaxCols) return fail(VBH_E_RANGE, "softmax_dim: n too large");
   if (outer == 0 || n == 0 || inner == 0) return 0;
   if (!x || !y) return fail(VBH_E_INVALID, "softmax_dim: null pointer");
-  if ((outer * inner + 255) / 256 * 256 > kMaxWorkItems)
+  if (mul_sat(outer, inner) > kMaxWorkItems / 256 * 256)
     return fail(VBH_E_RANGE, "softmax_dim: outer * inner too large");
   return hip_status(launch_softmax_dim(x, y, outer, static_cast<int>(n), inner, in_dtype,
                                        out_dtype, log_mode, static_cast<hipStream_t>(stream)),
@@ -439,8 +450,9 @@ int vbh_cross_entropy_fwd(const void* logits, const void* labels, int logits_dty
   const int vn = 16 / elt_size(logits_dtype);
   const bool vec_ok =
       n_cols % vn == 0 && bs % vn == 0 && row_stride % vn == 0 && aligned16(logits);
-  const Geometry g = geometry_for(VBH_OP_CROSS_ENTROPY, bs, vec_ok ? vn : 1, n_rows * ncb);
-  if (int rc = check_grid(n_rows * ncb, g)) return rc;
+  const int64_t segments = mul_sat(n_rows, ncb);
+  const Geometry g = geometry_for(VBH_OP_CROSS_ENTROPY, bs, vec_ok ? vn : 1, segments);
+  if (int rc = check_grid(segments, g)) return rc;
   CeArgs a;
   a.logits = logits;
   a.labels = labels;
@@ -516,7 +528,7 @@ int vbh_cross_entropy_bwd(const void* dloss, const void* logits, const void* lse
   // written through the L2 from kWriteThroughMinBytes of dlogits
   const int over = g_flags[VBH_OP_CROSS_ENTROPY].load();
   a.nt = !(over & kFlagTemporal);
-  bool wt = n_rows * n_cols * elt_size(logits_dtype) >= kWriteThroughMinBytes;
+  bool wt = mul_sat(mul_sat(n_rows, n_cols), elt_size(logits_dtype)) >= kWriteThroughMinBytes;
   if (over & kFlagWriteThrough) wt = true;
   if (over & kFlagNoWriteThrough) wt = false;
   a.wt = a.nt && wt;
@@ -544,7 +556,7 @@ int vbh_reduce_fwd(const void* x, void* values, void* indices, int64_t outer, in
     const bool vec_ok = n % vn == 0 && aligned16(x);
     g = reduce_geometry(n, vec_ok ? vn : 1, outer);
     if (int rc = check_grid(outer, g)) return rc;
-  } else if ((outer * inner + 255) / 256 * 256 > kMaxWorkItems) {
+  } else if (mul_sat(outer, inner) > kMaxWorkItems / 256 * 256) {
     return fail(VBH_E_RANGE, "reduce: outer * inner too large");
   }
   return hip_status(launch_reduce(x, values, static_cast<int64_t*>(indices), outer,

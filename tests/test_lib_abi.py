@@ -83,6 +83,27 @@ def test_argument_errors_before_launch():
     assert _lib.last_error()
 
 
+def test_huge_sizes_are_range_errors_before_launch():
+    """Row counts whose products overflow 64 bits (or exceed 2^32 work-items)
+    are rejected with VBH_E_RANGE before anything is launched."""
+    huge = 1 << 62
+    _expect(_lib.E_RANGE, "vbh_layer_norm_fwd", 16, 16, 16, 16, huge, 1024, 1e-5, _lib.F32,
+            _lib.F32, None, match="exceeds 2\\^32")
+    _expect(_lib.E_RANGE, "vbh_rms_norm_fwd", 16, 16, 16, huge, 4096, 1e-5, _lib.BF16,
+            _lib.BF16, None)
+    _expect(_lib.E_RANGE, "vbh_softmax_fwd", 16, 16, huge, 8, _lib.F16, _lib.F16, 1, None)
+    _expect(_lib.E_RANGE, "vbh_logsumexp_fwd", 16, 16, huge, 8, _lib.F32, _lib.F32, None)
+    _expect(_lib.E_RANGE, "vbh_softmax_dim_fwd", 16, 16, huge, 4, huge, _lib.F32, _lib.F32, 0,
+            None, match="too large")
+    _expect(_lib.E_RANGE, "vbh_reduce_fwd", 16, 16, 16, huge, 64, 1, _lib.F32, _lib.F32, 1, None)
+    _expect(_lib.E_RANGE, "vbh_reduce_fwd", 16, 16, 16, huge, 64, huge, _lib.F32, _lib.F32, 1,
+            None, match="too large")
+    _expect(_lib.E_RANGE, "vbh_cross_entropy_fwd", 16, 16, _lib.F32, _lib.I64, 16, 16, 16, huge,
+            1 << 20, 1 << 20, 0.0, 1.0, 0.0, -100, 1 << 20, 0, 16, 0, 0, None)
+    _expect(_lib.E_RANGE, "vbh_cross_entropy_bwd", 16, 16, 16, 16, 16, _lib.F32, _lib.I64, huge,
+            1 << 20, 1 << 20, 1 << 20, 1, 0.0, 1.0, 0.0, -100, 1 << 20, 0, 0, None)
+
+
 def test_empty_sizes_are_noops():
     # zero rows: nothing to launch, status 0 (no device touched)
     _lib.call("vbh_layer_norm_fwd", None, None, None, None, 0, 128, 1e-5, _lib.F32, _lib.F32,
