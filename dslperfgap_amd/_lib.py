@@ -8,7 +8,10 @@ Two bindings of the same C ABI: ctypes (every entry point; also checks the ABI
 version and the exported symbols), and the CPython module ``_vbhfast`` built
 from csrc/vbhfast.c, whose METH_FASTCALL functions the launching entry points
 go through because its argument conversion costs about 0.1 us per call
-against ctypes' 0.7 us.
+against ctypes' 0.7 us.  ``_vbhfast`` does not link the library: it is bound
+to the entry-point addresses of the instance ctypes loaded, so launches, the
+tuning hook and the error message all reach one instance, whichever file
+``VBHIP_LIB`` names.
 
 There is no non-HIP fallback: if the library or the binding module is
 missing, :func:`lib` raises ``ImportError`` naming the build command.
@@ -112,6 +115,8 @@ def lib() -> ctypes.CDLL:
                                   f"({e}): build it with `python -m dslperfgap_amd.build`") from e
             if _vbhfast.ABI_VERSION != ABI_VERSION:
                 raise ImportError(f"_vbhfast has ABI {_vbhfast.ABI_VERSION}, expected {ABI_VERSION}")
+            _vbhfast.bind({name: ctypes.cast(getattr(handle, name), ctypes.c_void_p).value
+                           for name in FAST_ENTRY_POINTS})
             _fns.update({name: getattr(handle, name) for name in SIGNATURES})
             # launching entry points through the fast binding
             _fns.update({name: getattr(_vbhfast, name) for name in FAST_ENTRY_POINTS})

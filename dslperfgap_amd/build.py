@@ -85,16 +85,15 @@ def build(verbose: bool = True) -> Path:
 
 
 def build_fast() -> Path:
-    """Compile the CPython binding (csrc/vbhfast.c) against the built library;
-    the loader finds libvbhip.so next to it ($ORIGIN)."""
+    """Compile the CPython binding (csrc/vbhfast.c).  It does not link the
+    library: _lib binds it to the entry points of the instance it loads."""
     cc = os.environ.get("CC") or shutil.which("gcc") or shutil.which("cc")
     if not cc:
         raise RuntimeError("no host C compiler (gcc) found for the CPython binding")
     tmp = FAST_PATH.with_suffix(".so.tmp")
     cmd = [cc, "-O2", "-shared", "-fPIC", "-Wall", "-Werror",
            f"-I{sysconfig.get_paths()['include']}", f"-I{REPO_ROOT / 'include'}",
-           str(CSRC / "vbhfast.c"), "-o", str(tmp), f"-L{PKG_DIR}", "-lvbhip",
-           "-Wl,-rpath,$ORIGIN"]
+           str(CSRC / "vbhfast.c"), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"building {FAST_PATH.name} failed:\n{res.stdout}\n{res.stderr}")

@@ -8,6 +8,11 @@
  * Python ints or None, sizes as ints, scalars as floats, the stream handle
  * last) and returns its status code; the GIL is released around the call, as
  * ctypes does.  No torch types are involved.
+ *
+ * The module does not link the library.  bind() receives the entry points'
+ * addresses from the library instance the caller loaded (ctypes), so every
+ * call -- launches, vbh_tune_override, vbh_last_error -- reaches that one
+ * instance, whichever file it was loaded from.  Calls before bind() raise.
  */
 #define PY_SSIZE_T_CLEAN
 #include <Python.h>
@@ -70,40 +75,86 @@ static int parse(PyObject* const* args, Py_ssize_t n, const char* fmt, arg_t* ou
 #define I(k) ((int)a[k].q)
 #define F(k) ((float)a[k].f)
 
+/* `call` invokes the entry point through fn_<name>, set by bind(). */
 #define ENTRY(name, fmt, call)                                                   \
+  static __typeof__(&name) fn_##name = NULL;                                     \
   static const char fmt_##name[] = fmt;                                          \
   static PyObject* py_##name(PyObject* self, PyObject* const* args, Py_ssize_t n) { \
     arg_t a[24];                                                                 \
     int rc;                                                                      \
     (void)self;                                                                  \
+    if (fn_##name == NULL) {                                                     \
+      PyErr_SetString(PyExc_RuntimeError, #name " is not bound: call bind() first"); \
+      return NULL;                                                               \
+    }                                                                            \
     if (parse(args, n, fmt_##name, a) < 0) return NULL;                          \
     Py_BEGIN_ALLOW_THREADS rc = call;                                            \
     Py_END_ALLOW_THREADS return PyLong_FromLong(rc);                             \
   }
 
 ENTRY(vbh_layer_norm_fwd, "ppppqqfiip",
-      vbh_layer_norm_fwd(P(0), P(1), P(2), P(3), Q(4), Q(5), F(6), I(7), I(8), P(9)))
+      fn_vbh_layer_norm_fwd(P(0), P(1), P(2), P(3), Q(4), Q(5), F(6), I(7), I(8), P(9)))
 ENTRY(vbh_rms_norm_fwd, "pppqqfiip",
-      vbh_rms_norm_fwd(P(0), P(1), P(2), Q(3), Q(4), F(5), I(6), I(7), P(8)))
+      fn_vbh_rms_norm_fwd(P(0), P(1), P(2), Q(3), Q(4), F(5), I(6), I(7), P(8)))
 ENTRY(vbh_softmax_fwd, "ppqqiiip",
-      vbh_softmax_fwd(P(0), P(1), Q(2), Q(3), I(4), I(5), I(6), P(7)))
+      fn_vbh_softmax_fwd(P(0), P(1), Q(2), Q(3), I(4), I(5), I(6), P(7)))
 ENTRY(vbh_softmax_dim_fwd, "ppqqqiiip",
-      vbh_softmax_dim_fwd(P(0), P(1), Q(2), Q(3), Q(4), I(5), I(6), I(7), P(8)))
+      fn_vbh_softmax_dim_fwd(P(0), P(1), Q(2), Q(3), Q(4), I(5), I(6), I(7), P(8)))
 ENTRY(vbh_logsumexp_fwd, "ppqqiip",
-      vbh_logsumexp_fwd(P(0), P(1), Q(2), Q(3), I(4), I(5), P(6)))
+      fn_vbh_logsumexp_fwd(P(0), P(1), Q(2), Q(3), I(4), I(5), P(6)))
 ENTRY(vbh_cross_entropy_fwd, "ppiipppqqqfffqqqqiip",
-      vbh_cross_entropy_fwd(P(0), P(1), I(2), I(3), P(4), P(5), P(6), Q(7), Q(8), Q(9), F(10),
+      fn_vbh_cross_entropy_fwd(P(0), P(1), I(2), I(3), P(4), P(5), P(6), Q(7), Q(8), Q(9), F(10),
                             F(11), F(12), Q(13), Q(14), Q(15), Q(16), I(17), I(18), P(19)))
 ENTRY(vbh_cross_entropy_bwd, "pppppiiqqqqqfffqqqip",
-      vbh_cross_entropy_bwd(P(0), P(1), P(2), P(3), P(4), I(5), I(6), Q(7), Q(8), Q(9), Q(10),
+      fn_vbh_cross_entropy_bwd(P(0), P(1), P(2), P(3), P(4), I(5), I(6), Q(7), Q(8), Q(9), Q(10),
                             Q(11), F(12), F(13), F(14), Q(15), Q(16), Q(17), I(18), P(19)))
 ENTRY(vbh_reduce_fwd, "pppqqqiiip",
-      vbh_reduce_fwd(P(0), P(1), P(2), Q(3), Q(4), Q(5), I(6), I(7), I(8), P(9)))
-ENTRY(vbh_stream_copy, "ppqp", vbh_stream_copy(P(0), P(1), Q(2), P(3)))
+      fn_vbh_reduce_fwd(P(0), P(1), P(2), Q(3), Q(4), Q(5), I(6), I(7), I(8), P(9)))
+ENTRY(vbh_stream_copy, "ppqp", fn_vbh_stream_copy(P(0), P(1), Q(2), P(3)))
 
 #define METHOD(name) {#name, (PyCFunction)(void (*)(void))py_##name, METH_FASTCALL, NULL}
 
+/* Entry point name -> its slot, for bind() and FORMATS. */
+#define SLOT(name) {#name, (void**)&fn_##name, fmt_##name}
+static const struct {
+  const char* name;
+  void** fn;
+  const char* fmt;
+} slots[] = {
+    SLOT(vbh_layer_norm_fwd),  SLOT(vbh_rms_norm_fwd),      SLOT(vbh_softmax_fwd),
+    SLOT(vbh_softmax_dim_fwd), SLOT(vbh_logsumexp_fwd),     SLOT(vbh_cross_entropy_fwd),
+    SLOT(vbh_cross_entropy_bwd), SLOT(vbh_reduce_fwd),      SLOT(vbh_stream_copy),
+};
+#define N_SLOTS (sizeof(slots) / sizeof(slots[0]))
+
+/* bind({name: address}): set every entry point from the addresses of one
+ * loaded library (all names must be present and nonzero). */
+static PyObject* py_bind(PyObject* self, PyObject* addrs) {
+  void* got[N_SLOTS];
+  (void)self;
+  if (!PyDict_Check(addrs)) {
+    PyErr_SetString(PyExc_TypeError, "bind() takes a dict {entry point name: address}");
+    return NULL;
+  }
+  for (size_t i = 0; i < N_SLOTS; ++i) {
+    PyObject* v = PyDict_GetItemString(addrs, slots[i].name);
+    if (v == NULL) {
+      PyErr_Format(PyExc_KeyError, "bind(): no address for %s", slots[i].name);
+      return NULL;
+    }
+    got[i] = PyLong_AsVoidPtr(v);
+    if (got[i] == NULL) {
+      if (!PyErr_Occurred())
+        PyErr_Format(PyExc_ValueError, "bind(): null address for %s", slots[i].name);
+      return NULL;
+    }
+  }
+  for (size_t i = 0; i < N_SLOTS; ++i) *slots[i].fn = got[i];
+  Py_RETURN_NONE;
+}
+
 static PyMethodDef methods[] = {
+    {"bind", py_bind, METH_O, "bind({entry point name: address}) -- set the entry points"},
     METHOD(vbh_layer_norm_fwd),    METHOD(vbh_rms_norm_fwd),   METHOD(vbh_softmax_fwd),
     METHOD(vbh_softmax_dim_fwd),   METHOD(vbh_logsumexp_fwd),  METHOD(vbh_cross_entropy_fwd),
     METHOD(vbh_cross_entropy_bwd), METHOD(vbh_reduce_fwd),     METHOD(vbh_stream_copy),
@@ -118,25 +169,11 @@ static struct PyModuleDef module = {
 /* FORMATS: entry point name -> its argument format string, so that callers
  * can check the binding against their own declaration of the header. */
 static int add_formats(PyObject* m) {
-  static const struct {
-    const char* name;
-    const char* fmt;
-  } table[] = {
-      {"vbh_layer_norm_fwd", fmt_vbh_layer_norm_fwd},
-      {"vbh_rms_norm_fwd", fmt_vbh_rms_norm_fwd},
-      {"vbh_softmax_fwd", fmt_vbh_softmax_fwd},
-      {"vbh_softmax_dim_fwd", fmt_vbh_softmax_dim_fwd},
-      {"vbh_logsumexp_fwd", fmt_vbh_logsumexp_fwd},
-      {"vbh_cross_entropy_fwd", fmt_vbh_cross_entropy_fwd},
-      {"vbh_cross_entropy_bwd", fmt_vbh_cross_entropy_bwd},
-      {"vbh_reduce_fwd", fmt_vbh_reduce_fwd},
-      {"vbh_stream_copy", fmt_vbh_stream_copy},
-  };
   PyObject* d = PyDict_New();
   if (d == NULL) return -1;
-  for (size_t i = 0; i < sizeof(table) / sizeof(table[0]); ++i) {
-    PyObject* v = PyUnicode_FromString(table[i].fmt);
-    if (v == NULL || PyDict_SetItemString(d, table[i].name, v) < 0) {
+  for (size_t i = 0; i < N_SLOTS; ++i) {
+    PyObject* v = PyUnicode_FromString(slots[i].fmt);
+    if (v == NULL || PyDict_SetItemString(d, slots[i].name, v) < 0) {
       Py_XDECREF(v);
       Py_DECREF(d);
       return -1;
@@ -153,7 +190,8 @@ static int add_formats(PyObject* m) {
 PyMODINIT_FUNC PyInit__vbhfast(void) {
   PyObject* m = PyModule_Create(&module);
   if (m == NULL) return NULL;
-  if (PyModule_AddIntConstant(m, "ABI_VERSION", vbh_abi_version()) < 0 || add_formats(m) < 0) {
+  /* the header version this binding was compiled against */
+  if (PyModule_AddIntConstant(m, "ABI_VERSION", VBH_ABI_VERSION) < 0 || add_formats(m) < 0) {
     Py_DECREF(m);
     return NULL;
   }

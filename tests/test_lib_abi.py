@@ -194,3 +194,39 @@ def test_fast_binding_rejects_ints_outside_c_int():
         fast.vbh_softmax_fwd(16, 16, -1, 4, 1 << 32, 0, 0, None)
     with pytest.raises(OverflowError):
         fast.vbh_reduce_fwd(16, 16, 16, 1, 8, 1, 0, 0, -(1 << 31) - 1, None)
+
+
+def test_fast_binding_calls_the_instance_ctypes_loaded(tmp_path):
+    """With VBHIP_LIB naming another copy of the library, launches through
+    _vbhfast reach that copy: an argument error raised through the fast path
+    leaves its message in that copy's vbh_last_error (read through ctypes)."""
+    import os
+    import shutil
+    import subprocess
+    import sys
+
+    copy = tmp_path / "libvbhip.so"
+    shutil.copy(_lib.LIB_PATH, copy)
+    code = (
+        "from pathlib import Path\n"
+        "from dslperfgap_amd import _lib\n"
+        "_lib.lib()\n"
+        f"assert _lib.LIB_PATH == Path({str(copy)!r}), _lib.LIB_PATH\n"
+        "rc = _lib.entry('vbh_softmax_fwd')(16, 16, -1, 4, 0, 0, 0, None)\n"
+        "assert rc == _lib.E_INVALID, rc\n"
+        "assert 'negative size' in _lib.last_error(), repr(_lib.last_error())\n"
+    )
+    env = dict(os.environ, VBHIP_LIB=str(copy),
+               PYTHONPATH=str(HEADER.parents[1]) + os.pathsep + os.environ.get("PYTHONPATH", ""))
+    res = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True,
+                         timeout=120)
+    assert res.returncode == 0, res.stderr[-2000:]
+
+
+def test_fast_binding_refuses_calls_before_bind():
+    """The module only calls entry points it was bound to (by _lib.lib())."""
+    fast = _fast()
+    with pytest.raises(KeyError, match="no address"):
+        fast.bind({})
+    with pytest.raises(TypeError):
+        fast.bind([])
