@@ -19,6 +19,7 @@ missing, :func:`lib` raises ``ImportError`` naming the build command.
 from __future__ import annotations
 
 import ctypes
+import functools
 import os
 import threading
 from pathlib import Path
@@ -52,6 +53,8 @@ SIGNATURES = {
     "vbh_softmax_fwd": (_i32, [_vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp]),
     "vbh_softmax_dim_fwd": (_i32, [_vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32, _vp]),
     "vbh_logsumexp_fwd": (_i32, [_vp, _vp, _i64, _i64, _i32, _i32, _vp]),
+    "vbh_logsumexp_fwd_ws": (_i32, [_vp, _vp, _i64, _i64, _i32, _i32, _vp, _i64, _vp]),
+    "vbh_logsumexp_workspace_bytes": (_i64, [_i64, _i64, _i32]),
     "vbh_cross_entropy_fwd": (
         _i32,
         [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _f32, _f32, _i64, _i64,
@@ -63,6 +66,9 @@ SIGNATURES = {
          _i64, _i64, _i64, _i32, _vp],
     ),
     "vbh_reduce_fwd": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32, _vp]),
+    "vbh_reduce_fwd_ws": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32, _vp, _i64,
+                                 _vp]),
+    "vbh_reduce_workspace_bytes": (_i64, [_i64, _i64, _i64, _i32, _i32]),
     "vbh_stream_copy": (_i32, [_vp, _vp, _i64, _vp]),
     "vbh_tune_override": (_i32, [_i32, _i32, _i32, _i32]),
 }
@@ -71,8 +77,8 @@ SIGNATURES = {
 # entry points _vbhfast binds (every launching one)
 FAST_ENTRY_POINTS = (
     "vbh_layer_norm_fwd", "vbh_rms_norm_fwd", "vbh_softmax_fwd", "vbh_softmax_dim_fwd",
-    "vbh_logsumexp_fwd", "vbh_cross_entropy_fwd", "vbh_cross_entropy_bwd", "vbh_reduce_fwd",
-    "vbh_stream_copy",
+    "vbh_logsumexp_fwd", "vbh_logsumexp_fwd_ws", "vbh_cross_entropy_fwd",
+    "vbh_cross_entropy_bwd", "vbh_reduce_fwd", "vbh_reduce_fwd_ws", "vbh_stream_copy",
 )
 
 
@@ -155,3 +161,18 @@ def tune_override(op: int, tpr: int = 0, block: int = 0, flags: int = 0) -> None
     """Force threads-per-row / workgroup size / kernel flags for one op
     (all zero restores the built-in heuristic)."""
     call("vbh_tune_override", op, tpr, block, flags)
+    # an overridden geometry turns the row split off (and back on when cleared)
+    logsumexp_workspace_bytes.cache_clear()
+    reduce_workspace_bytes.cache_clear()
+
+
+@functools.lru_cache(maxsize=4096)
+def logsumexp_workspace_bytes(rows: int, cols: int, in_dtype: int) -> int:
+    """Workspace bytes that split a logsumexp launch (0: no split)."""
+    return lib().vbh_logsumexp_workspace_bytes(rows, cols, in_dtype)
+
+
+@functools.lru_cache(maxsize=4096)
+def reduce_workspace_bytes(outer: int, n: int, inner: int, in_dtype: int, op: int) -> int:
+    """Workspace bytes that split a mean / max / argmax launch (0: no split)."""
+    return lib().vbh_reduce_workspace_bytes(outer, n, inner, in_dtype, op)

@@ -75,6 +75,12 @@ def reduce(x: torch.Tensor, dims: list[int], keepdim: bool, op: int, out_dtype, 
                                                                  dtype=torch.int64)
     if outer * inner == 0:
         return vals, idx
-    _bridge.launch("vbh_reduce_fwd", dev, _bridge.ptr(xc), _bridge.ptr(vals), _bridge.ptr(idx),
-                   outer, n, inner, idt, odt, op)
+    ws_bytes = _lib.reduce_workspace_bytes(outer, n, inner, idt, op)
+    if ws_bytes:  # few long rows: split each row over several workgroups
+        ws = _bridge.empty(x, (ws_bytes,), torch.uint8)
+        _bridge.launch("vbh_reduce_fwd_ws", dev, xc.data_ptr(), _bridge.ptr(vals),
+                       _bridge.ptr(idx), outer, n, inner, idt, odt, op, ws.data_ptr(), ws_bytes)
+    else:
+        _bridge.launch("vbh_reduce_fwd", dev, xc.data_ptr(), _bridge.ptr(vals), _bridge.ptr(idx),
+                       outer, n, inner, idt, odt, op)
     return vals, idx

@@ -139,6 +139,39 @@ int fill_it(int it, int64_t nvec, int64_t units) {
 // 4096 x 1024 (16 MiB out) -0.2%, RMSNorm bf16 1024 x 4096 (8 MiB out) -2.5%.
 constexpr int64_t kWriteThroughMinBytes = int64_t(32) << 20;
 
+// Few wide rows leave CUs idle when each row has one row group (128 fp32 rows
+// of 131072 columns: 128 workgroups on 256 CUs).  The read-only row
+// reductions (logsumexp, mean / max / argmax) then split every row into
+// `segs` equal segments: a first launch reduces the [rows * segs, cols / segs]
+// view into a caller-provided workspace, a second combines each row's
+// segments.  On MI355X (fp32 logsumexp, time per call of both launches):
+// 128 x 131072 27.7 -> 15.5 us, 64 x 131072 18.9 -> 10.8, 32 x 262144
+// 33.8 -> 10.8; 512 x 32768 is better unsplit (14.7 vs 15.3-16.2).  The
+// register-resident logsumexp row kernel also gains on longer rows at up to
+// 512 rows (fp32 256 x 65536 3770 -> 4380 GB/s, 335 x 50000 3132 -> 3772,
+// fp16 256 x 131072 3419 -> 4438; 384 x 32768: 3929 unsplit, 3569-3848
+// split); the streaming mean does not (fp32 256 x 65536: 5217 unsplit,
+// 4840-5004 split).
+constexpr int64_t kSplitMaxRows = 256;   // split only launches of fewer rows
+constexpr int64_t kSplitMaxRowsLong = 512;  // ... or, logsumexp, of fewer long rows
+constexpr int64_t kSplitLongVecs = 12288;   // a long row's 16-byte vectors, at least
+constexpr int64_t kSplitTarget = 1024;  // segments per launch to aim for
+constexpr int64_t kSplitMinVecs = 512;  // 16-byte vectors per segment, at least
+constexpr int kSplitMaxSegs = 64;
+
+// Segments per row (a power of two dividing the row's vectors), or 1.
+// `long_rows`: the op also splits up to kSplitMaxRowsLong rows of long rows.
+int split_segments(int64_t rows, int64_t nvec, bool long_rows = false) {
+  const int64_t max_rows =
+      long_rows && nvec >= kSplitLongVecs ? kSplitMaxRowsLong : kSplitMaxRows;
+  if (rows <= 0 || rows >= max_rows) return 1;
+  int segs = 1;
+  while (segs < kSplitMaxSegs && rows * segs < kSplitTarget && nvec % (2 * segs) == 0 &&
+         nvec / (2 * segs) >= kSplitMinVecs)
+    segs *= 2;
+  return segs;
+}
+
 // `units`: row groups of the launch (see fill_it); `out_bytes`: bytes it writes.
 Geometry geometry_for(int op, int64_t cols, int vec, int64_t units, int64_t out_bytes = 0) {
   const int over = g_flags[op].load();
@@ -407,12 +440,22 @@ int vbh_softmax_dim_fwd(const void* x, void* y, int64_t outer, int64_t n, int64_
                     "softmax_dim launch");
 }
 
-int vbh_logsumexp_fwd(const void* x, void* y, int64_t rows, int64_t cols, int in_dtype,
-                      int out_dtype, void* stream) {
+int64_t vbh_logsumexp_workspace_bytes(int64_t rows, int64_t cols, int in_dtype) {
+  if (!is_float(in_dtype) || rows <= 0 || cols <= 0 || cols > kMaxCols) return 0;
+  const int vn = 16 / elt_size(in_dtype);
+  if (cols % vn != 0 || g_tpr[VBH_OP_LOGSUMEXP].load() || g_block[VBH_OP_LOGSUMEXP].load())
+    return 0;
+  const int segs = split_segments(rows, cols / vn, true);
+  return segs > 1 ? rows * segs * static_cast<int64_t>(sizeof(float)) : 0;
+}
+
+int vbh_logsumexp_fwd_ws(const void* x, void* y, int64_t rows, int64_t cols, int in_dtype,
+                         int out_dtype, void* workspace, int64_t workspace_bytes, void* stream) {
   if (!softmax_pair_ok(in_dtype, out_dtype))
     return fail(VBH_E_DTYPE, "logsumexp: unsupported (in, out) dtype pair (%d, %d)", in_dtype,
                 out_dtype);
   if (rows < 0 || cols < 0) return fail(VBH_E_INVALID, "logsumexp: negative size");
+  if (workspace_bytes < 0) return fail(VBH_E_INVALID, "logsumexp: negative workspace size");
   if (cols > kMaxCols) return fail(VBH_E_RANGE, "logsumexp: cols %lld too large",
                                    static_cast<long long>(cols));
   if (rows == 0) return 0;
@@ -420,11 +463,31 @@ int vbh_logsumexp_fwd(const void* x, void* y, int64_t rows, int64_t cols, int in
   if ((!x && cols > 0) || !y) return fail(VBH_E_INVALID, "logsumexp: null pointer");
   const int vn = 16 / elt_size(in_dtype);
   const bool vec_ok = cols % vn == 0 && aligned16(x);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t need = vbh_logsumexp_workspace_bytes(rows, cols, in_dtype);
+  if (need > 0 && vec_ok && workspace != nullptr && workspace_bytes >= need &&
+      aligned16(workspace)) {
+    // segment results in fp32, then a logsumexp over each row's segments
+    const int segs = split_segments(rows, cols / vn, true);
+    const int64_t units = rows * segs;
+    const int seg_cols = static_cast<int>(cols / segs);
+    const Geometry g1 = geometry_for(VBH_OP_LOGSUMEXP, seg_cols, vn, units);
+    if (int rc = check_grid(units, g1)) return rc;
+    const Geometry g2 = geometry_for(VBH_OP_LOGSUMEXP, segs, segs % 4 == 0 ? 4 : 1, rows);
+    hipError_t e = launch_logsumexp(x, workspace, units, seg_cols, in_dtype, kF32, g1, s);
+    if (e == hipSuccess) e = launch_logsumexp(workspace, y, rows, segs, kF32, out_dtype, g2, s);
+    return hip_status(e, "logsumexp launch");
+  }
   const Geometry g = geometry_for(VBH_OP_LOGSUMEXP, cols, vec_ok ? vn : 1, rows);
   if (int rc = check_grid(rows, g)) return rc;
   return hip_status(launch_logsumexp(x, y, rows, static_cast<int>(cols), in_dtype, out_dtype,
-                                     g, static_cast<hipStream_t>(stream)),
+                                     g, s),
                     "logsumexp launch");
+}
+
+int vbh_logsumexp_fwd(const void* x, void* y, int64_t rows, int64_t cols, int in_dtype,
+                      int out_dtype, void* stream) {
+  return vbh_logsumexp_fwd_ws(x, y, rows, cols, in_dtype, out_dtype, nullptr, 0, stream);
 }
 
 int vbh_cross_entropy_fwd(const void* logits, const void* labels, int logits_dtype,
@@ -536,8 +599,26 @@ int vbh_cross_entropy_bwd(const void* dloss, const void* logits, const void* lse
                     "cross_entropy_bwd launch");
 }
 
-int vbh_reduce_fwd(const void* x, void* values, void* indices, int64_t outer, int64_t n,
-                   int64_t inner, int in_dtype, int out_dtype, int op, void* stream) {
+// Split reductions keep, per segment, an fp32 mean, or an int64 index followed
+// (after all indices) by a value of the input type.
+int64_t split_entry_bytes(int op, int in_dtype) {
+  return op == 0 ? static_cast<int64_t>(sizeof(float)) : 8 + elt_size(in_dtype);
+}
+
+int64_t vbh_reduce_workspace_bytes(int64_t outer, int64_t n, int64_t inner, int in_dtype,
+                                   int op) {
+  if (op < 0 || op > 2 || !is_float(in_dtype) || inner != 1 || outer <= 0 || n <= 0 ||
+      n > kMaxCols)
+    return 0;
+  const int vn = 16 / elt_size(in_dtype);
+  if (n % vn != 0 || g_tpr[VBH_OP_REDUCE].load() || g_block[VBH_OP_REDUCE].load()) return 0;
+  const int segs = split_segments(outer, n / vn);
+  return segs > 1 ? outer * segs * split_entry_bytes(op, in_dtype) : 0;
+}
+
+int vbh_reduce_fwd_ws(const void* x, void* values, void* indices, int64_t outer, int64_t n,
+                      int64_t inner, int in_dtype, int out_dtype, int op, void* workspace,
+                      int64_t workspace_bytes, void* stream) {
   if (op < 0 || op > 2) return fail(VBH_E_INVALID, "reduce: unknown op %d", op);
   if (!is_float(in_dtype)) return fail(VBH_E_DTYPE, "reduce: unsupported dtype %d", in_dtype);
   if (op == 0 ? !(out_dtype == in_dtype || (out_dtype == kF32 && in_dtype != kF32))
@@ -545,24 +626,59 @@ int vbh_reduce_fwd(const void* x, void* values, void* indices, int64_t outer, in
     return fail(VBH_E_DTYPE, "reduce: unsupported (in, out) dtype pair (%d, %d)", in_dtype,
                 out_dtype);
   if (outer < 0 || n < 0 || inner < 0) return fail(VBH_E_INVALID, "reduce: negative size");
+  if (workspace_bytes < 0) return fail(VBH_E_INVALID, "reduce: negative workspace size");
   if (n > kMaxCols) return fail(VBH_E_RANGE, "reduce: n too large");
   if (outer == 0 || inner == 0) return 0;
   if (n == 0 && op != 0) return fail(VBH_E_INVALID, "reduce: max / argmax of an empty axis");
   if ((!x && n > 0) || (op != 2 && !values) || (op != 0 && !indices))
     return fail(VBH_E_INVALID, "reduce: null pointer");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  int64_t* idx = static_cast<int64_t*>(indices);
   Geometry g;
   if (inner == 1) {
     const int vn = 16 / elt_size(in_dtype);
     const bool vec_ok = n % vn == 0 && aligned16(x);
+    const int64_t need = vbh_reduce_workspace_bytes(outer, n, inner, in_dtype, op);
+    if (need > 0 && vec_ok && workspace != nullptr && workspace_bytes >= need &&
+        aligned16(workspace)) {
+      const int segs = split_segments(outer, n / vn);
+      const int64_t units = outer * segs;
+      const int seg_n = static_cast<int>(n / segs);
+      const Geometry g1 = reduce_geometry(seg_n, vn, units);
+      if (int rc = check_grid(units, g1)) return rc;
+      hipError_t e;
+      if (op == 0) {
+        // segment means in fp32 (equal segments: their mean is the row's mean)
+        float* means = static_cast<float*>(workspace);
+        e = launch_reduce(x, means, nullptr, units, seg_n, 1, in_dtype, kF32, 0, g1, s);
+        const Geometry g2 = reduce_geometry(segs, segs % 4 == 0 ? 4 : 1, outer);
+        if (e == hipSuccess)
+          e = launch_reduce(means, values, nullptr, outer, segs, 1, kF32, out_dtype, 0, g2, s);
+      } else {
+        // segment (value, index) results, then the first maximal one per row
+        int64_t* pidx = static_cast<int64_t*>(workspace);
+        void* pvals = pidx + units;
+        e = launch_reduce(x, pvals, pidx, units, seg_n, 1, in_dtype, in_dtype, 1, g1, s);
+        if (e == hipSuccess)
+          e = launch_reduce_combine(pvals, pidx, values, idx, outer, segs, seg_n, in_dtype, op,
+                                    s);
+      }
+      return hip_status(e, "reduce launch");
+    }
     g = reduce_geometry(n, vec_ok ? vn : 1, outer);
     if (int rc = check_grid(outer, g)) return rc;
   } else if (mul_sat(outer, inner) > kMaxWorkItems / 256 * 256) {
     return fail(VBH_E_RANGE, "reduce: outer * inner too large");
   }
-  return hip_status(launch_reduce(x, values, static_cast<int64_t*>(indices), outer,
-                                  static_cast<int>(n), inner, in_dtype, out_dtype, op, g,
-                                  static_cast<hipStream_t>(stream)),
+  return hip_status(launch_reduce(x, values, idx, outer, static_cast<int>(n), inner, in_dtype,
+                                  out_dtype, op, g, s),
                     "reduce launch");
+}
+
+int vbh_reduce_fwd(const void* x, void* values, void* indices, int64_t outer, int64_t n,
+                   int64_t inner, int in_dtype, int out_dtype, int op, void* stream) {
+  return vbh_reduce_fwd_ws(x, values, indices, outer, n, inner, in_dtype, out_dtype, op, nullptr,
+                           0, stream);
 }
 
 int vbh_stream_copy(const void* src, void* dst, int64_t bytes, void* stream) {

@@ -184,6 +184,30 @@ __global__ __launch_bounds__(kMaxBlock) void reduce_rows(const Ti* __restrict__ 
   }
 }
 
+// Second stage of a row reduction split into `segs` segments of `segn`
+// elements (max / argmax): one lane per row picks the winner of the segments'
+// (value, index) results, which the first stage wrote as values of type T and
+// int64 segment-local indices, under the same order as the row kernel (NaN
+// largest, then the smaller global index).
+template <typename T, int OP>
+__global__ __launch_bounds__(256) void reduce_combine_vi(const T* __restrict__ pvals,
+                                                         const int64_t* __restrict__ pidx,
+                                                         void* __restrict__ vals,
+                                                         int64_t* __restrict__ idx, int64_t rows,
+                                                         int segs, int segn) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (row >= rows) return;
+  const int64_t base = row * segs;
+  ValIdx best{static_cast<float>(pvals[base]), static_cast<int>(pidx[base])};
+  for (int s = 1; s < segs; ++s) {
+    const ValIdx c{static_cast<float>(pvals[base + s]),
+                   s * segn + static_cast<int>(pidx[base + s])};
+    best = pick(best, c);
+  }
+  if constexpr (OP == 1) store_from_f32<T, 1>(static_cast<T*>(vals) + row, &best.v);
+  idx[row] = best.i;
+}
+
 template <typename Ti, typename To, int OP>
 __global__ __launch_bounds__(256) void reduce_cols(const Ti* __restrict__ x,
                                                    void* __restrict__ vals,
@@ -242,7 +266,28 @@ hipError_t launch_reduce(const void* x, void* vals, int64_t* idx, int64_t outer,
     dispatch_float_type(idt, [&](auto t) { body(t, t); });
   } else if (op == 0 && odt == kF32 && (idt == kF16 || idt == kBF16)) {
     dispatch_float_type(idt, [&](auto t) { body(t, TypeTag<float>{}); });
+  } else if (op == 0 && idt == kF32 && (odt == kF16 || odt == kBF16) && inner == 1) {
+    // second stage of a split mean: fp32 segment means in, the output type out
+    dispatch_float_type(odt, [&](auto t) { body(TypeTag<float>{}, t); });
   }
+  return err;
+}
+
+hipError_t launch_reduce_combine(const void* pvals, const int64_t* pidx, void* vals, int64_t* idx,
+                                 int64_t rows, int segs, int segn, int dt, int op,
+                                 hipStream_t s) {
+  hipError_t err = hipErrorInvalidValue;
+  const int64_t grid = (rows + 255) / 256;
+  dispatch_float_type(dt, [&](auto t) {
+    using T = typename decltype(t)::type;
+    if (op == 1)
+      hipLaunchKernelGGL((reduce_combine_vi<T, 1>), dim3(grid), dim3(256), 0, s,
+                         static_cast<const T*>(pvals), pidx, vals, idx, rows, segs, segn);
+    else
+      hipLaunchKernelGGL((reduce_combine_vi<T, 2>), dim3(grid), dim3(256), 0, s,
+                         static_cast<const T*>(pvals), pidx, vals, idx, rows, segs, segn);
+    err = hipGetLastError();
+  });
   return err;
 }
 

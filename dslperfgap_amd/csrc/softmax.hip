@@ -352,7 +352,9 @@ hipError_t launch_logsumexp(const void* x, void* y, int64_t rows, int cols, int 
     if (g.v == 1) go(std::integral_constant<int, 1>{});
     else go(std::integral_constant<int, VN>{});
   };
-  dispatch_in_out(idt, odt, body);
+  if (!dispatch_in_out(idt, odt, body) && idt == kF32)
+    // second stage of a split logsumexp: fp32 segment results in, the output type out
+    dispatch_float_type(odt, [&](auto t) { body(TypeTag<float>{}, t); });
   return err;
 }
 

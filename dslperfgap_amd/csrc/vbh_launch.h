@@ -192,6 +192,11 @@ hipError_t launch_cross_entropy_bwd(const CeBwdArgs& a, hipStream_t s);
 hipError_t launch_reduce(const void* x, void* vals, int64_t* idx, int64_t outer, int n,
                          int64_t inner, int idt, int odt, int op, const Geometry& g,
                          hipStream_t s);
+// Second stage of a split max (op 1) / argmax (op 2): per row, the winner of
+// `segs` segment results (values of type `dt`, int64 segment-local indices).
+hipError_t launch_reduce_combine(const void* pvals, const int64_t* pidx, void* vals, int64_t* idx,
+                                 int64_t rows, int segs, int segn, int dt, int op,
+                                 hipStream_t s);
 
 hipError_t launch_stream_copy(const void* src, void* dst, int64_t bytes, hipStream_t s);
 

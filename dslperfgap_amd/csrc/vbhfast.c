@@ -102,6 +102,8 @@ ENTRY(vbh_softmax_dim_fwd, "ppqqqiiip",
       fn_vbh_softmax_dim_fwd(P(0), P(1), Q(2), Q(3), Q(4), I(5), I(6), I(7), P(8)))
 ENTRY(vbh_logsumexp_fwd, "ppqqiip",
       fn_vbh_logsumexp_fwd(P(0), P(1), Q(2), Q(3), I(4), I(5), P(6)))
+ENTRY(vbh_logsumexp_fwd_ws, "ppqqiipqp",
+      fn_vbh_logsumexp_fwd_ws(P(0), P(1), Q(2), Q(3), I(4), I(5), P(6), Q(7), P(8)))
 ENTRY(vbh_cross_entropy_fwd, "ppiipppqqqfffqqqqiip",
       fn_vbh_cross_entropy_fwd(P(0), P(1), I(2), I(3), P(4), P(5), P(6), Q(7), Q(8), Q(9), F(10),
                             F(11), F(12), Q(13), Q(14), Q(15), Q(16), I(17), I(18), P(19)))
@@ -110,6 +112,9 @@ ENTRY(vbh_cross_entropy_bwd, "pppppiiqqqqqfffqqqip",
                             Q(11), F(12), F(13), F(14), Q(15), Q(16), Q(17), I(18), P(19)))
 ENTRY(vbh_reduce_fwd, "pppqqqiiip",
       fn_vbh_reduce_fwd(P(0), P(1), P(2), Q(3), Q(4), Q(5), I(6), I(7), I(8), P(9)))
+ENTRY(vbh_reduce_fwd_ws, "pppqqqiiipqp",
+      fn_vbh_reduce_fwd_ws(P(0), P(1), P(2), Q(3), Q(4), Q(5), I(6), I(7), I(8), P(9), Q(10),
+                           P(11)))
 ENTRY(vbh_stream_copy, "ppqp", fn_vbh_stream_copy(P(0), P(1), Q(2), P(3)))
 
 #define METHOD(name) {#name, (PyCFunction)(void (*)(void))py_##name, METH_FASTCALL, NULL}
@@ -121,9 +126,10 @@ static const struct {
   void** fn;
   const char* fmt;
 } slots[] = {
-    SLOT(vbh_layer_norm_fwd),  SLOT(vbh_rms_norm_fwd),      SLOT(vbh_softmax_fwd),
-    SLOT(vbh_softmax_dim_fwd), SLOT(vbh_logsumexp_fwd),     SLOT(vbh_cross_entropy_fwd),
-    SLOT(vbh_cross_entropy_bwd), SLOT(vbh_reduce_fwd),      SLOT(vbh_stream_copy),
+    SLOT(vbh_layer_norm_fwd),    SLOT(vbh_rms_norm_fwd),     SLOT(vbh_softmax_fwd),
+    SLOT(vbh_softmax_dim_fwd),   SLOT(vbh_logsumexp_fwd),    SLOT(vbh_logsumexp_fwd_ws),
+    SLOT(vbh_cross_entropy_fwd), SLOT(vbh_cross_entropy_bwd), SLOT(vbh_reduce_fwd),
+    SLOT(vbh_reduce_fwd_ws),     SLOT(vbh_stream_copy),
 };
 #define N_SLOTS (sizeof(slots) / sizeof(slots[0]))
 
@@ -155,9 +161,10 @@ static PyObject* py_bind(PyObject* self, PyObject* addrs) {
 
 static PyMethodDef methods[] = {
     {"bind", py_bind, METH_O, "bind({entry point name: address}) -- set the entry points"},
-    METHOD(vbh_layer_norm_fwd),    METHOD(vbh_rms_norm_fwd),   METHOD(vbh_softmax_fwd),
-    METHOD(vbh_softmax_dim_fwd),   METHOD(vbh_logsumexp_fwd),  METHOD(vbh_cross_entropy_fwd),
-    METHOD(vbh_cross_entropy_bwd), METHOD(vbh_reduce_fwd),     METHOD(vbh_stream_copy),
+    METHOD(vbh_layer_norm_fwd),    METHOD(vbh_rms_norm_fwd),      METHOD(vbh_softmax_fwd),
+    METHOD(vbh_softmax_dim_fwd),   METHOD(vbh_logsumexp_fwd),     METHOD(vbh_logsumexp_fwd_ws),
+    METHOD(vbh_cross_entropy_fwd), METHOD(vbh_cross_entropy_bwd), METHOD(vbh_reduce_fwd),
+    METHOD(vbh_reduce_fwd_ws),     METHOD(vbh_stream_copy),
     {NULL, NULL, 0, NULL},
 };
 

@@ -101,6 +101,25 @@ int vbh_softmax_dim_fwd(const void* x, void* y, int64_t outer, int64_t n,
 int vbh_logsumexp_fwd(const void* x, void* y, int64_t rows, int64_t cols,
                       int in_dtype, int out_dtype, void* stream);
 
+/* vbh_logsumexp_fwd with a caller-provided device workspace (16-byte aligned).
+ * When a launch has few rows (fewer than 256) of many 16-byte vectors, each
+ * row is split into segments reduced in parallel into the workspace, then
+ * combined by a logsumexp over each row's segment results -- the two-stage
+ * shape of ViperBench/logsumexp/triton_impl.py:48-71 (block partials, then a
+ * logsumexp over them), with the second stage on the GPU.  The workspace must
+ * hold vbh_logsumexp_workspace_bytes(rows, cols, in_dtype) bytes; when that is
+ * 0, or the workspace is null or smaller, this is vbh_logsumexp_fwd.  The
+ * workspace is scratch of this call (stream-ordered: reuse it after the call's
+ * work on `stream`, not concurrently on another stream). */
+int vbh_logsumexp_fwd_ws(const void* x, void* y, int64_t rows, int64_t cols,
+                         int in_dtype, int out_dtype, void* workspace,
+                         int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes vbh_logsumexp_fwd_ws splits such a launch with (0: it does
+ * not split).  A pure function of its arguments and of vbh_tune_override's
+ * state (an overridden logsumexp geometry disables the split). */
+int64_t vbh_logsumexp_workspace_bytes(int64_t rows, int64_t cols, int in_dtype);
+
 /* Column-blocked cross-entropy forward.  For every (row, column block cb) with
  * cb < ceil(n_cols / block_size) it writes loss, lse and z_loss (fp32) at flat
  * index cb * n_rows + row of the three output buffers.  Positions past
@@ -146,6 +165,21 @@ int vbh_cross_entropy_bwd(const void* dloss, const void* logits, const void* lse
  *           ViperBench/argmax/pytorch_impl.py:4-8 (torch.argmax). */
 int vbh_reduce_fwd(const void* x, void* values, void* indices, int64_t outer, int64_t n,
                    int64_t inner, int in_dtype, int out_dtype, int op, void* stream);
+
+/* vbh_reduce_fwd with a caller-provided device workspace (16-byte aligned):
+ * last-axis reductions (inner == 1) of few long rows are split into segments
+ * reduced in parallel, then combined per row (the mean of the equal segments'
+ * fp32 means; the first maximal segment result, NaN largest).  Workspace
+ * size, fallback and reuse as for vbh_logsumexp_fwd_ws, with
+ * vbh_reduce_workspace_bytes.  No reference counterpart: torch.mean / max /
+ * argmax (the goldens above) choose their own split internally. */
+int vbh_reduce_fwd_ws(const void* x, void* values, void* indices, int64_t outer, int64_t n,
+                      int64_t inner, int in_dtype, int out_dtype, int op, void* workspace,
+                      int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes vbh_reduce_fwd_ws splits such a launch with (0: no split). */
+int64_t vbh_reduce_workspace_bytes(int64_t outer, int64_t n, int64_t inner, int in_dtype,
+                                   int op);
 
 /* Device-to-device stream copy of `bytes` (16-byte aligned pointers and size),
  * the kernel whose sustained rate is the measured HBM peak.

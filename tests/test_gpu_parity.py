@@ -697,3 +697,46 @@ def test_vocab_parallel_cross_entropy_at_c4():
     rel = ((merged - want).abs() / want.abs().clamp_min(1e-6)).max().item()
     assert rel < 1e-4, rel
     assert abs(merged.mean().item() - want.mean().item()) <= 1e-4 * abs(want.mean().item())
+
+
+# ---------------------------------------------------------------------------
+# logsumexp of few long rows: the split path
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("rows,cols", [(1, 65536), (3, 131072), (33, 32768), (255, 16384),
+                                       (300, 131072)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_split_logsumexp(rows, cols, dtype):
+    """Launches that split every row (the workspace query says so) match the
+    oracle, with special rows: all -inf (-inf), one +inf (+inf), one NaN
+    (NaN), and a large value in one late segment only."""
+    code = {torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}[dtype]
+    assert _lib.logsumexp_workspace_bytes(rows, cols, code) > 0
+    x = (3 * torch.randn(rows, cols, generator=_g(400 + rows))).to(dtype)
+    x[0, cols - 2] = 30.0
+    if rows > 1:
+        x[1, :] = float("-inf")
+    if rows > 2:
+        x[2, cols // 2] = float("inf")
+    if rows > 3:
+        x[3, 5] = float("nan")
+    got = logsumexp(x.to(DEV))
+    want = ref.logsumexp(x)
+    check(got, want, dtype, what=f"split logsumexp {rows}x{cols} {dtype}")
+
+
+def test_split_logsumexp_matches_the_unsplit_kernel():
+    """The same launch through vbh_logsumexp_fwd_ws with and without a
+    workspace: the split and unsplit kernels agree to fp32 rounding."""
+    rows, cols = 7, 131072
+    x = (3 * torch.randn(rows, cols, generator=_g(410))).to(DEV)
+    need = _lib.logsumexp_workspace_bytes(rows, cols, _lib.F32)
+    assert need > 0
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    outs = []
+    for w, nb in ((ws, need), (None, 0)):
+        y = torch.empty(rows, device=DEV)
+        _lib.call("vbh_logsumexp_fwd_ws", x.data_ptr(), y.data_ptr(), rows, cols, _lib.F32,
+                  _lib.F32, w.data_ptr() if w is not None else None, nb,
+                  torch.cuda.current_stream().cuda_stream)
+        outs.append(y.cpu())
+    assert torch.allclose(outs[0], outs[1], atol=1e-5, rtol=1e-6), (outs[0] - outs[1]).abs().max()

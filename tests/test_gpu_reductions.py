@@ -156,3 +156,68 @@ def test_reduce_geometry_overrides(tpr, block):
         _close(mean_reduction(xd, 1), ref.mean_reduction(x, 1))
     finally:
         _lib.tune_override(_lib.OP_REDUCE, 0, 0, 0)
+
+
+# ---------------------------------------------------------------------------
+# few long rows: the split path (segments reduced in parallel, then combined)
+# ---------------------------------------------------------------------------
+SPLIT_SHAPES = [(1, 65536), (3, 131072), (17, 32768), (200, 16384)]
+
+
+@pytest.mark.parametrize("rows,cols", SPLIT_SHAPES)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_split_reductions_match_the_oracle(rows, cols, dtype):
+    """These launches split every row (the workspace query says so); special
+    values sit in different segments: the row maximum twice (ties across
+    segments give the first), and, in other rows, a NaN after an earlier
+    maximum or two NaNs (the first NaN wins)."""
+    code = {torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}[dtype]
+    for op in (_lib.REDUCE_MEAN, _lib.REDUCE_MAX, _lib.REDUCE_ARGMAX):
+        assert _lib.reduce_workspace_bytes(rows, cols, 1, code, op) > 0, (rows, cols, op)
+    x = torch.randn(rows, cols, generator=_g(310 + rows)).to(dtype)
+    x[0, cols // 3] = 50.0
+    x[0, cols - 5] = 50.0
+    if rows > 1:
+        x[1, 7] = 60.0
+        x[1, cols // 2 + 1] = float("nan")
+    if rows > 2:
+        x[2, cols - 1] = float("nan")
+        x[2, cols // 4] = float("nan")
+        x[2, 3] = float("inf")
+    xd = x.to(DEV)
+    what = f"{rows}x{cols} {dtype}"
+    v, i = max_reduction(xd, 1)
+    rv, ri = ref.max_reduction(x, 1)
+    _same(v, rv, "max values " + what)
+    _same(i, ri, "max indices " + what)
+    _same(argmax(xd, 1), ref.argmax(x, 1), "argmax " + what)
+    _same(argmax(xd, -1, True), ref.argmax(x, -1, True), "argmax keepdim " + what)
+    xm = torch.randn(rows, cols, generator=_g(320 + rows)).to(dtype) + 3.0
+    xmd = xm.to(DEV)
+    _close(mean_reduction(xmd, 1), ref.mean_reduction(xm, 1), "mean " + what)
+    if dtype != torch.float32:
+        _close(mean_reduction(xmd, 1, False, torch.float32),
+               ref.mean_reduction(xm, 1, False, torch.float32), "mean fp32 out " + what)
+
+
+def test_split_reduction_falls_back_without_enough_workspace():
+    """vbh_reduce_fwd_ws with a workspace smaller than the query's size (or
+    none) runs the unsplit kernel: the same indices and values."""
+    rows, cols = 5, 65536
+    x = torch.randn(rows, cols, generator=_g(330)).to(DEV)
+    need = _lib.reduce_workspace_bytes(rows, cols, 1, _lib.F32, _lib.REDUCE_MAX)
+    assert need > 0
+    outs = []
+    for ws_bytes in (need, need - 16, 0):
+        v = torch.empty(rows, device=DEV)
+        i = torch.empty(rows, dtype=torch.int64, device=DEV)
+        ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=DEV)
+        _lib.call("vbh_reduce_fwd_ws", x.data_ptr(), v.data_ptr(), i.data_ptr(), rows, cols, 1,
+                  _lib.F32, _lib.F32, _lib.REDUCE_MAX, ws.data_ptr() if ws_bytes else None,
+                  ws_bytes, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        outs.append((v.cpu(), i.cpu()))
+    for v, i in outs[1:]:
+        assert torch.equal(v, outs[0][0]) and torch.equal(i, outs[0][1])
+    rv, ri = ref.max_reduction(x.cpu(), 1)
+    assert torch.equal(outs[0][1], ri)

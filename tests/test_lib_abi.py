@@ -20,7 +20,7 @@ def _declared():
     text = HEADER.read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     decls = {}
-    for m in re.finditer(r"\b(?:int|const char\*)\s+(vbh_\w+)\s*\(([^)]*)\)\s*;", text):
+    for m in re.finditer(r"\b(?:int|int64_t|const char\*)\s+(vbh_\w+)\s*\(([^)]*)\)\s*;", text):
         args = [a.strip() for a in m.group(2).split(",") if a.strip() and a.strip() != "void"]
         decls[m.group(1)] = len(args)
     return decls
@@ -230,3 +230,41 @@ def test_fast_binding_refuses_calls_before_bind():
         fast.bind({})
     with pytest.raises(TypeError):
         fast.bind([])
+
+
+def test_split_workspace_sizes():
+    """The row split is a pure function of the launch shape: few long rows split
+    (segments of >= 512 16-byte vectors, a power of two per row, about 1024
+    segments per launch), many rows or short rows do not, and an overridden
+    geometry turns it off."""
+    h = _lib.lib()
+    lse, red = h.vbh_logsumexp_workspace_bytes, h.vbh_reduce_workspace_bytes
+    assert lse(8192, 4096, _lib.F32) == 0                 # many rows
+    assert lse(128, 131072, _lib.F32) == 128 * 8 * 4      # 8 segments of 4096 vectors
+    assert lse(1, 65536, _lib.F32) == 1 * 32 * 4          # capped by the segment size
+    assert lse(300, 131072, _lib.F32) == 300 * 4 * 4      # long rows: up to 511 rows
+    assert lse(384, 32768, _lib.F32) == 0                 # not long enough for that
+    assert lse(4, 1000, _lib.F32) == 0                    # too short to split
+    assert lse(4, 65537, _lib.F32) == 0                   # not whole 16-byte vectors
+    assert lse(4, 65536, 9) == 0 and lse(0, 65536, _lib.F32) == 0
+    assert red(128, 131072, 1, _lib.F32, _lib.REDUCE_MEAN) == 128 * 8 * 4
+    assert red(128, 131072, 1, _lib.F32, _lib.REDUCE_MAX) == 128 * 8 * (8 + 4)
+    assert red(128, 131072, 1, _lib.F16, _lib.REDUCE_ARGMAX) == 128 * 8 * (8 + 2)
+    assert red(300, 131072, 1, _lib.F32, _lib.REDUCE_MEAN) == 0  # long rows: logsumexp only
+    assert red(128, 131072, 4, _lib.F32, _lib.REDUCE_MEAN) == 0  # middle axis: not split
+    try:
+        _lib.tune_override(_lib.OP_LOGSUMEXP, 64, 0, 0)
+        assert _lib.logsumexp_workspace_bytes(128, 131072, _lib.F32) == 0
+    finally:
+        _lib.tune_override(_lib.OP_LOGSUMEXP, 0, 0, 0)
+    assert _lib.logsumexp_workspace_bytes(128, 131072, _lib.F32) == 128 * 8 * 4
+
+
+def test_split_entry_points_check_arguments():
+    _expect(_lib.E_INVALID, "vbh_logsumexp_fwd_ws", 16, 16, 4, 4, _lib.F32, _lib.F32, 16, -1,
+            None, match="workspace")
+    _expect(_lib.E_INVALID, "vbh_reduce_fwd_ws", 16, 16, 16, 4, 8, 1, _lib.F32, _lib.F32, 1, 16,
+            -1, None, match="workspace")
+    _expect(_lib.E_DTYPE, "vbh_logsumexp_fwd_ws", 16, 16, 4, 4, _lib.F32, _lib.F16, 16, 64, None)
+    _expect(_lib.E_RANGE, "vbh_reduce_fwd_ws", 16, 16, 16, 1 << 62, 64, 1, _lib.F32, _lib.F32, 1,
+            16, 64, None)
