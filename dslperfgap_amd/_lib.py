@@ -60,6 +60,12 @@ SIGNATURES = {
         [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _f32, _f32, _i64, _i64,
          _i64, _i64, _i32, _i32, _vp],
     ),
+    "vbh_cross_entropy_fwd_ws": (
+        _i32,
+        [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _f32, _f32, _i64, _i64,
+         _i64, _i64, _i32, _i32, _vp, _i64, _vp],
+    ),
+    "vbh_cross_entropy_workspace_bytes": (_i64, [_i64, _i64, _i64, _i32]),
     "vbh_cross_entropy_bwd": (
         _i32,
         [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _f32,
@@ -78,7 +84,8 @@ SIGNATURES = {
 FAST_ENTRY_POINTS = (
     "vbh_layer_norm_fwd", "vbh_rms_norm_fwd", "vbh_softmax_fwd", "vbh_softmax_dim_fwd",
     "vbh_logsumexp_fwd", "vbh_logsumexp_fwd_ws", "vbh_cross_entropy_fwd",
-    "vbh_cross_entropy_bwd", "vbh_reduce_fwd", "vbh_reduce_fwd_ws", "vbh_stream_copy",
+    "vbh_cross_entropy_fwd_ws", "vbh_cross_entropy_bwd", "vbh_reduce_fwd", "vbh_reduce_fwd_ws",
+    "vbh_stream_copy",
 )
 
 
@@ -164,12 +171,20 @@ def tune_override(op: int, tpr: int = 0, block: int = 0, flags: int = 0) -> None
     # an overridden geometry turns the row split off (and back on when cleared)
     logsumexp_workspace_bytes.cache_clear()
     reduce_workspace_bytes.cache_clear()
+    cross_entropy_workspace_bytes.cache_clear()
 
 
 @functools.lru_cache(maxsize=4096)
 def logsumexp_workspace_bytes(rows: int, cols: int, in_dtype: int) -> int:
     """Workspace bytes that split a logsumexp launch (0: no split)."""
     return lib().vbh_logsumexp_workspace_bytes(rows, cols, in_dtype)
+
+
+@functools.lru_cache(maxsize=4096)
+def cross_entropy_workspace_bytes(n_rows: int, n_cols: int, block_size: int,
+                                  logits_dtype: int) -> int:
+    """Workspace bytes that split a cross-entropy forward launch (0: no split)."""
+    return lib().vbh_cross_entropy_workspace_bytes(n_rows, n_cols, block_size, logits_dtype)
 
 
 @functools.lru_cache(maxsize=4096)

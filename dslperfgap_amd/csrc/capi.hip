@@ -140,31 +140,40 @@ int fill_it(int it, int64_t nvec, int64_t units) {
 constexpr int64_t kWriteThroughMinBytes = int64_t(32) << 20;
 
 // Few wide rows leave CUs idle when each row has one row group (128 fp32 rows
-// of 131072 columns: 128 workgroups on 256 CUs).  The read-only row
-// reductions (logsumexp, mean / max / argmax) then split every row into
-// `segs` equal segments: a first launch reduces the [rows * segs, cols / segs]
-// view into a caller-provided workspace, a second combines each row's
-// segments.  On MI355X (fp32 logsumexp, time per call of both launches):
-// 128 x 131072 27.7 -> 15.5 us, 64 x 131072 18.9 -> 10.8, 32 x 262144
-// 33.8 -> 10.8; 512 x 32768 is better unsplit (14.7 vs 15.3-16.2).  The
-// register-resident logsumexp row kernel also gains on longer rows at up to
-// 512 rows (fp32 256 x 65536 3770 -> 4380 GB/s, 335 x 50000 3132 -> 3772,
-// fp16 256 x 131072 3419 -> 4438; 384 x 32768: 3929 unsplit, 3569-3848
-// split); the streaming mean does not (fp32 256 x 65536: 5217 unsplit,
-// 4840-5004 split).
-constexpr int64_t kSplitMaxRows = 256;   // split only launches of fewer rows
-constexpr int64_t kSplitMaxRowsLong = 512;  // ... or, logsumexp, of fewer long rows
-constexpr int64_t kSplitLongVecs = 12288;   // a long row's 16-byte vectors, at least
-constexpr int64_t kSplitTarget = 1024;  // segments per launch to aim for
-constexpr int64_t kSplitMinVecs = 512;  // 16-byte vectors per segment, at least
+// of 131072 columns: 128 workgroups on 256 CUs), and one workgroup streams a
+// long row at about 20 GB/s.  The read-only row reductions (logsumexp, cross
+// entropy with one column block per row, mean / max / argmax) then split every
+// row into `segs` equal segments: a first launch reduces the
+// [rows * segs, cols / segs] view into a caller-provided workspace, a second
+// combines each row's segments.  On MI355X, time per call of both launches:
+// fp32 logsumexp 128 x 131072 27.7 -> 15.5 us, 32 x 262144 33.8 -> 10.8;
+// cross entropy fp32 64 x 128256 26.8 -> 16.4, 1 x 128256 24.8 -> 15.7.  The
+// split costs a second launch and, in Python, a workspace allocation, so
+// shorter rows stay unsplit: cross entropy fp32 64 x 50304 (200 KB rows)
+// 11.6 us unsplit, 14.9 split.  The register-resident logsumexp and cross
+// entropy row kernels also gain at 256-511 rows of at least 12288 vectors,
+// (fp32, interleaved: logsumexp 256 x 65536 3778 -> 4377 GB/s, 335 x 50000
+// 3126 -> 4202, 400 x 65536 3780 -> 4923; cross entropy 335 x 50000 2965 ->
+// 3650, 400 x 65536 3695 -> 4387, but 256 x 65536 3734 -> 3584, so cross
+// entropy starts above 256 rows; 384 x 32768 logsumexp: 3929 unsplit,
+// 3569-3848 split); the streaming mean does not (fp32 256 x 65536: 5217
+// unsplit, 4840-5004 split).
+constexpr int64_t kSplitMaxRows = 256;      // split launches of fewer rows ...
+constexpr int64_t kSplitRowVecs = 16384;    // ... of 16-byte vectors per row, at least
+constexpr int64_t kSplitMaxRowsLong = 512;  // two-round launches (logsumexp, CE) ...
+constexpr int64_t kSplitLongVecs = 12288;   // ... of rows of at least this many vectors
+constexpr int64_t kSplitTarget = 1024;      // segments per launch to aim for
+constexpr int64_t kSplitMinVecs = 512;      // 16-byte vectors per segment, at least
 constexpr int kSplitMaxSegs = 64;
 
 // Segments per row (a power of two dividing the row's vectors), or 1.
-// `long_rows`: the op also splits up to kSplitMaxRowsLong rows of long rows.
-int split_segments(int64_t rows, int64_t nvec, bool long_rows = false) {
-  const int64_t max_rows =
-      long_rows && nvec >= kSplitLongVecs ? kSplitMaxRowsLong : kSplitMaxRows;
-  if (rows <= 0 || rows >= max_rows) return 1;
+// `long_from`: the op also splits launches of long_from to 511 rows of long
+// rows (0: it does not).
+int split_segments(int64_t rows, int64_t nvec, int64_t long_from = 0) {
+  const bool few = rows > 0 && rows < kSplitMaxRows && nvec >= kSplitRowVecs;
+  const bool two_rounds = long_from > 0 && rows >= long_from && rows < kSplitMaxRowsLong &&
+                          nvec >= kSplitLongVecs;
+  if (!few && !two_rounds) return 1;
   int segs = 1;
   while (segs < kSplitMaxSegs && rows * segs < kSplitTarget && nvec % (2 * segs) == 0 &&
          nvec / (2 * segs) >= kSplitMinVecs)
@@ -445,7 +454,7 @@ int64_t vbh_logsumexp_workspace_bytes(int64_t rows, int64_t cols, int in_dtype) 
   const int vn = 16 / elt_size(in_dtype);
   if (cols % vn != 0 || g_tpr[VBH_OP_LOGSUMEXP].load() || g_block[VBH_OP_LOGSUMEXP].load())
     return 0;
-  const int segs = split_segments(rows, cols / vn, true);
+  const int segs = split_segments(rows, cols / vn, kSplitMaxRows);
   return segs > 1 ? rows * segs * static_cast<int64_t>(sizeof(float)) : 0;
 }
 
@@ -468,7 +477,7 @@ int vbh_logsumexp_fwd_ws(const void* x, void* y, int64_t rows, int64_t cols, int
   if (need > 0 && vec_ok && workspace != nullptr && workspace_bytes >= need &&
       aligned16(workspace)) {
     // segment results in fp32, then a logsumexp over each row's segments
-    const int segs = split_segments(rows, cols / vn, true);
+    const int segs = split_segments(rows, cols / vn, kSplitMaxRows);
     const int64_t units = rows * segs;
     const int seg_cols = static_cast<int>(cols / segs);
     const Geometry g1 = geometry_for(VBH_OP_LOGSUMEXP, seg_cols, vn, units);
@@ -490,18 +499,35 @@ int vbh_logsumexp_fwd(const void* x, void* y, int64_t rows, int64_t cols, int in
   return vbh_logsumexp_fwd_ws(x, y, rows, cols, in_dtype, out_dtype, nullptr, 0, stream);
 }
 
-int vbh_cross_entropy_fwd(const void* logits, const void* labels, int logits_dtype,
-                          int label_dtype, void* loss, void* lse, void* z_loss,
-                          int64_t n_rows, int64_t n_cols, int64_t row_stride, float smoothing,
-                          float logit_scale, float lse_square_scale, int64_t ignored_index,
-                          int64_t total_classes, int64_t class_start_idx, int64_t block_size,
-                          int has_smoothing, int split, void* stream) {
+int64_t vbh_cross_entropy_workspace_bytes(int64_t n_rows, int64_t n_cols, int64_t block_size,
+                                          int logits_dtype) {
+  if (!is_float(logits_dtype) || n_rows <= 0 || n_cols <= 0 || n_cols > (int64_t(1) << 30) ||
+      block_size < n_cols)  // one column block per row only
+    return 0;
+  const int vn = 16 / elt_size(logits_dtype);
+  if (n_cols % vn != 0 || g_tpr[VBH_OP_CROSS_ENTROPY].load() ||
+      g_block[VBH_OP_CROSS_ENTROPY].load())
+    return 0;
+  const int segs = split_segments(n_rows, n_cols / vn, kSplitMaxRows + 1);
+  // segment loss, lse and (unused) z_loss
+  return segs > 1 ? 3 * n_rows * segs * static_cast<int64_t>(sizeof(float)) : 0;
+}
+
+int vbh_cross_entropy_fwd_ws(const void* logits, const void* labels, int logits_dtype,
+                             int label_dtype, void* loss, void* lse, void* z_loss,
+                             int64_t n_rows, int64_t n_cols, int64_t row_stride, float smoothing,
+                             float logit_scale, float lse_square_scale, int64_t ignored_index,
+                             int64_t total_classes, int64_t class_start_idx, int64_t block_size,
+                             int has_smoothing, int split, void* workspace,
+                             int64_t workspace_bytes, void* stream) {
   if (!is_float(logits_dtype))
     return fail(VBH_E_DTYPE, "cross_entropy_fwd: unsupported logits dtype %d", logits_dtype);
   if (label_dtype != kI32 && label_dtype != kI64)
     return fail(VBH_E_DTYPE, "cross_entropy_fwd: labels must be int32 or int64");
   if (n_rows < 0 || n_cols < 0) return fail(VBH_E_INVALID, "cross_entropy_fwd: negative size");
   if (block_size <= 0) return fail(VBH_E_INVALID, "cross_entropy_fwd: BLOCK_SIZE must be > 0");
+  if (workspace_bytes < 0)
+    return fail(VBH_E_INVALID, "cross_entropy_fwd: negative workspace size");
   if (n_cols > (int64_t(1) << 30))
     return fail(VBH_E_RANGE, "cross_entropy_fwd: n_cols too large");
   if (row_stride < n_cols) return fail(VBH_E_INVALID, "cross_entropy_fwd: row_stride < n_cols");
@@ -513,9 +539,7 @@ int vbh_cross_entropy_fwd(const void* logits, const void* labels, int logits_dty
   const int vn = 16 / elt_size(logits_dtype);
   const bool vec_ok =
       n_cols % vn == 0 && bs % vn == 0 && row_stride % vn == 0 && aligned16(logits);
-  const int64_t segments = mul_sat(n_rows, ncb);
-  const Geometry g = geometry_for(VBH_OP_CROSS_ENTROPY, bs, vec_ok ? vn : 1, segments);
-  if (int rc = check_grid(segments, g)) return rc;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
   CeArgs a;
   a.logits = logits;
   a.labels = labels;
@@ -537,8 +561,45 @@ int vbh_cross_entropy_fwd(const void* logits, const void* labels, int logits_dty
   a.class_start = class_start_idx;
   a.has_smoothing = has_smoothing != 0;
   a.split = split != 0;
-  return hip_status(launch_cross_entropy_fwd(a, g, static_cast<hipStream_t>(stream)),
-                    "cross_entropy_fwd launch");
+  const int64_t need =
+      vbh_cross_entropy_workspace_bytes(n_rows, n_cols, block_size, logits_dtype);
+  if (need > 0 && vec_ok && workspace != nullptr && workspace_bytes >= need &&
+      aligned16(workspace)) {
+    // first stage: the row's segments as column blocks with SPLIT semantics
+    const int segs = split_segments(n_rows, n_cols / vn, kSplitMaxRows + 1);
+    const int64_t units = n_rows * segs;
+    const Geometry g1 =
+        geometry_for(VBH_OP_CROSS_ENTROPY, n_cols / segs, vn, units);
+    if (int rc = check_grid(units, g1)) return rc;
+    CeArgs p = a;
+    p.loss = static_cast<float*>(workspace);
+    p.lse = p.loss + units;
+    p.z_loss = p.lse + units;
+    p.block_size = static_cast<int>(n_cols / segs);
+    p.ncb = segs;
+    p.split = 1;
+    p.empty_neg_inf = 1;
+    hipError_t e = launch_cross_entropy_fwd(p, g1, s);
+    if (e == hipSuccess) e = launch_cross_entropy_combine(a, p.loss, p.lse, segs, s);
+    return hip_status(e, "cross_entropy_fwd launch");
+  }
+  const int64_t segments = mul_sat(n_rows, ncb);
+  const Geometry g = geometry_for(VBH_OP_CROSS_ENTROPY, bs, vec_ok ? vn : 1, segments);
+  if (int rc = check_grid(segments, g)) return rc;
+  return hip_status(launch_cross_entropy_fwd(a, g, s), "cross_entropy_fwd launch");
+}
+
+int vbh_cross_entropy_fwd(const void* logits, const void* labels, int logits_dtype,
+                          int label_dtype, void* loss, void* lse, void* z_loss,
+                          int64_t n_rows, int64_t n_cols, int64_t row_stride, float smoothing,
+                          float logit_scale, float lse_square_scale, int64_t ignored_index,
+                          int64_t total_classes, int64_t class_start_idx, int64_t block_size,
+                          int has_smoothing, int split, void* stream) {
+  return vbh_cross_entropy_fwd_ws(logits, labels, logits_dtype, label_dtype, loss, lse, z_loss,
+                                  n_rows, n_cols, row_stride, smoothing, logit_scale,
+                                  lse_square_scale, ignored_index, total_classes,
+                                  class_start_idx, block_size, has_smoothing, split, nullptr, 0,
+                                  stream);
 }
 
 int vbh_cross_entropy_bwd(const void* dloss, const void* logits, const void* lse,

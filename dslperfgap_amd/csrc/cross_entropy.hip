@@ -31,6 +31,10 @@ struct CeScalars {
   float one_minus_smoothing, smooth_negative, two_lse_square_scale;
   int64_t ignored_index, class_start;
   int has_smoothing, split;
+  // first stage of a split row: an all -inf segment (no NaN) gets lse = -inf,
+  // as a logsumexp would, not the golden's NaN; the second stage applies the
+  // golden's rule to the whole row
+  int empty_neg_inf;
 };
 
 CeScalars make_scalars(float smoothing, float logit_scale, float lse_square_scale,
@@ -49,6 +53,7 @@ CeScalars make_scalars(float smoothing, float logit_scale, float lse_square_scal
   c.class_start = class_start;
   c.has_smoothing = has_smoothing;
   c.split = split;
+  c.empty_neg_inf = 0;
   return c;
 }
 
@@ -165,10 +170,12 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
     }
   const float s = group_allreduce<Sum>(se[0], tpr, lds[1]);
   float sum_logits = 0.f;
-  if (c.has_smoothing) sum_logits = group_allreduce<Sum>(sl[0], tpr, lds[2]);
+  if (c.has_smoothing || c.empty_neg_inf) sum_logits = group_allreduce<Sum>(sl[0], tpr, lds[2]);
 
   if (live && g == 0) {
-    const float lse = fast_log(s) + m;
+    float lse = fast_log(s) + m;
+    // all -inf (the sum of logits is -inf, not NaN): -inf in a first stage
+    if (c.empty_neg_inf && m == kNegInf && sum_logits == sum_logits) lse = kNegInf;
     ce_store(lse, sum_logits, in_block, logit_label, ignored, c, loss, lse_out, z_out,
              static_cast<int64_t>(cb) * n_rows + row);
   }
@@ -224,7 +231,8 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_stream(
   // Golden lse = log(sum(exp(L - max))) + max with a NaN-propagating max: a NaN
   // logit, a +inf max (inf - inf) or an all -inf segment (-inf - -inf) give NaN.
   const bool has_nan = nan != 0.f || (gl != gl);
-  const float lse = (has_nan || !finite) ? __builtin_nanf("") : fast_log(gs) + gm;
+  float lse = (has_nan || !finite) ? __builtin_nanf("") : fast_log(gs) + gm;
+  if (c.empty_neg_inf && !has_nan && gm == kNegInf) lse = kNegInf;  // as in ce_fwd_rows
   const int64_t label = read_label(labels, label_i64, row);
   const bool ignored = label == c.ignored_index;
   const int64_t adj = label - c.class_start;
@@ -234,6 +242,58 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_stream(
     logit_label = static_cast<float>(logits[row * ld + adj]) * c.logit_scale;
   ce_store(lse, gl, in_block, logit_label, ignored, c, loss, lse_out, z_out,
            static_cast<int64_t>(cb) * n_rows + row);
+}
+
+// Second stage of a split row (one column block per row, cut into `segs`
+// segments that a first stage reduced with SPLIT semantics into seg_loss /
+// seg_lse at flat index k * n_rows + row).  One lane per row: the row's lse is
+// the logsumexp of its segments' lse under the golden's rule (a NaN logit, a
+// +inf or an all -inf row give NaN: every segment lse NaN or -inf), and the
+// loss adds the lse term the first stage left out (pytorch_impl.py:54-70):
+// lse where the row holds the label, smoothing * lse elsewhere with smoothing,
+// 0 with SPLIT; plus z = lse_square_scale * lse^2 without SPLIT.  The segment
+// losses sum to the rest of the golden's loss (-logit_label and the smoothing
+// sums are additive over segments).
+__global__ __launch_bounds__(256) void ce_combine(
+    const float* __restrict__ seg_loss, const float* __restrict__ seg_lse,
+    const void* __restrict__ labels, int label_i64, float* __restrict__ loss,
+    float* __restrict__ lse_out, float* __restrict__ z_out, int64_t n_rows, int n_cols,
+    int segs, CeScalars c) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (row >= n_rows) return;
+  float mx = kNegInf, rest = 0.f;
+  bool nan = false;
+  for (int k = 0; k < segs; ++k) {
+    const float v = seg_lse[static_cast<int64_t>(k) * n_rows + row];
+    nan |= v != v;
+    mx = fmaxf(mx, v);
+    rest += seg_loss[static_cast<int64_t>(k) * n_rows + row];
+  }
+  float lse;
+  if (nan || mx == kNegInf) {
+    lse = __builtin_nanf("");
+  } else {
+    float s = 0.f;
+    for (int k = 0; k < segs; ++k)
+      s += fast_exp(seg_lse[static_cast<int64_t>(k) * n_rows + row] - mx);
+    lse = fast_log(s) + mx;
+  }
+  lse_out[row] = lse;
+  const int64_t label = read_label(labels, label_i64, row);
+  float l = 0.f, z = 0.f;
+  if (label != c.ignored_index) {
+    const int64_t adj = label - c.class_start;
+    const bool in_row = adj >= 0 && adj < n_cols;
+    if (!c.split) {
+      const float base = in_row ? lse : (c.has_smoothing ? c.smoothing * lse : 0.f);
+      z = c.lse_square_scale * lse * lse;
+      l = base + rest + z;
+    } else {
+      l = rest;
+    }
+  }
+  loss[row] = l;
+  z_out[row] = z;
 }
 
 // Backward: elementwise over the rows.  One 256-lane workgroup per tile of
@@ -286,9 +346,10 @@ __global__ __launch_bounds__(kBwdLanes) void ce_bwd_tiles(
 
 hipError_t launch_cross_entropy_fwd(const CeArgs& a, const Geometry& g, hipStream_t s) {
   hipError_t err = hipErrorInvalidValue;
-  const CeScalars c =
+  CeScalars c =
       make_scalars(a.smoothing, a.logit_scale, a.lse_square_scale, a.total_classes,
                    a.ignored_index, a.class_start, a.has_smoothing, a.split);
+  c.empty_neg_inf = a.empty_neg_inf;
   const int64_t nseg = a.n_rows * a.ncb;
   dispatch_float_type(a.logits_dt, [&](auto tt) {
     using T = typename decltype(tt)::type;
@@ -322,6 +383,17 @@ hipError_t launch_cross_entropy_fwd(const CeArgs& a, const Geometry& g, hipStrea
     else go(std::integral_constant<int, VN>{});
   });
   return err;
+}
+
+hipError_t launch_cross_entropy_combine(const CeArgs& a, const float* seg_loss,
+                                        const float* seg_lse, int segs, hipStream_t s) {
+  const CeScalars c =
+      make_scalars(a.smoothing, a.logit_scale, a.lse_square_scale, a.total_classes,
+                   a.ignored_index, a.class_start, a.has_smoothing, a.split);
+  hipLaunchKernelGGL(ce_combine, dim3((a.n_rows + 255) / 256), dim3(256), 0, s, seg_loss,
+                     seg_lse, a.labels, a.label_i64, a.loss, a.lse, a.z_loss, a.n_rows,
+                     a.n_cols, segs, c);
+  return hipGetLastError();
 }
 
 hipError_t launch_cross_entropy_bwd(const CeBwdArgs& a, hipStream_t s) {

@@ -158,8 +158,14 @@ struct CeArgs {
   int64_t class_start;
   int has_smoothing;
   int split;
+  int empty_neg_inf = 0;  // first stage of a split row (see ce_combine)
 };
 hipError_t launch_cross_entropy_fwd(const CeArgs& a, const Geometry& g, hipStream_t s);
+// Second stage of a split row: `a` describes the caller's launch (one column
+// block per row); seg_loss / seg_lse hold the first stage's `segs` segments
+// per row at flat index k * n_rows + row.
+hipError_t launch_cross_entropy_combine(const CeArgs& a, const float* seg_loss,
+                                        const float* seg_lse, int segs, hipStream_t s);
 
 struct CeBwdArgs {
   const float* dloss;

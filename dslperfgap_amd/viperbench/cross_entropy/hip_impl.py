@@ -27,7 +27,7 @@ if _ROOT not in sys.path:
 
 import torch  # noqa: E402
 
-from dslperfgap_amd import _bridge  # noqa: E402
+from dslperfgap_amd import _bridge, _lib  # noqa: E402
 
 
 def _labels(labels, n_rows, what):
@@ -66,12 +66,17 @@ def cross_entropy_fwd(
     lse = _bridge.empty(logits, (n_rows, n_cols), torch.float32)
     z_loss = _bridge.empty(logits, (n_rows, n_cols), torch.float32)
     row_stride = logits.stride(0) if n_rows > 1 else n_cols
-    _bridge.launch("vbh_cross_entropy_fwd", dev, _bridge.ptr(logits), _bridge.ptr(labels), dt,
-                   _bridge.LABEL_CODES[labels.dtype], _bridge.ptr(loss), _bridge.ptr(lse),
-                   _bridge.ptr(z_loss), n_rows, n_cols, row_stride, float(smoothing),
-                   float(logit_scale), float(lse_square_scale), int(ignored_index),
-                   int(total_classes), int(class_start_idx), int(BLOCK_SIZE),
-                   int(bool(HAS_SMOOTHING)), int(bool(SPLIT)))
+    args = (logits.data_ptr(), labels.data_ptr(), dt, _bridge.LABEL_CODES[labels.dtype],
+            loss.data_ptr(), lse.data_ptr(), z_loss.data_ptr(), n_rows, n_cols, row_stride,
+            float(smoothing), float(logit_scale), float(lse_square_scale), int(ignored_index),
+            int(total_classes), int(class_start_idx), int(BLOCK_SIZE), int(bool(HAS_SMOOTHING)),
+            int(bool(SPLIT)))
+    ws_bytes = _lib.cross_entropy_workspace_bytes(n_rows, n_cols, int(BLOCK_SIZE), dt)
+    if ws_bytes:  # few long rows in one column block: split each row over workgroups
+        ws = _bridge.empty(logits, (ws_bytes,), torch.uint8)
+        _bridge.launch("vbh_cross_entropy_fwd_ws", dev, *args, ws.data_ptr(), ws_bytes)
+    else:
+        _bridge.launch("vbh_cross_entropy_fwd", dev, *args)
     return loss, lse, z_loss
 
 

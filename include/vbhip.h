@@ -137,6 +137,29 @@ int vbh_cross_entropy_fwd(const void* logits, const void* labels, int logits_dty
                           int64_t class_start_idx, int64_t block_size,
                           int has_smoothing, int split, void* stream);
 
+/* vbh_cross_entropy_fwd with a caller-provided device workspace (16-byte
+ * aligned).  When each row is one column block (block_size >= n_cols) and the
+ * launch has few long rows, each row is cut into segments reduced in parallel
+ * as column blocks with SPLIT semantics -- the vocab-parallel form of the
+ * golden (pytorch_impl.py:38-52: a row's loss is the logsumexp of its blocks'
+ * lse plus the sum of their SPLIT losses) -- then one lane per row combines
+ * them into the caller's outputs, with the golden's NaN rule for the whole
+ * row.  Workspace size from vbh_cross_entropy_workspace_bytes; fallback and
+ * reuse as for vbh_logsumexp_fwd_ws. */
+int vbh_cross_entropy_fwd_ws(const void* logits, const void* labels, int logits_dtype,
+                             int label_dtype, void* loss, void* lse, void* z_loss,
+                             int64_t n_rows, int64_t n_cols, int64_t row_stride,
+                             float smoothing, float logit_scale, float lse_square_scale,
+                             int64_t ignored_index, int64_t total_classes,
+                             int64_t class_start_idx, int64_t block_size,
+                             int has_smoothing, int split, void* workspace,
+                             int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes vbh_cross_entropy_fwd_ws splits such a launch with (0: no
+ * split). */
+int64_t vbh_cross_entropy_workspace_bytes(int64_t n_rows, int64_t n_cols, int64_t block_size,
+                                          int logits_dtype);
+
 /* Cross-entropy backward: dlogits[r, c] = dloss[r] * logit_scale *
  * (p + 2 * lse_square_scale * lse[r] * p - target), p = exp(logit_scale * x - lse[r]).
  * dloss is read at dloss[r * dloss_stride]; ignored rows get dlogits = 0 * (...).

@@ -702,7 +702,7 @@ def test_vocab_parallel_cross_entropy_at_c4():
 # ---------------------------------------------------------------------------
 # logsumexp of few long rows: the split path
 # ---------------------------------------------------------------------------
-@pytest.mark.parametrize("rows,cols", [(1, 65536), (3, 131072), (33, 32768), (255, 16384),
+@pytest.mark.parametrize("rows,cols", [(1, 262144), (3, 131072), (33, 131072), (255, 131072),
                                        (300, 131072)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_split_logsumexp(rows, cols, dtype):
@@ -740,3 +740,72 @@ def test_split_logsumexp_matches_the_unsplit_kernel():
                   torch.cuda.current_stream().cuda_stream)
         outs.append(y.cpu())
     assert torch.allclose(outs[0], outs[1], atol=1e-5, rtol=1e-6), (outs[0] - outs[1]).abs().max()
+
+
+# ---------------------------------------------------------------------------
+# cross-entropy forward of few long rows (one column block): the split path
+# ---------------------------------------------------------------------------
+CE_SPLIT_PARAMS = [
+    dict(smoothing=0.0, logit_scale=1.0, lse_square_scale=0.0, HAS_SMOOTHING=False, SPLIT=False),
+    dict(smoothing=0.1, logit_scale=0.7, lse_square_scale=1e-4, HAS_SMOOTHING=True, SPLIT=False),
+    dict(smoothing=0.0, logit_scale=1.3, lse_square_scale=1e-4, HAS_SMOOTHING=False, SPLIT=True),
+    dict(smoothing=0.2, logit_scale=1.0, lse_square_scale=0.0, HAS_SMOOTHING=True, SPLIT=True),
+]
+
+
+@pytest.mark.parametrize("rows,cols,dtype", [(1, 65536, torch.float32), (7, 131072, torch.float32),
+                                             (100, 131072, torch.bfloat16),
+                                             (300, 131072, torch.float32),
+                                             (33, 262144, torch.float16)])
+@pytest.mark.parametrize("pi", range(len(CE_SPLIT_PARAMS)))
+def test_split_cross_entropy(rows, cols, dtype, pi):
+    """Launches that split every row match the oracle on every output: labels
+    in and out of range (class_start shift), an ignored row, int32 labels, and
+    the golden's row-level special values -- an all -inf segment inside a
+    finite row stays finite, an all -inf row, a +inf or a NaN give NaN."""
+    p = CE_SPLIT_PARAMS[pi]
+    code = {torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}[dtype]
+    assert _lib.cross_entropy_workspace_bytes(rows, cols, 1 << 18, code) > 0
+    g = _g(500 + rows + pi)
+    logits = (2 * torch.randn(rows, cols, generator=g)).to(dtype)
+    start = cols // 5
+    labels = torch.randint(0, cols + start, (rows,), generator=g).to(torch.int32)
+    if rows > 4:
+        labels[4] = -100
+        logits[0, : cols // 2] = float("-inf")   # whole segments of -inf, finite row
+        labels[0] = start + cols - 3
+        logits[1, :] = float("-inf")
+        logits[2, cols // 3] = float("inf")
+        logits[3, 11] = float("nan")
+    args = dict(ignored_index=-100, total_classes=cols + start, class_start_idx=start,
+                BLOCK_SIZE=1 << 18, **p)
+    got = cross_entropy_fwd(logits.to(DEV), labels.to(DEV), **args)
+    want = ref.cross_entropy_fwd(logits, labels, **args)
+    for k, (t, w) in enumerate(zip(got, want)):
+        check(t.reshape(-1)[:rows], w.reshape(-1)[:rows], torch.float32,
+              what=f"split ce[{k}] {rows}x{cols} {dtype} {p}")
+    if rows > 4:
+        assert torch.isfinite(got[1].reshape(-1)[0]).item()   # the masked row's lse
+
+
+def test_split_cross_entropy_matches_the_unsplit_kernel():
+    """One launch through vbh_cross_entropy_fwd_ws with and without a workspace:
+    the split and unsplit results agree to fp32 rounding."""
+    rows, cols = 9, 131072
+    g = _g(520)
+    logits = (2 * torch.randn(rows, cols, generator=g)).to(DEV)
+    labels = torch.randint(0, cols, (rows,), generator=g).to(DEV)
+    need = _lib.cross_entropy_workspace_bytes(rows, cols, cols, _lib.F32)
+    assert need > 0
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    outs = []
+    for w, nb in ((ws, need), (None, 0)):
+        o = [torch.empty(rows, device=DEV) for _ in range(3)]
+        _lib.call("vbh_cross_entropy_fwd_ws", logits.data_ptr(), labels.data_ptr(), _lib.F32,
+                  _lib.I64, o[0].data_ptr(), o[1].data_ptr(), o[2].data_ptr(), rows, cols, cols,
+                  0.1, 1.0, 1e-4, -100, cols, 0, cols, 1, 0,
+                  w.data_ptr() if w is not None else None, nb,
+                  torch.cuda.current_stream().cuda_stream)
+        outs.append([t.cpu() for t in o])
+    for a, b in zip(*outs):
+        assert torch.allclose(a, b, atol=1e-5, rtol=1e-5), (a - b).abs().max()

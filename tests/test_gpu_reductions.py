@@ -161,7 +161,7 @@ def test_reduce_geometry_overrides(tpr, block):
 # ---------------------------------------------------------------------------
 # few long rows: the split path (segments reduced in parallel, then combined)
 # ---------------------------------------------------------------------------
-SPLIT_SHAPES = [(1, 65536), (3, 131072), (17, 32768), (200, 16384)]
+SPLIT_SHAPES = [(1, 131072), (3, 131072), (17, 262144), (200, 131072)]
 
 
 @pytest.mark.parametrize("rows,cols", SPLIT_SHAPES)

@@ -233,10 +233,10 @@ def test_fast_binding_refuses_calls_before_bind():
 
 
 def test_split_workspace_sizes():
-    """The row split is a pure function of the launch shape: few long rows split
-    (segments of >= 512 16-byte vectors, a power of two per row, about 1024
-    segments per launch), many rows or short rows do not, and an overridden
-    geometry turns it off."""
+    """The row split is a pure function of the launch shape: few rows of at
+    least 256 KiB split (segments of >= 512 16-byte vectors, a power of two per
+    row, about 1024 segments per launch), many rows or shorter rows do not, and
+    an overridden geometry turns it off."""
     h = _lib.lib()
     lse, red = h.vbh_logsumexp_workspace_bytes, h.vbh_reduce_workspace_bytes
     assert lse(8192, 4096, _lib.F32) == 0                 # many rows
@@ -244,6 +244,8 @@ def test_split_workspace_sizes():
     assert lse(1, 65536, _lib.F32) == 1 * 32 * 4          # capped by the segment size
     assert lse(300, 131072, _lib.F32) == 300 * 4 * 4      # long rows: up to 511 rows
     assert lse(384, 32768, _lib.F32) == 0                 # not long enough for that
+    assert lse(64, 50304, _lib.F32) == 0                  # 200 KB rows: not worth a split
+    assert lse(1, 65536, _lib.F16) == 0                   # 128 KB row
     assert lse(4, 1000, _lib.F32) == 0                    # too short to split
     assert lse(4, 65537, _lib.F32) == 0                   # not whole 16-byte vectors
     assert lse(4, 65536, 9) == 0 and lse(0, 65536, _lib.F32) == 0
@@ -252,6 +254,10 @@ def test_split_workspace_sizes():
     assert red(128, 131072, 1, _lib.F16, _lib.REDUCE_ARGMAX) == 128 * 8 * (8 + 2)
     assert red(300, 131072, 1, _lib.F32, _lib.REDUCE_MEAN) == 0  # long rows: logsumexp only
     assert red(128, 131072, 4, _lib.F32, _lib.REDUCE_MEAN) == 0  # middle axis: not split
+    ce = h.vbh_cross_entropy_workspace_bytes
+    assert ce(64, 128256, 1 << 17, _lib.F32) == 3 * 64 * 16 * 4  # one block per row
+    assert ce(64, 128256, 32768, _lib.F32) == 0           # several column blocks: not split
+    assert ce(64, 50304, 65536, _lib.F32) == 0
     try:
         _lib.tune_override(_lib.OP_LOGSUMEXP, 64, 0, 0)
         assert _lib.logsumexp_workspace_bytes(128, 131072, _lib.F32) == 0
