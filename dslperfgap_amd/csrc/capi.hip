@@ -137,7 +137,19 @@ int fill_it(int it, int64_t nvec, int64_t units) {
 // nontemporal stores kept in the L2: RMSNorm bf16 8192 x 4096 +0.9%, softmax
 // fp32 16384 x 4096 +1.6%, softmax fp16 4096 x 32768 +4.3%, LayerNorm fp32
 // 4096 x 1024 (16 MiB out) -0.2%, RMSNorm bf16 1024 x 4096 (8 MiB out) -2.5%.
+// Only rows that are whole 128-byte L2 lines: where a line holds the end of
+// one row and the start of the next, the two halves are written through
+// separately, and the launch is slower than with L2 stores (softmax fp16
+// 50256 columns -5%, log_softmax fp16 -7%; rows of 50257 or 4097 columns
+// -7 to -24%).
 constexpr int64_t kWriteThroughMinBytes = int64_t(32) << 20;
+constexpr int64_t kLineBytes = 128;
+
+// Write-through suits a launch of `units` output rows, `out_bytes` in all.
+bool write_through_ok(int64_t out_bytes, int64_t units) {
+  return out_bytes >= kWriteThroughMinBytes && units > 0 && out_bytes % units == 0 &&
+         (out_bytes / units) % kLineBytes == 0;
+}
 
 // Few wide rows leave CUs idle when each row has one row group (128 fp32 rows
 // of 131072 columns: 128 workgroups on 256 CUs), and one workgroup streams a
@@ -181,6 +193,14 @@ int split_segments(int64_t rows, int64_t nvec, int64_t long_from = 0) {
   return segs;
 }
 
+// Rows whose length is not a multiple of the 16-byte vector (GPT-2's 50257
+// columns) run the MIS row kernels -- scalar head and tail, aligned vector
+// body -- instead of one scalar access per element, when every row of input
+// and output starts at the same offset within a vector (both buffers 16-byte
+// aligned, same row length) and the row fits the register-resident kernel.
+// MI355X, 50257 columns: fp32 log_softmax 2407 GB/s scalar, 4811 at 50256.
+constexpr int64_t kMisMinVecs = 4;  // shorter rows keep the scalar kernel
+
 // `units`: row groups of the launch (see fill_it); `out_bytes`: bytes it writes.
 Geometry geometry_for(int op, int64_t cols, int vec, int64_t units, int64_t out_bytes = 0) {
   const int over = g_flags[op].load();
@@ -195,7 +215,7 @@ Geometry geometry_for(int op, int64_t cols, int vec, int64_t units, int64_t out_
   if (g.persist && !(over & kFlagPersist) && g.tpr < kPersistMinTpr[op]) g.persist = false;
   const bool full_output =
       op == VBH_OP_LAYER_NORM || op == VBH_OP_RMS_NORM || op == VBH_OP_SOFTMAX;
-  bool wt = full_output && out_bytes >= kWriteThroughMinBytes;
+  bool wt = full_output && write_through_ok(out_bytes, units);
   if (over & kFlagWriteThrough) wt = true;
   if (over & kFlagNoWriteThrough) wt = false;
   g.wt = g.nt && wt;
@@ -221,6 +241,18 @@ int check_grid(int64_t units, const Geometry& g) {
 // multiple of tpr (and is at least tpr).  A tpr alone may come from the
 // heuristic while the size comes from vbh_tune_override.
 int fit_block(int block, int tpr) { return block < tpr ? tpr : block / tpr * tpr; }
+
+// Switch `g` (computed for `vn`-wide vectors) to the MIS kernel, or return
+// false when the launch must take the scalar kernel instead.
+bool use_mis(Geometry& g, int vn) {
+  if (g.stream || g.v != vn || vn == 1) return false;
+  g.mis = true;
+  if (g.tpr < vn) {  // every head / tail element needs its own lane
+    g.tpr = vn;
+    g.block = fit_block(g.block, vn);
+  }
+  return true;
+}
 
 // The reduction row kernel streams its row whatever the vectors per lane, so
 // its geometry has no register cap: it_target vectors per lane, with more
@@ -422,9 +454,12 @@ int vbh_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols, int in_d
   if (rows == 0 || cols == 0) return 0;
   if (!x || !y) return fail(VBH_E_INVALID, "softmax: null pointer");
   const int vn = 16 / elt_size(in_dtype);
-  const bool vec_ok = cols % vn == 0 && aligned16(x) && aligned16(y);
-  const Geometry g = geometry_for(VBH_OP_SOFTMAX, cols, vec_ok ? vn : 1, rows,
-                                  mul_sat(mul_sat(rows, cols), elt_size(out_dtype)));
+  const bool aligned = aligned16(x) && aligned16(y);
+  const bool vec_ok = cols % vn == 0 && aligned;
+  const bool mis_ok = !vec_ok && aligned && cols >= kMisMinVecs * vn;
+  const int64_t out_bytes = mul_sat(mul_sat(rows, cols), elt_size(out_dtype));
+  Geometry g = geometry_for(VBH_OP_SOFTMAX, cols, vec_ok || mis_ok ? vn : 1, rows, out_bytes);
+  if (mis_ok && !use_mis(g, vn)) g = geometry_for(VBH_OP_SOFTMAX, cols, 1, rows, out_bytes);
   if (int rc = check_grid(rows, g)) return rc;
   return hip_status(launch_softmax(x, y, rows, static_cast<int>(cols), in_dtype, out_dtype,
                                    log_mode, g, static_cast<hipStream_t>(stream)),
@@ -487,7 +522,9 @@ int vbh_logsumexp_fwd_ws(const void* x, void* y, int64_t rows, int64_t cols, int
     if (e == hipSuccess) e = launch_logsumexp(workspace, y, rows, segs, kF32, out_dtype, g2, s);
     return hip_status(e, "logsumexp launch");
   }
-  const Geometry g = geometry_for(VBH_OP_LOGSUMEXP, cols, vec_ok ? vn : 1, rows);
+  const bool mis_ok = !vec_ok && aligned16(x) && cols >= kMisMinVecs * vn;
+  Geometry g = geometry_for(VBH_OP_LOGSUMEXP, cols, vec_ok || mis_ok ? vn : 1, rows);
+  if (mis_ok && !use_mis(g, vn)) g = geometry_for(VBH_OP_LOGSUMEXP, cols, 1, rows);
   if (int rc = check_grid(rows, g)) return rc;
   return hip_status(launch_logsumexp(x, y, rows, static_cast<int>(cols), in_dtype, out_dtype,
                                      g, s),
@@ -649,10 +686,11 @@ int vbh_cross_entropy_bwd(const void* dloss, const void* logits, const void* lse
   a.has_smoothing = has_smoothing != 0;
   a.vec = vec_ok ? vn : 1;
   // store policy: the cross-entropy op's tune flags, else nontemporal, and
-  // written through the L2 from kWriteThroughMinBytes of dlogits
+  // written through the L2 from kWriteThroughMinBytes of dlogits in whole lines
   const int over = g_flags[VBH_OP_CROSS_ENTROPY].load();
   a.nt = !(over & kFlagTemporal);
-  bool wt = mul_sat(mul_sat(n_rows, n_cols), elt_size(logits_dtype)) >= kWriteThroughMinBytes;
+  bool wt = write_through_ok(mul_sat(mul_sat(n_rows, n_cols), elt_size(logits_dtype)), n_rows) &&
+            dlogits_row_stride == n_cols;
   if (over & kFlagWriteThrough) wt = true;
   if (over & kFlagNoWriteThrough) wt = false;
   a.wt = a.nt && wt;

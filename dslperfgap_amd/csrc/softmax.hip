@@ -73,32 +73,63 @@ __device__ __forceinline__ float lane_sum_exp(const typename Raw<T, V>::type (&x
   return a[0];
 }
 
-template <typename Ti, typename To, int V, int IT, bool LOG, int SP>
+// Rows whose length is not a multiple of the vector width start at varying
+// offsets within a 16-byte vector.  MIS kernels split such a row (element
+// `start` of a 16-byte aligned buffer, `cols` long) into a head of up to V - 1
+// elements before the first 16-byte boundary, a body of whole aligned vectors
+// and a tail of up to V - 1 elements; lanes g < head and g < tail each hold one
+// head / tail element as an extra scalar (the launcher makes tpr >= V).
+// Nothing outside the row is read or written.
+struct MisRow {
+  int head, nvec, tail;
+};
+
+template <int V>
+__device__ __forceinline__ MisRow mis_row(int64_t start, int cols) {
+  int head = static_cast<int>((V - start % V) % V);
+  if (head > cols) head = cols;
+  const int nvec = (cols - head) / V;
+  return MisRow{head, nvec, cols - head - nvec * V};
+}
+
+template <typename Ti, typename To, int V, int IT, bool LOG, int SP, bool MIS>
 __global__ __launch_bounds__(kMaxBlock) void softmax_rows(const Ti* __restrict__ x,
                                                           To* __restrict__ y, int64_t rows,
                                                           int cols, int tpr) {
   typedef typename Raw<Ti, V>::type RT;
   __shared__ float lds[2][kMaxWaves];
-  const int nvec = cols / V;
   const int g = threadIdx.x % tpr;
   const int rpb = blockDim.x / tpr;
   const int64_t first = static_cast<int64_t>(blockIdx.x) * rpb;
   int64_t row = first + threadIdx.x / tpr;
   const bool live = row < rows;
   if (!live) row = rows - 1;
+  const int64_t start = row * cols;
+  const MisRow mr = MIS ? mis_row<V>(start, cols) : MisRow{0, cols / V, 0};
+  const int nvec = mr.nvec;
+  const Ti* xb = x + start + mr.head;  // 16-byte aligned body
 
   RT xr[IT];
-  load_raw_row<Ti, V, IT, SP != kStoreCached>(x + row * cols, nvec, g, tpr, xr);
-  const float m = group_allreduce<Max>(lane_max<Ti, V, IT>(xr, nvec, g, tpr), tpr, lds[0]);
+  load_raw_row<Ti, V, IT, SP != kStoreCached>(xb, nvec, g, tpr, xr);
+  const bool hv = MIS && g < mr.head, tv = MIS && g < mr.tail;
+  float hx = 0.f, tx = 0.f;
+  if (hv) hx = static_cast<float>(x[start + g]);
+  if (tv) tx = static_cast<float>(xb[static_cast<int64_t>(nvec) * V + g]);
+  float lm = lane_max<Ti, V, IT>(xr, nvec, g, tpr);
+  if (hv) lm = fmaxf(lm, hx);
+  if (tv) lm = fmaxf(lm, tx);
+  const float m = group_allreduce<Max>(lm, tpr, lds[0]);
   reload_barrier<Ti, V, IT>(xr);
-  const float s =
-      group_allreduce<Sum>(lane_sum_exp<Ti, V, IT>(xr, nvec, g, tpr, m), tpr, lds[1]);
+  float le = lane_sum_exp<Ti, V, IT>(xr, nvec, g, tpr, m);
+  if (hv) le += fast_exp(hx - m);
+  if (tv) le += fast_exp(tx - m);
+  const float s = group_allreduce<Sum>(le, tpr, lds[1]);
   if (!live) return;
   reload_barrier<Ti, V, IT>(xr);
 
   const OutWindow<To, SP> out(y + first * cols, std::min<int64_t>(rpb, rows - first) * cols);
-  To* yr = y + row * cols;
-  const int yoff = static_cast<int>(row - first) * cols;
+  To* yr = y + start + mr.head;
+  const int yoff = static_cast<int>(row - first) * cols + mr.head;
   const float ls = LOG ? fast_log(s) : 0.f;
   const float r = LOG ? 0.f : 1.0f / s;
 #pragma unroll
@@ -114,27 +145,47 @@ __global__ __launch_bounds__(kMaxBlock) void softmax_rows(const Ti* __restrict__
       out.template store<V>(yr + static_cast<int64_t>(j) * V, yoff + j * V, o);
     }
   }
+  if (hv) {
+    const float o = LOG ? (hx - m) - ls : fast_exp(hx - m) * r;
+    store_from_f32<To, 1>(y + start + g, &o);
+  }
+  if (tv) {
+    const float o = LOG ? (tx - m) - ls : fast_exp(tx - m) * r;
+    store_from_f32<To, 1>(yr + static_cast<int64_t>(nvec) * V + g, &o);
+  }
 }
 
-template <typename Ti, typename To, int V, int IT, bool NT>
+template <typename Ti, typename To, int V, int IT, bool NT, bool MIS>
 __global__ __launch_bounds__(kMaxBlock) void logsumexp_rows(const Ti* __restrict__ x,
                                                             To* __restrict__ y, int64_t rows,
                                                             int cols, int tpr) {
   typedef typename Raw<Ti, V>::type RT;
   __shared__ float lds[2][kMaxWaves];
-  const int nvec = cols / V;
   const int g = threadIdx.x % tpr;
   int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / tpr) + threadIdx.x / tpr;
   const bool live = row < rows;
   if (!live) row = rows - 1;
+  const int64_t start = row * cols;
+  const MisRow mr = MIS ? mis_row<V>(start, cols) : MisRow{0, cols / V, 0};
+  const int nvec = mr.nvec;
+  const Ti* xb = x + start + mr.head;
 
   RT xr[IT];
-  load_raw_row<Ti, V, IT, NT>(x + row * cols, nvec, g, tpr, xr);
-  float m = group_allreduce<Max>(lane_max<Ti, V, IT>(xr, nvec, g, tpr), tpr, lds[0]);
+  load_raw_row<Ti, V, IT, NT>(xb, nvec, g, tpr, xr);
+  const bool hv = MIS && g < mr.head, tv = MIS && g < mr.tail;
+  float hx = 0.f, tx = 0.f;
+  if (hv) hx = static_cast<float>(x[start + g]);
+  if (tv) tx = static_cast<float>(xb[static_cast<int64_t>(nvec) * V + g]);
+  float lm = lane_max<Ti, V, IT>(xr, nvec, g, tpr);
+  if (hv) lm = fmaxf(lm, hx);
+  if (tv) lm = fmaxf(lm, tx);
+  float m = group_allreduce<Max>(lm, tpr, lds[0]);
   reload_barrier<Ti, V, IT>(xr);
   if (__builtin_isinf(m)) m = 0.f;
-  const float s =
-      group_allreduce<Sum>(lane_sum_exp<Ti, V, IT>(xr, nvec, g, tpr, m), tpr, lds[1]);
+  float le = lane_sum_exp<Ti, V, IT>(xr, nvec, g, tpr, m);
+  if (hv) le += fast_exp(hx - m);
+  if (tv) le += fast_exp(tx - m);
+  const float s = group_allreduce<Sum>(le, tpr, lds[1]);
   if (live && g == 0) {
     const float r = fast_log(s) + m;
     store_from_f32<To, 1>(y + row, &r);
@@ -301,9 +352,16 @@ hipError_t launch_softmax(const void* x, void* y, int64_t rows, int cols, int id
         if constexpr (M <= lane_cap(V)) {
           dispatch_store_policy<V>(g, [&](auto sp) {
             constexpr int SP = decltype(sp)::value;
-            hipLaunchKernelGGL((softmax_rows<Ti, To, V, M, LOG, SP>), dim3(grid_for(rows, g)),
-                               dim3(g.block), 0, s, static_cast<const Ti*>(x),
-                               static_cast<To*>(y), rows, cols, g.tpr);
+            if (V > 1 && g.mis)
+              hipLaunchKernelGGL((softmax_rows<Ti, To, V, M, LOG, SP, V != 1>),
+                                 dim3(grid_for(rows, g)), dim3(g.block), 0, s,
+                                 static_cast<const Ti*>(x), static_cast<To*>(y), rows, cols,
+                                 g.tpr);
+            else
+              hipLaunchKernelGGL((softmax_rows<Ti, To, V, M, LOG, SP, false>),
+                                 dim3(grid_for(rows, g)), dim3(g.block), 0, s,
+                                 static_cast<const Ti*>(x), static_cast<To*>(y), rows, cols,
+                                 g.tpr);
           });
           err = hipGetLastError();
         }
@@ -337,14 +395,14 @@ hipError_t launch_logsumexp(const void* x, void* y, int64_t rows, int cols, int 
       dispatch_maxit(g.maxit, [&](auto mc) {
         constexpr int M = decltype(mc)::value;
         if constexpr (M <= lane_cap(V)) {
-          if (g.nt)
-            hipLaunchKernelGGL((logsumexp_rows<Ti, To, V, M, true>), dim3(grid_for(rows, g)),
-                               dim3(g.block), 0, s, static_cast<const Ti*>(x),
-                               static_cast<To*>(y), rows, cols, g.tpr);
-          else
-            hipLaunchKernelGGL((logsumexp_rows<Ti, To, V, M, false>), dim3(grid_for(rows, g)),
-                               dim3(g.block), 0, s, static_cast<const Ti*>(x),
-                               static_cast<To*>(y), rows, cols, g.tpr);
+          auto launch = [&](auto kern) {
+            hipLaunchKernelGGL(kern, dim3(grid_for(rows, g)), dim3(g.block), 0, s,
+                               static_cast<const Ti*>(x), static_cast<To*>(y), rows, cols,
+                               g.tpr);
+          };
+          if (V > 1 && g.mis) launch(logsumexp_rows<Ti, To, V, M, true, V != 1>);
+          else if (g.nt) launch(logsumexp_rows<Ti, To, V, M, true, false>);
+          else launch(logsumexp_rows<Ti, To, V, M, false, false>);
           err = hipGetLastError();
         }
       });

@@ -37,6 +37,9 @@ struct Geometry {
   bool persist = false;
   bool nt = false;
   bool wt = false;
+  // rows not a multiple of V long: head / aligned body / tail per row (MIS
+  // kernels; v is the vector width, tpr >= v)
+  bool mis = false;
 };
 
 // vbh_tune_override flag bits

@@ -809,3 +809,30 @@ def test_split_cross_entropy_matches_the_unsplit_kernel():
         outs.append([t.cpu() for t in o])
     for a, b in zip(*outs):
         assert torch.allclose(a, b, atol=1e-5, rtol=1e-5), (a - b).abs().max()
+
+
+# ---------------------------------------------------------------------------
+# rows not a multiple of the 16-byte vector: head / aligned body / tail
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_misaligned_rows_softmax_family(dtype):
+    """Every residue of cols modulo the vector width, and rows whose starts
+    cycle through every offset within a vector: the row maximum sits in the
+    head of one row and the tail of another, a NaN in a head; softmax,
+    log_softmax (also fp16/bf16 in, fp32 out) and logsumexp match the oracle."""
+    vn = 16 // torch.empty(0, dtype=dtype).element_size()
+    widths = [4 * vn + r for r in range(1, vn)] + [50257, 1000 * vn + vn // 2]
+    for cols in widths:
+        rows = 2 * vn + 1
+        x = (3 * torch.randn(rows, cols, generator=_g(600 + cols))).to(dtype)
+        x[0, 0] = 40.0                      # head of a row starting on a boundary: max first
+        x[1, cols - 1] = 40.0               # last element: in the tail unless aligned
+        x[2, 1 % cols] = float("nan")
+        xd = x.to(DEV)
+        what = f"misaligned {dtype} cols={cols}"
+        check(softmax(xd), ref.softmax(x), dtype, what="softmax " + what)
+        check(log_softmax(xd), ref.log_softmax(x), dtype, what="log_softmax " + what)
+        check(logsumexp(xd), ref.logsumexp(x), dtype, what="logsumexp " + what)
+        if dtype != torch.float32:
+            check(log_softmax(xd, -1, torch.float32), ref.log_softmax(x, -1, torch.float32),
+                  torch.float32, what="log_softmax fp32 out " + what)
