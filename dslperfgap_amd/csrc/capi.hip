@@ -621,7 +621,9 @@ int vbh_cross_entropy_fwd_ws(const void* logits, const void* labels, int logits_
     return hip_status(e, "cross_entropy_fwd launch");
   }
   const int64_t segments = mul_sat(n_rows, ncb);
-  const Geometry g = geometry_for(VBH_OP_CROSS_ENTROPY, bs, vec_ok ? vn : 1, segments);
+  const bool mis_ok = !vec_ok && aligned16(logits) && bs >= kMisMinVecs * vn;
+  Geometry g = geometry_for(VBH_OP_CROSS_ENTROPY, bs, vec_ok || mis_ok ? vn : 1, segments);
+  if (mis_ok && !use_mis(g, vn)) g = geometry_for(VBH_OP_CROSS_ENTROPY, bs, 1, segments);
   if (int rc = check_grid(segments, g)) return rc;
   return hip_status(launch_cross_entropy_fwd(a, g, s), "cross_entropy_fwd launch");
 }
@@ -764,7 +766,9 @@ int vbh_reduce_fwd_ws(const void* x, void* values, void* indices, int64_t outer,
       }
       return hip_status(e, "reduce launch");
     }
-    g = reduce_geometry(n, vec_ok ? vn : 1, outer);
+    const bool mis_ok = !vec_ok && aligned16(x) && n >= kMisMinVecs * vn;
+    g = reduce_geometry(n, vec_ok || mis_ok ? vn : 1, outer);
+    if (mis_ok && !use_mis(g, vn)) g = reduce_geometry(n, 1, outer);
     if (int rc = check_grid(outer, g)) return rc;
   } else if (mul_sat(outer, inner) > kMaxWorkItems / 256 * 256) {
     return fail(VBH_E_RANGE, "reduce: outer * inner too large");

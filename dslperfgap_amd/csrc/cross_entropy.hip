@@ -94,7 +94,24 @@ __device__ __forceinline__ void ce_store(float lse, float sum_logits, bool in_bl
   z_out[idx] = z;
 }
 
-template <typename T, int V, int IT, bool NT>
+// Segments whose start is not on a 16-byte boundary (rows not a multiple of
+// the vector width long): MIS kernels read a scalar head up to the first
+// boundary, whole aligned vectors and a scalar tail, one head and one tail
+// element per lane (the launcher makes tpr >= V); nothing outside the
+// segment is read.
+struct MisSeg {
+  int head, nvec, tail;
+};
+
+template <int V>
+__device__ __forceinline__ MisSeg mis_seg(int64_t start, int len) {
+  int head = static_cast<int>((V - start % V) % V);
+  if (head > len) head = len;
+  const int nvec = (len - head) / V;
+  return MisSeg{head, nvec, len - head - nvec * V};
+}
+
+template <typename T, int V, int IT, bool NT, bool MIS>
 __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
     const T* __restrict__ logits, const void* __restrict__ labels, int label_i64,
     float* __restrict__ loss, float* __restrict__ lse_out, float* __restrict__ z_out,
@@ -110,8 +127,11 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
   const int cb = static_cast<int>(seg - row * ncb);
   const int col0 = cb * bs;
   const int col_end = min(n_cols, col0 + bs);
-  const int nvec = (col_end - col0) / V;
   const T* lr = logits + row * ld;
+  const int64_t sstart = row * ld + col0;
+  const MisSeg ms = MIS ? mis_seg<V>(sstart, col_end - col0) : MisSeg{0, (col_end - col0) / V, 0};
+  const int nvec = ms.nvec;
+  const T* lb = logits + sstart + ms.head;  // 16-byte aligned body
 
   // label logit, fetched early by the storing lane
   bool ignored = false, in_block = false;
@@ -128,10 +148,14 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
 #pragma unroll
   for (int i = 0; i < IT; ++i) {
     const int j = i * tpr + g;
-    if (j < nvec) xr[i] = load_raw<T, V, NT>(lr + col0 + static_cast<int64_t>(j) * V);
+    if (j < nvec) xr[i] = load_raw<T, V, NT>(lb + static_cast<int64_t>(j) * V);
     else xr[i] = RT{};
   }
   const float scale = c.logit_scale;
+  const bool hv = MIS && g < ms.head, tv = MIS && g < ms.tail;
+  float hx = 0.f, tx = 0.f;
+  if (hv) hx = static_cast<float>(logits[sstart + g]) * scale;
+  if (tv) tx = static_cast<float>(lb[static_cast<int64_t>(nvec) * V + g]) * scale;
 
   float mx[V];
 #pragma unroll
@@ -144,6 +168,8 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
   float lm = mx[0];
 #pragma unroll
   for (int k = 1; k < V; ++k) lm = fmaxf(lm, mx[k]);
+  if (hv) lm = fmaxf(lm, hx);
+  if (tv) lm = fmaxf(lm, tx);
   const float m = group_allreduce<Max>(lm, tpr, lds[0]);
   reload_barrier<T, V, IT>(xr);
 
@@ -168,6 +194,14 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
       se[k] += se[k + w];
       sl[k] += sl[k + w];
     }
+  if (hv) {
+    se[0] += fast_exp(hx - m);
+    sl[0] += hx;
+  }
+  if (tv) {
+    se[0] += fast_exp(tx - m);
+    sl[0] += tx;
+  }
   const float s = group_allreduce<Sum>(se[0], tpr, lds[1]);
   float sum_logits = 0.f;
   if (c.has_smoothing || c.empty_neg_inf) sum_logits = group_allreduce<Sum>(sl[0], tpr, lds[2]);
@@ -374,8 +408,9 @@ hipError_t launch_cross_entropy_fwd(const CeArgs& a, const Geometry& g, hipStrea
                                g.tpr, c);
             err = hipGetLastError();
           };
-          if (g.nt) launch(ce_fwd_rows<T, V, M, true>);
-          else launch(ce_fwd_rows<T, V, M, false>);
+          if (V > 1 && g.mis) launch(ce_fwd_rows<T, V, M, true, V != 1>);
+          else if (g.nt) launch(ce_fwd_rows<T, V, M, true, false>);
+          else launch(ce_fwd_rows<T, V, M, false, false>);
         }
       });
     };

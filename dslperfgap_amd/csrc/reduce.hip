@@ -96,19 +96,33 @@ __device__ __forceinline__ void write_result(void* vals, int64_t* idx, int64_t o
   }
 }
 
-// OP: 0 = mean (To = output type), 1 = max values + indices, 2 = argmax
-template <typename Ti, typename To, int V, int OP>
+// OP: 0 = mean (To = output type), 1 = max values + indices, 2 = argmax.
+// MIS: rows not a multiple of V long start at varying offsets within a
+// 16-byte vector; each row is read as a scalar head up to the first 16-byte
+// boundary (lanes g < head, element g), whole aligned vectors, and a scalar
+// tail (lanes g < tail); the launcher makes tpr >= V.  A lane visits its head
+// element first and its tail element last, so its positions still increase.
+template <typename Ti, typename To, int V, int OP, bool MIS>
 __global__ __launch_bounds__(kMaxBlock) void reduce_rows(const Ti* __restrict__ x,
                                                          void* __restrict__ vals,
                                                          int64_t* __restrict__ idx,
                                                          int64_t rows, int n, int tpr) {
   __shared__ float lds[2 * kMaxWaves];
-  const int nvec = n / V;
   const int g = threadIdx.x % tpr;
   int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / tpr) + threadIdx.x / tpr;
   const bool live = row < rows;
   if (!live) row = rows - 1;
-  const Ti* xr = x + row * n;
+  const int64_t start = row * n;
+  int head = 0, nvec = n / V, tail = 0;
+  if constexpr (MIS) {
+    head = static_cast<int>((V - start % V) % V);
+    if (head > n) head = n;
+    nvec = (n - head) / V;
+    tail = n - head - nvec * V;
+  }
+  const Ti* xr = x + start + head;  // 16-byte aligned body; element j * V + k is head + j * V + k
+  const bool hv = MIS && g < head, tv = MIS && g < tail;
+  const int tail0 = head + nvec * V;  // row index of the first tail element
   typedef typename Raw<Ti, V>::type RT;
   // Each lane loads kChunk vectors (kChunk * tpr apart... j, j + tpr, ...) before
   // processing any of them, so a chunk's loads are in flight together whatever
@@ -133,6 +147,8 @@ __global__ __launch_bounds__(kMaxBlock) void reduce_rows(const Ti* __restrict__ 
     float s = 0.f;
 #pragma unroll
     for (int k = 0; k < V; ++k) s += acc[k];
+    if (hv) s += static_cast<float>(x[start + g]);
+    if (tv) s += static_cast<float>(x[start + tail0 + g]);
     s = group_allreduce<Sum>(s, tpr, lds);
     if (live && g == 0) write_result<To, V, OP>(vals, idx, row, s, 0, n);
   } else {
@@ -142,6 +158,15 @@ __global__ __launch_bounds__(kMaxBlock) void reduce_rows(const Ti* __restrict__ 
     // beats the lane's best, which is rare after the first few vectors.
     ValIdx best{kNegInf, n};  // an empty lane loses to any element
     bool done = false;        // a NaN was found: nothing later can win
+    if (hv) {
+      const float v = static_cast<float>(x[start + g]);
+      if (v != v) {
+        best = ValIdx{__builtin_nanf(""), g};
+        done = true;
+      } else {
+        best = ValIdx{v, g};
+      }
+    }
     for (int base = g; base < nvec; base += kChunk * tpr) {
       RT r[kChunk];
 #pragma unroll
@@ -168,16 +193,21 @@ __global__ __launch_bounds__(kMaxBlock) void reduce_rows(const Ti* __restrict__ 
 #pragma unroll
           for (int k = V - 1; k >= 0; --k)
             if (v[k] != v[k]) kk = k;
-          best = ValIdx{__builtin_nanf(""), j * V + kk};
+          best = ValIdx{__builtin_nanf(""), head + j * V + kk};
           done = true;
         } else if (m > best.v || best.i == n) {  // first position of the vector max
           int kk = V - 1;
 #pragma unroll
           for (int k = V - 1; k >= 0; --k)
             if (v[k] == m) kk = k;
-          best = ValIdx{m, j * V + kk};
+          best = ValIdx{m, head + j * V + kk};
         }
       }
+    }
+    if (tv && !done) {
+      const float v = static_cast<float>(x[start + tail0 + g]);
+      if (v != v) best = ValIdx{__builtin_nanf(""), tail0 + g};
+      else if (v > best.v || best.i == n) best = ValIdx{v, tail0 + g};
     }
     best = group_allreduce_vi(best, tpr, lds);
     if (live && g == 0) write_result<To, V, OP>(vals, idx, row, best.v, best.i, n);
@@ -249,8 +279,9 @@ hipError_t launch_reduce(const void* x, void* vals, int64_t* idx, int64_t outer,
           hipLaunchKernelGGL(kern, dim3(grid_for(outer, g)), dim3(g.block), 0, s,
                              static_cast<const Ti*>(x), vals, idx, outer, n, g.tpr);
         };
-        if (g.v == 1) launch(reduce_rows<Ti, To, 1, OP>);
-        else launch(reduce_rows<Ti, To, VN, OP>);
+        if (g.v == 1) launch(reduce_rows<Ti, To, 1, OP, false>);
+        else if (g.mis) launch(reduce_rows<Ti, To, VN, OP, true>);
+        else launch(reduce_rows<Ti, To, VN, OP, false>);
       } else {
         const int64_t cols = outer * inner;
         hipLaunchKernelGGL((reduce_cols<Ti, To, OP>), dim3((cols + 255) / 256), dim3(256), 0, s,

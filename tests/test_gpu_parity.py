@@ -836,3 +836,27 @@ def test_misaligned_rows_softmax_family(dtype):
         if dtype != torch.float32:
             check(log_softmax(xd, -1, torch.float32), ref.log_softmax(x, -1, torch.float32),
                   torch.float32, what="log_softmax fp32 out " + what)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("smooth", [False, True])
+def test_misaligned_cross_entropy(dtype, smooth):
+    """Cross-entropy segments that start inside a 16-byte vector: widths of
+    every residue modulo the vector width, one column block per row and blocks
+    of a non-multiple width (every segment misaligned), labels on the first and
+    last columns of a segment."""
+    vn = 16 // torch.empty(0, dtype=dtype).element_size()
+    for cols in [4 * vn + r for r in range(1, vn)] + [50257]:
+        rows = 2 * vn + 1
+        g = _g(800 + cols)
+        logits = (2 * torch.randn(rows, cols, generator=g)).to(dtype)
+        labels = torch.randint(0, cols, (rows,), generator=g)
+        labels[0], labels[1], labels[2] = 0, cols - 1, -100
+        for bs in (1 << 17, 4 * vn + 3):
+            args = (0.1 if smooth else 0.0, 1.0, 1e-4, -100, cols, 0, bs, smooth, False)
+            got = cross_entropy_fwd(logits.to(DEV), labels.to(DEV), *args)
+            want = ref.cross_entropy_fwd(logits, labels, *args)
+            n = rows * -(-cols // bs)
+            for k, (t, w) in enumerate(zip(got, want)):
+                check(t.reshape(-1)[:n], w.reshape(-1)[:n], torch.float32,
+                      what=f"misaligned ce[{k}] {dtype} cols={cols} bs={bs} smooth={smooth}")

@@ -221,3 +221,35 @@ def test_split_reduction_falls_back_without_enough_workspace():
         assert torch.equal(v, outs[0][0]) and torch.equal(i, outs[0][1])
     rv, ri = ref.max_reduction(x.cpu(), 1)
     assert torch.equal(outs[0][1], ri)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_misaligned_rows_reductions(dtype):
+    """Rows not a multiple of the 16-byte vector (head / aligned body / tail):
+    every residue of n modulo the vector width; the maximum in a head, in a
+    tail and tied between the two, a NaN in a head or a tail; max, argmax
+    exactly, mean at tolerance."""
+    vn = 16 // torch.empty(0, dtype=dtype).element_size()
+    for n in [4 * vn + r for r in range(1, vn)] + [50257]:
+        rows = 2 * vn + 3
+        x = torch.randn(rows, n, generator=_g(700 + n)).to(dtype)
+        for r in range(rows):
+            if r % 4 == 0:
+                x[r, 0] = 40.0                 # head of this row (or first body element)
+            elif r % 4 == 1:
+                x[r, n - 1] = 40.0             # tail
+            elif r % 4 == 2:
+                x[r, 1] = 40.0
+                x[r, n - 2] = 40.0             # tie: the first wins
+        x[3, 0] = float("nan")
+        x[7, n - 1] = float("nan")
+        x[7, n // 2] = 41.0
+        xd = x.to(DEV)
+        what = f"misaligned {dtype} n={n}"
+        v, i = max_reduction(xd, 1)
+        rv, ri = ref.max_reduction(x, 1)
+        _same(v, rv, "max values " + what)
+        _same(i, ri, "max indices " + what)
+        _same(argmax(xd, 1), ref.argmax(x, 1), "argmax " + what)
+        xm = torch.randn(rows, n, generator=_g(710 + n)).to(dtype) + 2.0
+        _close(mean_reduction(xm.to(DEV), 1), ref.mean_reduction(xm, 1), "mean " + what)
