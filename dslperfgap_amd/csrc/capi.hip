@@ -662,7 +662,11 @@ int vbh_cross_entropy_bwd(const void* dloss, const void* logits, const void* lse
   const int vn = 16 / elt_size(logits_dtype);
   const bool vec_ok = n_cols % vn == 0 && logits_row_stride % vn == 0 &&
                       dlogits_row_stride % vn == 0 && aligned16(logits) && aligned16(dlogits);
-  const int64_t tiles = (n_cols / (vec_ok ? vn : 1) + kCeBwdLanes - 1) / kCeBwdLanes;
+  // MIS: every logits and dlogits row starts at the same offset within a vector
+  const bool mis_ok = !vec_ok && aligned16(logits) && aligned16(dlogits) &&
+                      logits_row_stride == dlogits_row_stride && n_cols >= kMisMinVecs * vn;
+  const int64_t tiles =
+      (n_cols / (vec_ok || mis_ok ? vn : 1) + kCeBwdLanes - 1) / kCeBwdLanes;
   if (n_rows > kMaxWorkItems / (tiles * kCeBwdLanes))
     return fail(VBH_E_RANGE, "cross_entropy_bwd: %lld x %lld elements exceed one launch",
                 static_cast<long long>(n_rows), static_cast<long long>(n_cols));
@@ -686,7 +690,8 @@ int vbh_cross_entropy_bwd(const void* dloss, const void* logits, const void* lse
   a.total_classes = static_cast<float>(total_classes);
   a.class_start = class_start_idx;
   a.has_smoothing = has_smoothing != 0;
-  a.vec = vec_ok ? vn : 1;
+  a.vec = vec_ok || mis_ok ? vn : 1;
+  a.mis = mis_ok;
   // store policy: the cross-entropy op's tune flags, else nontemporal, and
   // written through the L2 from kWriteThroughMinBytes of dlogits in whole lines
   const int over = g_flags[VBH_OP_CROSS_ENTROPY].load();

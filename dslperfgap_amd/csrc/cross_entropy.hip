@@ -336,14 +336,30 @@ __global__ __launch_bounds__(256) void ce_combine(
 // read once per workgroup.
 constexpr int kBwdLanes = kCeBwdLanes;
 
-template <typename T, int V, int SP>
+// dlogits of one element: q = p + 2 * lss * lse * p, p = exp(x * scale - lse),
+// minus the (smoothed) one-hot; times dloss * logit_scale.
+__device__ __forceinline__ float ce_grad(float xv, int64_t col, int64_t adj, float lse_r,
+                                         float zfac, float hit, float smooth_neg, float scale,
+                                         const CeScalars& c) {
+  float p = fast_exp(xv * c.logit_scale - lse_r);
+  p = p + zfac * p;
+  if (col == adj) p = p - hit;
+  if (c.has_smoothing) p = p - smooth_neg;
+  return scale * p;
+}
+
+// MIS: rows not a multiple of V long (same offset within a vector for logits
+// and dlogits rows): tiles cover the row's aligned body; tile 0 also writes
+// the scalar head (before the first 16-byte boundary) and tail elements.
+template <typename T, int V, int SP, bool MIS>
 __global__ __launch_bounds__(kBwdLanes) void ce_bwd_tiles(
     const float* __restrict__ dloss, const T* __restrict__ logits,
     const float* __restrict__ lse, const void* __restrict__ labels, int label_i64,
     T* __restrict__ dlogits, int n_cols, uint32_t tiles_per_row, int64_t ld_in,
     int64_t ld_out, int64_t dloss_stride, CeScalars c) {
   const uint32_t row32 = blockIdx.x / tiles_per_row;
-  const int j0 = static_cast<int>(blockIdx.x - row32 * tiles_per_row) * kBwdLanes;
+  const int tix = static_cast<int>(blockIdx.x - row32 * tiles_per_row);
+  const int j0 = tix * kBwdLanes;
   const int64_t row = row32;
   const int64_t label = read_label(labels, label_i64, row);
   const float dl = label != c.ignored_index ? dloss[row * dloss_stride] : 0.f;
@@ -354,25 +370,42 @@ __global__ __launch_bounds__(kBwdLanes) void ce_bwd_tiles(
   const float zfac = c.two_lse_square_scale * lse_r;
   const float smooth_neg = c.has_smoothing ? c.smooth_negative : 0.f;
   const float hit = c.has_smoothing ? c.one_minus_smoothing : 1.0f;
-  const int nvec = n_cols / V;
-  const int tile = nvec - j0 < kBwdLanes ? nvec - j0 : kBwdLanes;
-  T* dr = dlogits + row * ld_out;
-  const OutWindow<T, SP> out(dr + static_cast<int64_t>(j0) * V, static_cast<int64_t>(tile) * V);
+  const int64_t in0 = row * ld_in;
+  int head = 0, nvec = n_cols / V, tail = 0;
+  if constexpr (MIS) {
+    head = static_cast<int>((V - in0 % V) % V);
+    if (head > n_cols) head = n_cols;
+    nvec = (n_cols - head) / V;
+    tail = n_cols - head - nvec * V;
+  }
+  const T* lr = logits + in0 + head;     // 16-byte aligned body
+  T* dr = dlogits + row * ld_out + head;
+  const int tile = nvec - j0 < kBwdLanes ? nvec - j0 : kBwdLanes;  // <= 0: no body here
+  const OutWindow<T, SP> out(dr + static_cast<int64_t>(j0) * V,
+                             static_cast<int64_t>(tile > 0 ? tile : 0) * V);
   const int j = j0 + static_cast<int>(threadIdx.x);
   if (j < nvec) {
-    const auto r = load_raw<T, V, SP != kStoreCached>(logits + row * ld_in +
-                                                      static_cast<int64_t>(j) * V);
+    const auto r = load_raw<T, V, SP != kStoreCached>(lr + static_cast<int64_t>(j) * V);
     float o[V];
 #pragma unroll
-    for (int k = 0; k < V; ++k) {
-      float p = fast_exp(raw_at<T, V>(r, k) * c.logit_scale - lse_r);
-      p = p + zfac * p;
-      const int64_t col = static_cast<int64_t>(j) * V + k;
-      if (col == adj) p = p - hit;
-      if (c.has_smoothing) p = p - smooth_neg;
-      o[k] = scale * p;
-    }
+    for (int k = 0; k < V; ++k)
+      o[k] = ce_grad(raw_at<T, V>(r, k), head + static_cast<int64_t>(j) * V + k, adj, lse_r,
+                     zfac, hit, smooth_neg, scale, c);
     out.template store<V>(dr + static_cast<int64_t>(j) * V, static_cast<int>(threadIdx.x) * V, o);
+  }
+  if (MIS && tix == 0) {
+    const int t = static_cast<int>(threadIdx.x);
+    if (t < head) {
+      const float o = ce_grad(static_cast<float>(logits[in0 + t]), t, adj, lse_r, zfac, hit,
+                              smooth_neg, scale, c);
+      store_from_f32<T, 1>(dr - head + t, &o);
+    }
+    if (t < tail) {
+      const int64_t k = static_cast<int64_t>(nvec) * V + t;
+      const float o = ce_grad(static_cast<float>(lr[k]), head + k, adj, lse_r, zfac, hit,
+                              smooth_neg, scale, c);
+      store_from_f32<T, 1>(dr + k, &o);
+    }
   }
 }
 
@@ -448,11 +481,14 @@ hipError_t launch_cross_entropy_bwd(const CeBwdArgs& a, hipStream_t s) {
       const int64_t tiles = (nvec + kBwdLanes - 1) / kBwdLanes;
       dispatch_store_policy<V>(g, [&](auto sp) {
         constexpr int SP = decltype(sp)::value;
-        hipLaunchKernelGGL((ce_bwd_tiles<T, V, SP>), dim3(a.n_rows * tiles), dim3(kBwdLanes),
-                           0, s, a.dloss, static_cast<const T*>(a.logits), a.lse, a.labels,
-                           a.label_i64, static_cast<T*>(a.dlogits), a.n_cols,
-                           static_cast<uint32_t>(tiles), a.ld_logits, a.ld_dlogits,
-                           a.dloss_stride, c);
+        auto launch = [&](auto kern) {
+          hipLaunchKernelGGL(kern, dim3(a.n_rows * tiles), dim3(kBwdLanes), 0, s, a.dloss,
+                             static_cast<const T*>(a.logits), a.lse, a.labels, a.label_i64,
+                             static_cast<T*>(a.dlogits), a.n_cols, static_cast<uint32_t>(tiles),
+                             a.ld_logits, a.ld_dlogits, a.dloss_stride, c);
+        };
+        if (V > 1 && a.mis) launch(ce_bwd_tiles<T, V, SP, V != 1>);
+        else launch(ce_bwd_tiles<T, V, SP, false>);
       });
       err = hipGetLastError();
     };

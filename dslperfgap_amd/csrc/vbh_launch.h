@@ -193,6 +193,7 @@ struct CeBwdArgs {
   int vec;
   int nt;  // nontemporal logits loads / dlogits stores
   int wt;  // dlogits stores also written through the L2 (with nt, 16-byte rows)
+  int mis = 0;  // rows not a multiple of vec long: head / aligned body / tail
 };
 // One workgroup of this many lanes per tile of as many vectors of one row.
 constexpr int kCeBwdLanes = 256;

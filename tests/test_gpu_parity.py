@@ -485,11 +485,14 @@ def test_cross_entropy_bwd(smoothing, lss, dtype):
 @pytest.mark.parametrize("cols,dtype,ldt", [(1001, torch.float32, torch.int64),
                                             (4096, torch.float32, torch.int32),
                                             (4104, torch.bfloat16, torch.int64),
-                                            (255, torch.float16, torch.int32)])
+                                            (255, torch.float16, torch.int32),
+                                            (50257, torch.float32, torch.int64),
+                                            (4099, torch.bfloat16, torch.int32)])
 def test_cross_entropy_bwd_tiles(cols, dtype, ldt, flags):
-    """The tiled backward: scalar rows (1001, 255 columns), whole and partial
-    256-vector tiles, int32 / int64 labels, ignored rows, a class_start shift
-    that puts some labels outside the shard, and every store policy."""
+    """The tiled backward: rows not a multiple of the vector (1001, 255, 50257,
+    4099 columns: head / aligned body / tail), whole and partial 256-vector
+    tiles, int32 / int64 labels, ignored rows, a class_start shift that puts
+    some labels outside the shard, and every store policy."""
     g = _g(121)
     rows = 37
     logits = (2 * torch.randn(rows, cols, generator=g)).to(dtype)
