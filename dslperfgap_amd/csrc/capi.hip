@@ -82,7 +82,24 @@ constexpr int64_t kMidRowVecs = 256;
 // above 256 vectors (+7% at 500, +12% at 2048), fp32 mean / max / argmax above
 // 256 vectors (+2 to +4%) and their 16-bit rows above 1024 vectors (+13% at
 // 2048); fp32 logsumexp keeps 4 up to 2048 vectors (within 1% either way).
+// Short rows (at most kShortRowVecs vectors) want several lanes per row: one
+// or two lanes per row serialise each row's loads and leave the reductions
+// nothing to share.  There each op takes kItShort vectors per lane, halved
+// until the row has kMinLanesShort lanes.  MI355X, bf16 at 64 MB per call,
+// default -> rule: 64 columns (8 vectors) LayerNorm 2068 -> 4794 GB/s,
+// RMSNorm 5006 -> 5841, softmax 1969 -> 5546, cross entropy 2170 -> 3073,
+// argmax 3139 -> 4645; 128 columns LayerNorm 4503 -> 5698, softmax 4532 ->
+// 5768, cross entropy 2786 -> 3970; 256 columns +0 to +4%.
+constexpr int64_t kShortRowVecs = 32;
+constexpr int kItShort[kNumOps] = {2, 2, 2, 2, 4, 4};
+constexpr int kMinLanesShort[kNumOps] = {4, 8, 8, 8, 2, 4};
+
 int it_target(int op, int64_t nvec, int vec) {
+  if (vec > 1 && nvec <= kShortRowVecs) {
+    int it = kItShort[op];
+    while (it > 1 && nvec / it < kMinLanesShort[op]) it /= 2;
+    return it;
+  }
   if (vec > 1) {
     if (op == VBH_OP_CROSS_ENTROPY) return 8;
     if (op == VBH_OP_LOGSUMEXP && vec == 8 && nvec > kMidRowVecs) return 8;
