@@ -56,11 +56,11 @@ COPY_KIB_EACH_WAY = (4 << 30) // 1024
 CONFIG_KERNELS = [
     ("C1_layer_norm", r"layer_norm_rows<float, float, 4, 4, \d>|layer_norm_rowsIffLi4ELi4ELi\dE"),
     ("C2_rms_norm", r"rms_norm_rowsIDF16bDF16bLi8ELi2ELi\dE"),
-    ("C3_log_softmax", r"softmax_rows<float, float, 4, 2, true, \d>"),
-    ("C3_softmax", r"softmax_rows<float, float, 4, 2, false, \d>"),
-    ("C3_logsumexp", r"logsumexp_rows<float, float, 4, 4, true>"),
-    ("C4_cross_entropy", r"ce_fwd_rows<float, 4, 8, true>"),
-    ("C4_cross_entropy_bwd", r"ce_bwd_tiles<float, 4, \d>|ce_bwd_tilesIfLi4ELi\dE"),
+    ("C3_log_softmax", r"softmax_rows<float, float, 4, 2, true, \d(, false)?>"),
+    ("C3_softmax", r"softmax_rows<float, float, 4, 2, false, \d(, false)?>"),
+    ("C3_logsumexp", r"logsumexp_rows<float, float, 4, 4, true(, false)?>"),
+    ("C4_cross_entropy", r"ce_fwd_rows<float, 4, 8, true(, false)?>"),
+    ("C4_cross_entropy_bwd", r"ce_bwd_tiles<float, 4, \d(, false)?>|ce_bwd_tilesIfLi4ELi\dE"),
     ("C5_layer_norm", r"layer_norm_pipeIDF16bDF16bLi8ELi4ELi\dELb1E"),
     (COPY, r"copy_kernel\("),
 ]
@@ -69,11 +69,11 @@ REFERENCE_KERNELS = [
     ("rms_norm", r"rms_norm_pipeIDF16_DF16_Li8ELi2ELi\dELb1E"),
     ("softmax", r"softmax_rowsIDF16_DF16_Li8ELi4ELb0ELi\dE"),
     ("log_softmax", r"softmax_rowsIDF16_DF16_Li8ELi4ELb1ELi\dE"),
-    ("logsumexp", r"logsumexp_rows<float, float, 4, 8, true>"),
-    ("cross_entropy", r"ce_fwd_rows<float, 4, \d, true>"),
+    ("logsumexp", r"logsumexp_rows<float, float, 4, 8, true(, false)?>"),
+    ("cross_entropy", r"ce_fwd_rows<float, 4, \d, true(, false)?>"),
     ("argmax", r"reduce_rowsIDF16_DF16_Li8ELi2E"),
     ("max_reduction", r"reduce_rowsIDF16_DF16_Li8ELi1E"),
-    ("mean_reduction", r"reduce_rows<float, float, 4, 0>"),
+    ("mean_reduction", r"reduce_rows<float, float, 4, 0(, false)?>"),
     (COPY, r"copy_kernel\("),
 ]
 
@@ -234,6 +234,13 @@ def render(preset: str, trace, fetch, write) -> tuple[str, str]:
     kernels, alg = p["kernels"], p["alg"]()
     order = [k for k, _ in kernels]
     stats = read_stats(trace, kernels)
+    fetched, written = read_counter(fetch, kernels), read_counter(write, kernels)
+    # a renamed kernel template must not drop a workload from the summaries
+    # (bench.py reads the traffic lines)
+    missing = [k for k in order if k not in stats or k not in fetched or k not in written]
+    if missing:
+        raise ValueError(f"{preset}: no kernel in the rocprofv3 files matched {missing}; "
+                         "update the symbol patterns")
     tr = trace_table(stats, alg, order)
     tdir, tpre = _dir_prefix(trace, "_kernel_stats.csv")
     run_dir = str(Path(tdir).parent)
@@ -247,8 +254,7 @@ def render(preset: str, trace, fetch, write) -> tuple[str, str]:
             f"achieved = algorithmic bytes / AverageNs (ns); of_copy = achieved / the 4 GiB copy\n"
             f"kernel's rate in the same run.\n\n")
     trace_txt = head + format_trace(tr)
-    rows, fs, ws = traffic_table(read_counter(fetch, kernels), read_counter(write, kernels), alg,
-                                 order)
+    rows, fs, ws = traffic_table(fetched, written, alg, order)
     pmc = []
     for c, path in (("FETCH_SIZE", fetch), ("WRITE_SIZE", write)):
         d, pre = _dir_prefix(path, "_counter_collection.csv")

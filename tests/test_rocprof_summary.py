@@ -69,8 +69,51 @@ def test_trace_and_traffic_arithmetic(tmp_path):
     assert t["ratio"] == pytest.approx(t["traffic"] / 134_225_920)
 
 
-def test_rendered_headers_and_machine_lines(tmp_path):
+# a symbol of every config's kernel as rocprofv3 printed them
+CONFIG_SYMBOLS = {
+    "C1_layer_norm": "void vbh::(anonymous namespace)::layer_norm_rows<float, float, 4, 4, 1>"
+                     "(float const*, float const*, float const*, float*, long, int, int, float)",
+    "C3_log_softmax": "void vbh::(anonymous namespace)::softmax_rows<float, float, 4, 2, true, "
+                      "2, false>(float const*, float*, long, int, int)",
+    "C3_softmax": "void vbh::(anonymous namespace)::softmax_rows<float, float, 4, 2, false, 2, "
+                  "false>(float const*, float*, long, int, int)",
+    "C3_logsumexp": "void vbh::(anonymous namespace)::logsumexp_rows<float, float, 4, 4, true, "
+                    "false>(float const*, float*, long, int, int)",
+    "C4_cross_entropy": "void vbh::(anonymous namespace)::ce_fwd_rows<float, 4, 8, true, false>"
+                        "(float const*, void const*, int, float*, float*, float*)",
+    "C4_cross_entropy_bwd": "void vbh::(anonymous namespace)::ce_bwd_tiles<float, 4, 2, false>"
+                            "(float const*, float const*, float const*)",
+    "C5_layer_norm": "_ZN3vbh12_GLOBAL__N_115layer_norm_pipeIDF16bDF16bLi8ELi4ELi2ELb1EEEvPKT_"
+                     "PKT0_S7_PS2_liif",
+}
+
+
+def _full_fixture(tmp_path):
+    """The C2 fixture plus one kernel of every other config."""
     stats, fetch, write = _fixture(tmp_path)
+    for path, rows in ((stats, [[n, 4, 400, 100, 0, 90, 110, 1] for n in CONFIG_SYMBOLS.values()]),
+                       (fetch, [[9, 9, n, "FETCH_SIZE", 100.0] for n in CONFIG_SYMBOLS.values()]),
+                       (write, [[9, 9, n, "WRITE_SIZE", 100.0] for n in CONFIG_SYMBOLS.values()])):
+        with open(path, "a", newline="") as f:
+            csv.writer(f).writerows(rows)
+    return stats, fetch, write
+
+
+def test_every_config_symbol_is_recognised():
+    for key, name in CONFIG_SYMBOLS.items():
+        assert rs.classify(name, rs.CONFIG_KERNELS) == key, key
+
+
+def test_a_workload_without_a_kernel_is_an_error(tmp_path):
+    """A renamed kernel template must not silently drop a workload (bench.py
+    reads the traffic lines)."""
+    stats, fetch, write = _fixture(tmp_path)
+    with pytest.raises(ValueError, match="C1_layer_norm"):
+        rs.render("configs", stats, fetch, write)
+
+
+def test_rendered_headers_and_machine_lines(tmp_path):
+    stats, fetch, write = _full_fixture(tmp_path)
     trace_txt, traffic_txt = rs.render("configs", stats, fetch, write)
     assert f"-d {stats.parent} -o all -- " in trace_txt
     assert f"--pmc FETCH_SIZE --output-format csv -d {fetch.parent} -o all" in traffic_txt
