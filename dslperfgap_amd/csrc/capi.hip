@@ -100,6 +100,10 @@ int it_target(int op, int64_t nvec, int vec) {
     while (it > 1 && nvec / it < kMinLanesShort[op]) it /= 2;
     return it;
   }
+  // fp32 softmax rows of 33-64 vectors: one wave per row (log_softmax fp32,
+  // 64 MB per call: 256 columns 5730 -> 5849 GB/s, 255 columns 4843 -> 5241;
+  // 512 columns and more keep 2 vectors per lane, within 1% of the best)
+  if (op == VBH_OP_SOFTMAX && vec == 4 && nvec <= kWave) return 1;
   if (vec > 1) {
     if (op == VBH_OP_CROSS_ENTROPY) return 8;
     if (op == VBH_OP_LOGSUMEXP && vec == 8 && nvec > kMidRowVecs) return 8;
