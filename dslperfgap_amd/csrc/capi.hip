@@ -426,9 +426,14 @@ int vbh_layer_norm_fwd(const void* x, const void* w, const void* b, void* y, int
   const int vn = 16 / elt_size(dtype);
   const bool vec_ok = cols % vn == 0 && aligned16(x) && aligned16(y) && aligned16(w) &&
                       (b == nullptr || aligned16(b));
-  const Geometry g =
-      geometry_for(VBH_OP_LAYER_NORM, cols, vec_ok ? vn : 1, rows,
-                   mul_sat(mul_sat(rows, cols), elt_size(dtype)));
+  // MIS: rows not whole vectors, x / y rows at the same offsets, weights read
+  // as aligned vectors and shifted to each row's offset
+  const bool mis_ok = cols % vn != 0 && aligned16(x) && aligned16(y) && aligned16(w) &&
+                      (b == nullptr || aligned16(b)) && cols >= kMisMinVecs * vn;
+  const int64_t out_bytes = mul_sat(mul_sat(rows, cols), elt_size(dtype));
+  Geometry g = geometry_for(VBH_OP_LAYER_NORM, cols, vec_ok || mis_ok ? vn : 1, rows, out_bytes);
+  if (mis_ok && use_mis(g, vn)) g.persist = false;  // the MIS kernel is one row group per row
+  else if (mis_ok) g = geometry_for(VBH_OP_LAYER_NORM, cols, 1, rows, out_bytes);
   if (int rc = check_grid(rows, g)) return rc;
   return hip_status(launch_layer_norm(x, w, b, y, rows, static_cast<int>(cols), eps, dtype,
                                       w_dtype, g, static_cast<hipStream_t>(stream)),
@@ -448,9 +453,12 @@ int vbh_rms_norm_fwd(const void* x, const void* w, void* y, int64_t rows, int64_
   if (!x || !w || !y) return fail(VBH_E_INVALID, "rms_norm: null pointer");
   const int vn = 16 / elt_size(dtype);
   const bool vec_ok = cols % vn == 0 && aligned16(x) && aligned16(y) && aligned16(w);
-  const Geometry g =
-      geometry_for(VBH_OP_RMS_NORM, cols, vec_ok ? vn : 1, rows,
-                   mul_sat(mul_sat(rows, cols), elt_size(dtype)));
+  const bool mis_ok = cols % vn != 0 && aligned16(x) && aligned16(y) && aligned16(w) &&
+                      cols >= kMisMinVecs * vn;
+  const int64_t out_bytes = mul_sat(mul_sat(rows, cols), elt_size(dtype));
+  Geometry g = geometry_for(VBH_OP_RMS_NORM, cols, vec_ok || mis_ok ? vn : 1, rows, out_bytes);
+  if (mis_ok && use_mis(g, vn)) g.persist = false;  // the MIS kernel is one row group per row
+  else if (mis_ok) g = geometry_for(VBH_OP_RMS_NORM, cols, 1, rows, out_bytes);
   if (int rc = check_grid(rows, g)) return rc;
   return hip_status(launch_rms_norm(x, w, y, rows, static_cast<int>(cols), eps, dtype,
                                     w_dtype, g, static_cast<hipStream_t>(stream)),

@@ -233,6 +233,135 @@ __global__ __launch_bounds__(kMaxBlock) void rms_norm_rows(
 }
 
 // ---------------------------------------------------------------------------
+// rows not a multiple of V long (MIS): each row, starting at element `start`
+// of a 16-byte aligned buffer, is a scalar head up to the first 16-byte
+// boundary (lanes g < head hold element g), whole aligned vectors and a
+// scalar tail (lanes g < tail); the launcher makes tpr >= V.  The weight and
+// bias of body vector j are elements [head + j V, head + j V + V), read as
+// vectors at the nearest dword boundary (row_weights).  Nothing outside the
+// row or the weights is read or written.
+// ---------------------------------------------------------------------------
+
+struct NormMisRow {
+  int head, nvec, tail;
+};
+
+template <int V>
+__device__ __forceinline__ NormMisRow norm_mis_row(int64_t start, int cols) {
+  int head = static_cast<int>((V - start % V) % V);
+  if (head > cols) head = cols;
+  const int nvec = (cols - head) / V;
+  return NormMisRow{head, nvec, cols - head - nvec * V};
+}
+
+// Global loads of several dwords need only dword alignment on gfx9, so the
+// weights of body vector j come from one vector load at a dword boundary:
+// elements [head + jV, head + jV + V) themselves for 4-byte weights and for
+// 16-bit weights at an even head; at an odd head, 16-bit weights load the V
+// elements from one element earlier plus element head + jV + V - 1 (inside
+// the body) and take each element from its upper neighbour.  No branch on
+// `head`, so a wave holding rows of different heads does not diverge.
+template <typename TW, int V>
+__device__ __forceinline__ void row_weights(const TW* __restrict__ w, int j, int head,
+                                            float (&out)[V]) {
+  typedef typename Raw<TW, V>::type RW;
+  const TW* p = w + head + static_cast<int64_t>(j) * V;
+  RW a;
+  if constexpr (sizeof(TW) == 4) {
+    __builtin_memcpy(&a, __builtin_assume_aligned(p, 4), sizeof(a));
+#pragma unroll
+    for (int k = 0; k < V; ++k) out[k] = raw_at<TW, V>(a, k);
+  } else {
+    static_assert(sizeof(TW) == 2, "16-bit or 4-byte weights");
+    const int odd = head & 1;
+    __builtin_memcpy(&a, __builtin_assume_aligned(p - odd, 4), sizeof(a));
+    const float last = odd ? static_cast<float>(p[V - 1]) : 0.f;
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      const float up = k + 1 < V ? raw_at<TW, V>(a, k + 1) : last;
+      out[k] = odd ? up : raw_at<TW, V>(a, k);
+    }
+  }
+}
+
+template <typename T, typename TW, int V, int IT, int SP, bool RMS>
+__global__ __launch_bounds__(kMaxBlock) void norm_rows_mis(
+    const T* __restrict__ x, const TW* __restrict__ w, const TW* __restrict__ b,
+    T* __restrict__ y, int64_t rows, int cols, int tpr, float eps) {
+  typedef typename Raw<T, V>::type RT;
+  __shared__ float lds[2][kMaxWaves];
+  const int g = threadIdx.x % tpr;
+  const int rpb = blockDim.x / tpr;
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * rpb;
+  int64_t row = first + threadIdx.x / tpr;
+  const bool live = row < rows;
+  if (!live) row = rows - 1;
+  const int64_t start = row * cols;
+  const NormMisRow mr = norm_mis_row<V>(start, cols);
+  const int nvec = mr.nvec;
+  const T* xb = x + start + mr.head;
+
+  RT xr[IT];
+  load_raw_row<T, V, IT, SP != kStoreCached>(xb, nvec, g, tpr, xr);
+  const bool hv = g < mr.head, tv = g < mr.tail;
+  const int tcol = mr.head + nvec * V + g;  // this lane's tail column
+  const float hx = hv ? static_cast<float>(x[start + g]) : 0.f;
+  const float tx = tv ? static_cast<float>(x[start + tcol]) : 0.f;
+  float mean = 0.f, scale;
+  if constexpr (RMS) {
+    const float ss = group_allreduce<Sum>(lane_sumsq<T, V, IT>(xr) + hx * hx + tx * tx, tpr,
+                                          lds[0]);
+    scale = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+  } else {
+    mean = group_allreduce<Sum>(lane_sum<T, V, IT>(xr) + hx + tx, tpr, lds[0]) /
+           static_cast<float>(cols);
+    reload_barrier<T, V, IT>(xr);
+    float c2 = lane_centered_sumsq<T, V, IT>(xr, mean, nvec, g, tpr);
+    if (hv) c2 = fmaf(hx - mean, hx - mean, c2);
+    if (tv) c2 = fmaf(tx - mean, tx - mean, c2);
+    const float m2 = group_allreduce<Sum>(c2, tpr, lds[1]);
+    scale = 1.0f / sqrtf(m2 / static_cast<float>(cols) + eps);
+  }
+  if (!live) return;
+  reload_barrier<T, V, IT>(xr);
+
+  // element c of this row's output, from its value v
+  auto out_at = [&](float v, int c) {
+    const float wv = static_cast<float>(w[c]);
+    if constexpr (RMS) return (v * scale) * wv;
+    const float bv = b != nullptr ? static_cast<float>(b[c]) : 0.f;
+    return (v - mean) * scale * wv + bv;
+  };
+  const OutWindow<T, SP> out(y + first * cols, std::min<int64_t>(rpb, rows - first) * cols);
+  T* yb = y + start + mr.head;
+  const int yoff = static_cast<int>(row - first) * cols + mr.head;
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    const int j = i * tpr + g;
+    if (j < nvec) {
+      float wv[V], bv[V], o[V];
+      row_weights<TW, V>(w, j, mr.head, wv);
+      if (!RMS && b != nullptr) row_weights<TW, V>(b, j, mr.head, bv);
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        const float v = raw_at<T, V>(xr[i], k);
+        if constexpr (RMS) o[k] = (v * scale) * wv[k];
+        else o[k] = (v - mean) * scale * wv[k] + (b != nullptr ? bv[k] : 0.f);
+      }
+      out.template store<V>(yb + static_cast<int64_t>(j) * V, yoff + j * V, o);
+    }
+  }
+  if (hv) {
+    const float o = out_at(hx, g);
+    store_from_f32<T, 1>(y + start + g, &o);
+  }
+  if (tv) {
+    const float o = out_at(tx, tcol);
+    store_from_f32<T, 1>(y + start + tcol, &o);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // persistent pipelined kernels
 //
 // Row group `grp` of workgroup `blk` handles rows blk*rpb + grp, then
@@ -537,6 +666,17 @@ hipError_t launch_layer_norm(const void* x, const void* w, const void* b, void* 
           if constexpr (M <= lane_cap(V)) {
             dispatch_store_policy<V>(g, [&](auto sp) {
               constexpr int SP = decltype(sp)::value;
+              if constexpr (V > 1) {
+                if (g.mis) {
+                  hipLaunchKernelGGL((norm_rows_mis<T, TW, V, M, SP, false>),
+                                     dim3(grid_for(rows, g)), dim3(g.block), 0, s,
+                                     static_cast<const T*>(x), static_cast<const TW*>(w),
+                                     static_cast<const TW*>(b), static_cast<T*>(y), rows, cols,
+                                     g.tpr, eps);
+                  err = hipGetLastError();
+                  return;
+                }
+              }
               constexpr int PC = pipe_cap<T, TW, V, 2>();
               constexpr int MP = M <= PC ? M : PC;
               auto pipe_k = pipe_full<T>(g, cols / V, MP)
@@ -583,6 +723,17 @@ hipError_t launch_rms_norm(const void* x, const void* w, void* y, int64_t rows, 
           if constexpr (M <= lane_cap(V)) {
             dispatch_store_policy<V>(g, [&](auto sp) {
               constexpr int SP = decltype(sp)::value;
+              if constexpr (V > 1) {
+                if (g.mis) {
+                  hipLaunchKernelGGL((norm_rows_mis<T, TW, V, M, SP, true>),
+                                     dim3(grid_for(rows, g)), dim3(g.block), 0, s,
+                                     static_cast<const T*>(x), static_cast<const TW*>(w),
+                                     static_cast<const TW*>(nullptr), static_cast<T*>(y), rows,
+                                     cols, g.tpr, eps);
+                  err = hipGetLastError();
+                  return;
+                }
+              }
               constexpr int PC = pipe_cap<T, TW, V, 1>();
               constexpr int MP = M <= PC ? M : PC;
               auto pipe_k = pipe_full<T>(g, cols / V, MP)

@@ -863,3 +863,36 @@ def test_misaligned_cross_entropy(dtype, smooth):
             for k, (t, w) in enumerate(zip(got, want)):
                 check(t.reshape(-1)[:n], w.reshape(-1)[:n], torch.float32,
                       what=f"misaligned ce[{k}] {dtype} cols={cols} bs={bs} smooth={smooth}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("wdt", ["same", "fp32"])
+def test_misaligned_rows_norms(dtype, wdt):
+    """LayerNorm / RMSNorm rows not a multiple of the vector width (head /
+    aligned body / tail, weights read at each row's shift): every residue of
+    cols modulo the vector width and 50257, rows starting at every offset within
+    a vector, fp32 weights with 16-bit rows, with and without bias, a constant
+    row (LayerNorm output = bias), and weights one element past a 16-byte
+    boundary (the scalar kernel)."""
+    vn = 16 // torch.empty(0, dtype=dtype).element_size()
+    w_dtype = dtype if wdt == "same" else torch.float32
+    for cols in [4 * vn + r for r in range(1, vn)] + [50257]:
+        rows = 2 * vn + 1
+        g = _g(900 + cols)
+        x = (2 * torch.randn(rows, cols, generator=g) + 0.5).to(dtype)
+        x[1, :] = 3.0
+        w = (1 + 0.1 * torch.randn(cols, generator=g)).to(w_dtype)
+        b = (0.1 * torch.randn(cols, generator=g)).to(w_dtype)
+        xd, wd, bd = cuda(x, w, b)
+        what = f"misaligned {dtype} w {w_dtype} cols={cols}"
+        check(layer_norm(xd, wd, bd), ref.layer_norm(x, w, b), dtype, what="layer_norm " + what)
+        check(layer_norm(xd, wd, None), ref.layer_norm(x, w, None), dtype,
+              what="layer_norm no bias " + what)
+        check(rms_norm(xd, (cols,), wd, 1e-6), ref.rms_norm(x, (cols,), w, 1e-6), dtype,
+              what="rms_norm " + what)
+        wm = torch.empty(cols + 1, dtype=w_dtype, device=wd.device)[1:]
+        wm.copy_(wd)
+        check(layer_norm(xd, wm, bd), ref.layer_norm(x, w, b), dtype,
+              what="layer_norm offset weights " + what)
+        check(rms_norm(xd, (cols,), wm, 1e-6), ref.rms_norm(x, (cols,), w, 1e-6), dtype,
+              what="rms_norm offset weights " + what)
