@@ -199,19 +199,39 @@ constexpr int64_t kSplitTarget = 1024;      // segments per launch to aim for
 constexpr int64_t kSplitMinVecs = 512;      // 16-byte vectors per segment, at least
 constexpr int kSplitMaxSegs = 64;
 
-// Segments per row (a power of two dividing the row's vectors), or 1.
-// `long_from`: the op also splits launches of long_from to 511 rows of long
-// rows (0: it does not).
-int split_segments(int64_t rows, int64_t nvec, int64_t long_from = 0) {
+// Segments per row (a power of two dividing the row's vectors unless `even` is
+// false), or 1.  `long_from`: the op also splits launches of long_from to 511
+// rows of long rows (0: it does not).
+int split_segments(int64_t rows, int64_t nvec, int64_t long_from = 0, bool even = true) {
   const bool few = rows > 0 && rows < kSplitMaxRows && nvec >= kSplitRowVecs;
   const bool two_rounds = long_from > 0 && rows >= long_from && rows < kSplitMaxRowsLong &&
                           nvec >= kSplitLongVecs;
   if (!few && !two_rounds) return 1;
   int segs = 1;
-  while (segs < kSplitMaxSegs && rows * segs < kSplitTarget && nvec % (2 * segs) == 0 &&
-         nvec / (2 * segs) >= kSplitMinVecs)
+  while (segs < kSplitMaxSegs && rows * segs < kSplitTarget &&
+         (!even || nvec % (2 * segs) == 0) && nvec / (2 * segs) >= kSplitMinVecs)
     segs *= 2;
   return segs;
+}
+
+// A split of rows of `cols` columns: `segs` segments of `seg_cols` columns.
+// Rows of whole vectors split evenly (split_segments); other rows (run by the
+// MIS kernels, each segment with its own head and tail) into segments of a
+// whole number of vectors, the last one shorter.
+struct RowSplit {
+  int segs;
+  int64_t seg_cols;
+};
+
+RowSplit split_row(int64_t rows, int64_t cols, int vn, int64_t long_from) {
+  if (cols % vn == 0) {
+    const int segs = split_segments(rows, cols / vn, long_from);
+    return RowSplit{segs, cols / segs};
+  }
+  const int segs = split_segments(rows, cols / vn, long_from, false);
+  if (segs == 1) return RowSplit{1, cols};
+  const int64_t seg_cols = ((cols + segs - 1) / segs + vn - 1) / vn * vn;
+  return RowSplit{static_cast<int>((cols + seg_cols - 1) / seg_cols), seg_cols};
 }
 
 // Rows whose length is not a multiple of the 16-byte vector (GPT-2's 50257
@@ -516,10 +536,9 @@ int vbh_softmax_dim_fwd(const void* x, void* y, int64_t outer, int64_t n, int64_
 int64_t vbh_logsumexp_workspace_bytes(int64_t rows, int64_t cols, int in_dtype) {
   if (!is_float(in_dtype) || rows <= 0 || cols <= 0 || cols > kMaxCols) return 0;
   const int vn = 16 / elt_size(in_dtype);
-  if (cols % vn != 0 || g_tpr[VBH_OP_LOGSUMEXP].load() || g_block[VBH_OP_LOGSUMEXP].load())
-    return 0;
-  const int segs = split_segments(rows, cols / vn, kSplitMaxRows);
-  return segs > 1 ? rows * segs * static_cast<int64_t>(sizeof(float)) : 0;
+  if (g_tpr[VBH_OP_LOGSUMEXP].load() || g_block[VBH_OP_LOGSUMEXP].load()) return 0;
+  const RowSplit sp = split_row(rows, cols, vn, kSplitMaxRows);
+  return sp.segs > 1 ? rows * sp.segs * static_cast<int64_t>(sizeof(float)) : 0;
 }
 
 int vbh_logsumexp_fwd_ws(const void* x, void* y, int64_t rows, int64_t cols, int in_dtype,
@@ -538,18 +557,27 @@ int vbh_logsumexp_fwd_ws(const void* x, void* y, int64_t rows, int64_t cols, int
   const bool vec_ok = cols % vn == 0 && aligned16(x);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t need = vbh_logsumexp_workspace_bytes(rows, cols, in_dtype);
-  if (need > 0 && vec_ok && workspace != nullptr && workspace_bytes >= need &&
+  if (need > 0 && aligned16(x) && workspace != nullptr && workspace_bytes >= need &&
       aligned16(workspace)) {
-    // segment results in fp32, then a logsumexp over each row's segments
-    const int segs = split_segments(rows, cols / vn, kSplitMaxRows);
+    // segment results in fp32, then a logsumexp over each row's segments;
+    // rows of whole vectors as a [rows * segs, seg_cols] view, other rows
+    // through the MIS kernel's segment mode
+    const RowSplit sp = split_row(rows, cols, vn, kSplitMaxRows);
+    const int segs = sp.segs;
     const int64_t units = rows * segs;
-    const int seg_cols = static_cast<int>(cols / segs);
-    const Geometry g1 = geometry_for(VBH_OP_LOGSUMEXP, seg_cols, vn, units);
-    if (int rc = check_grid(units, g1)) return rc;
-    const Geometry g2 = geometry_for(VBH_OP_LOGSUMEXP, segs, segs % 4 == 0 ? 4 : 1, rows);
-    hipError_t e = launch_logsumexp(x, workspace, units, seg_cols, in_dtype, kF32, g1, s);
-    if (e == hipSuccess) e = launch_logsumexp(workspace, y, rows, segs, kF32, out_dtype, g2, s);
-    return hip_status(e, "logsumexp launch");
+    const int seg_cols = static_cast<int>(sp.seg_cols);
+    Geometry g1 = geometry_for(VBH_OP_LOGSUMEXP, seg_cols, vn, units);
+    if (vec_ok || use_mis(g1, vn)) {
+      if (int rc = check_grid(units, g1)) return rc;
+      const Geometry g2 = geometry_for(VBH_OP_LOGSUMEXP, segs, segs % 4 == 0 ? 4 : 1, rows);
+      hipError_t e =
+          vec_ok ? launch_logsumexp(x, workspace, units, seg_cols, in_dtype, kF32, g1, s)
+                 : launch_logsumexp(x, workspace, units, static_cast<int>(cols), in_dtype, kF32,
+                                    g1, s, segs, seg_cols);
+      if (e == hipSuccess)
+        e = launch_logsumexp(workspace, y, rows, segs, kF32, out_dtype, g2, s);
+      return hip_status(e, "logsumexp launch");
+    }
   }
   const bool mis_ok = !vec_ok && aligned16(x) && cols >= kMisMinVecs * vn;
   Geometry g = geometry_for(VBH_OP_LOGSUMEXP, cols, vec_ok || mis_ok ? vn : 1, rows);
@@ -571,12 +599,10 @@ int64_t vbh_cross_entropy_workspace_bytes(int64_t n_rows, int64_t n_cols, int64_
       block_size < n_cols)  // one column block per row only
     return 0;
   const int vn = 16 / elt_size(logits_dtype);
-  if (n_cols % vn != 0 || g_tpr[VBH_OP_CROSS_ENTROPY].load() ||
-      g_block[VBH_OP_CROSS_ENTROPY].load())
-    return 0;
-  const int segs = split_segments(n_rows, n_cols / vn, kSplitMaxRows + 1);
+  if (g_tpr[VBH_OP_CROSS_ENTROPY].load() || g_block[VBH_OP_CROSS_ENTROPY].load()) return 0;
+  const RowSplit sp = split_row(n_rows, n_cols, vn, kSplitMaxRows + 1);
   // segment loss, lse and (unused) z_loss
-  return segs > 1 ? 3 * n_rows * segs * static_cast<int64_t>(sizeof(float)) : 0;
+  return sp.segs > 1 ? 3 * n_rows * sp.segs * static_cast<int64_t>(sizeof(float)) : 0;
 }
 
 int vbh_cross_entropy_fwd_ws(const void* logits, const void* labels, int logits_dtype,
@@ -629,25 +655,28 @@ int vbh_cross_entropy_fwd_ws(const void* logits, const void* labels, int logits_
   a.split = split != 0;
   const int64_t need =
       vbh_cross_entropy_workspace_bytes(n_rows, n_cols, block_size, logits_dtype);
-  if (need > 0 && vec_ok && workspace != nullptr && workspace_bytes >= need &&
+  if (need > 0 && aligned16(logits) && workspace != nullptr && workspace_bytes >= need &&
       aligned16(workspace)) {
     // first stage: the row's segments as column blocks with SPLIT semantics
-    const int segs = split_segments(n_rows, n_cols / vn, kSplitMaxRows + 1);
+    // (the MIS kernel where a segment does not start at a vector boundary)
+    const RowSplit sp = split_row(n_rows, n_cols, vn, kSplitMaxRows + 1);
+    const int segs = sp.segs;
     const int64_t units = n_rows * segs;
-    const Geometry g1 =
-        geometry_for(VBH_OP_CROSS_ENTROPY, n_cols / segs, vn, units);
-    if (int rc = check_grid(units, g1)) return rc;
-    CeArgs p = a;
-    p.loss = static_cast<float*>(workspace);
-    p.lse = p.loss + units;
-    p.z_loss = p.lse + units;
-    p.block_size = static_cast<int>(n_cols / segs);
-    p.ncb = segs;
-    p.split = 1;
-    p.empty_neg_inf = 1;
-    hipError_t e = launch_cross_entropy_fwd(p, g1, s);
-    if (e == hipSuccess) e = launch_cross_entropy_combine(a, p.loss, p.lse, segs, s);
-    return hip_status(e, "cross_entropy_fwd launch");
+    Geometry g1 = geometry_for(VBH_OP_CROSS_ENTROPY, sp.seg_cols, vn, units);
+    if (vec_ok || use_mis(g1, vn)) {
+      if (int rc = check_grid(units, g1)) return rc;
+      CeArgs p = a;
+      p.loss = static_cast<float*>(workspace);
+      p.lse = p.loss + units;
+      p.z_loss = p.lse + units;
+      p.block_size = static_cast<int>(sp.seg_cols);
+      p.ncb = segs;
+      p.split = 1;
+      p.empty_neg_inf = 1;
+      hipError_t e = launch_cross_entropy_fwd(p, g1, s);
+      if (e == hipSuccess) e = launch_cross_entropy_combine(a, p.loss, p.lse, segs, s);
+      return hip_status(e, "cross_entropy_fwd launch");
+    }
   }
   const int64_t segments = mul_sat(n_rows, ncb);
   const bool mis_ok = !vec_ok && aligned16(logits) && bs >= kMisMinVecs * vn;

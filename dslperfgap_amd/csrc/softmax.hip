@@ -155,18 +155,30 @@ __global__ __launch_bounds__(kMaxBlock) void softmax_rows(const Ti* __restrict__
   }
 }
 
+// `rows` units of `cols` columns.  MIS launches may instead split each row of
+// `cols` columns into `segs` segments of `seg_cols` columns (the last one
+// shorter): unit u is then segment u % segs of row u / segs, and y[u] its
+// logsumexp.
 template <typename Ti, typename To, int V, int IT, bool NT, bool MIS>
 __global__ __launch_bounds__(kMaxBlock) void logsumexp_rows(const Ti* __restrict__ x,
                                                             To* __restrict__ y, int64_t rows,
-                                                            int cols, int tpr) {
+                                                            int cols, int tpr, int segs,
+                                                            int seg_cols) {
   typedef typename Raw<Ti, V>::type RT;
   __shared__ float lds[2][kMaxWaves];
   const int g = threadIdx.x % tpr;
   int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / tpr) + threadIdx.x / tpr;
   const bool live = row < rows;
   if (!live) row = rows - 1;
-  const int64_t start = row * cols;
-  const MisRow mr = MIS ? mis_row<V>(start, cols) : MisRow{0, cols / V, 0};
+  int64_t start = row * cols;
+  int len = cols;
+  if (MIS && segs > 1) {
+    const int64_t r = row / segs;
+    const int k = static_cast<int>(row - r * segs);
+    start = r * cols + static_cast<int64_t>(k) * seg_cols;
+    len = min(seg_cols, cols - k * seg_cols);
+  }
+  const MisRow mr = MIS ? mis_row<V>(start, len) : MisRow{0, cols / V, 0};
   const int nvec = mr.nvec;
   const Ti* xb = x + start + mr.head;
 
@@ -378,7 +390,7 @@ hipError_t launch_softmax(const void* x, void* y, int64_t rows, int cols, int id
 }
 
 hipError_t launch_logsumexp(const void* x, void* y, int64_t rows, int cols, int idt, int odt,
-                            const Geometry& g, hipStream_t s) {
+                            const Geometry& g, hipStream_t s, int segs, int seg_cols) {
   hipError_t err = hipErrorInvalidValue;
   auto body = [&](auto ti, auto to) {
     using Ti = typename decltype(ti)::type;
@@ -398,7 +410,7 @@ hipError_t launch_logsumexp(const void* x, void* y, int64_t rows, int cols, int 
           auto launch = [&](auto kern) {
             hipLaunchKernelGGL(kern, dim3(grid_for(rows, g)), dim3(g.block), 0, s,
                                static_cast<const Ti*>(x), static_cast<To*>(y), rows, cols,
-                               g.tpr);
+                               g.tpr, segs, seg_cols);
           };
           if (V > 1 && g.mis) launch(logsumexp_rows<Ti, To, V, M, true, V != 1>);
           else if (g.nt) launch(logsumexp_rows<Ti, To, V, M, true, false>);

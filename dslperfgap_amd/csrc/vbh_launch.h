@@ -137,8 +137,11 @@ hipError_t launch_softmax(const void* x, void* y, int64_t rows, int cols, int id
 hipError_t launch_softmax_dim(const void* x, void* y, int64_t outer, int n,
                               int64_t inner, int idt, int odt, int log_mode,
                               hipStream_t s);
+// segs > 1 (MIS geometry only): each of rows / segs rows of `cols` columns is
+// split into segs segments of seg_cols columns, the last one shorter.
 hipError_t launch_logsumexp(const void* x, void* y, int64_t rows, int cols, int idt,
-                            int odt, const Geometry& g, hipStream_t s);
+                            int odt, const Geometry& g, hipStream_t s, int segs = 1,
+                            int seg_cols = 0);
 
 struct CeArgs {
   const void* logits;

@@ -706,12 +706,13 @@ def test_vocab_parallel_cross_entropy_at_c4():
 # logsumexp of few long rows: the split path
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("rows,cols", [(1, 262144), (3, 131072), (33, 131072), (255, 131072),
-                                       (300, 131072)])
+                                       (300, 131072), (3, 131075), (300, 100003)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_split_logsumexp(rows, cols, dtype):
     """Launches that split every row (the workspace query says so) match the
     oracle, with special rows: all -inf (-inf), one +inf (+inf), one NaN
-    (NaN), and a large value in one late segment only."""
+    (NaN), and a large value in one late segment only.  Rows that are not
+    whole 16-byte vectors split into segments with their own head and tail."""
     code = {torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}[dtype]
     assert _lib.logsumexp_workspace_bytes(rows, cols, code) > 0
     x = (3 * torch.randn(rows, cols, generator=_g(400 + rows))).to(dtype)
@@ -727,10 +728,11 @@ def test_split_logsumexp(rows, cols, dtype):
     check(got, want, dtype, what=f"split logsumexp {rows}x{cols} {dtype}")
 
 
-def test_split_logsumexp_matches_the_unsplit_kernel():
+@pytest.mark.parametrize("cols", [131072, 131077])
+def test_split_logsumexp_matches_the_unsplit_kernel(cols):
     """The same launch through vbh_logsumexp_fwd_ws with and without a
     workspace: the split and unsplit kernels agree to fp32 rounding."""
-    rows, cols = 7, 131072
+    rows = 7
     x = (3 * torch.randn(rows, cols, generator=_g(410))).to(DEV)
     need = _lib.logsumexp_workspace_bytes(rows, cols, _lib.F32)
     assert need > 0
@@ -759,7 +761,10 @@ CE_SPLIT_PARAMS = [
 @pytest.mark.parametrize("rows,cols,dtype", [(1, 65536, torch.float32), (7, 131072, torch.float32),
                                              (100, 131072, torch.bfloat16),
                                              (300, 131072, torch.float32),
-                                             (33, 262144, torch.float16)])
+                                             (33, 262144, torch.float16),
+                                             (5, 131075, torch.float32),
+                                             (300, 100003, torch.bfloat16),
+                                             (7, 131073, torch.float16)])
 @pytest.mark.parametrize("pi", range(len(CE_SPLIT_PARAMS)))
 def test_split_cross_entropy(rows, cols, dtype, pi):
     """Launches that split every row match the oracle on every output: labels
@@ -791,10 +796,11 @@ def test_split_cross_entropy(rows, cols, dtype, pi):
         assert torch.isfinite(got[1].reshape(-1)[0]).item()   # the masked row's lse
 
 
-def test_split_cross_entropy_matches_the_unsplit_kernel():
+@pytest.mark.parametrize("cols", [131072, 131077])
+def test_split_cross_entropy_matches_the_unsplit_kernel(cols):
     """One launch through vbh_cross_entropy_fwd_ws with and without a workspace:
     the split and unsplit results agree to fp32 rounding."""
-    rows, cols = 9, 131072
+    rows = 9
     g = _g(520)
     logits = (2 * torch.randn(rows, cols, generator=g)).to(DEV)
     labels = torch.randint(0, cols, (rows,), generator=g).to(DEV)

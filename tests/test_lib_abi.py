@@ -247,7 +247,8 @@ def test_split_workspace_sizes():
     assert lse(64, 50304, _lib.F32) == 0                  # 200 KB rows: not worth a split
     assert lse(1, 65536, _lib.F16) == 0                   # 128 KB row
     assert lse(4, 1000, _lib.F32) == 0                    # too short to split
-    assert lse(4, 65537, _lib.F32) == 0                   # not whole 16-byte vectors
+    assert lse(4, 65537, _lib.F32) == 4 * 32 * 4          # not whole vectors: 31 x 2052 + 1925
+    assert lse(333, 50257, _lib.F32) == 333 * 4 * 4       # long rows, 4 segments of 12568
     assert lse(4, 65536, 9) == 0 and lse(0, 65536, _lib.F32) == 0
     assert red(128, 131072, 1, _lib.F32, _lib.REDUCE_MEAN) == 128 * 8 * 4
     assert red(128, 131072, 1, _lib.F32, _lib.REDUCE_MAX) == 128 * 8 * (8 + 4)
@@ -258,6 +259,8 @@ def test_split_workspace_sizes():
     assert ce(64, 128256, 1 << 17, _lib.F32) == 3 * 64 * 16 * 4  # one block per row
     assert ce(64, 128256, 32768, _lib.F32) == 0           # several column blocks: not split
     assert ce(64, 50304, 65536, _lib.F32) == 0
+    assert ce(333, 50257, 65536, _lib.F32) == 3 * 333 * 4 * 4  # long rows, not whole vectors
+    assert ce(667, 50257, 65536, _lib.BF16) == 0          # 667 rows: not split
     try:
         _lib.tune_override(_lib.OP_LOGSUMEXP, 64, 0, 0)
         assert _lib.logsumexp_workspace_bytes(128, 131072, _lib.F32) == 0
