@@ -104,6 +104,12 @@ int it_target(int op, int64_t nvec, int vec) {
   // 64 MB per call: 256 columns 5730 -> 5849 GB/s, 255 columns 4843 -> 5241;
   // 512 columns and more keep 2 vectors per lane, within 1% of the best)
   if (op == VBH_OP_SOFTMAX && vec == 4 && nvec <= kWave) return 1;
+  // 16-bit LayerNorm rows of 1025-1536 vectors: 2 vectors per lane, 9-12 waves
+  // per row (bf16 at 64 MB per call, 4 -> 2: 9216 columns 4298 -> 5247 GB/s,
+  // 10240 4501 -> 5194, 11264 4855 -> 5199, 12288 5126 -> 5290; at 768 and
+  // 896 vectors 2 per lane loses 1-8%, from 1664 vectors on 13 or more waves
+  // per row lose 6%)
+  if (op == VBH_OP_LAYER_NORM && vec == 8 && nvec > 1024 && nvec <= 1536) return 2;
   if (vec > 1) {
     if (op == VBH_OP_CROSS_ENTROPY) return 8;
     if (op == VBH_OP_LOGSUMEXP && vec == 8 && nvec > kMidRowVecs) return 8;
