@@ -51,6 +51,8 @@ SIGNATURES = {
     "vbh_layer_norm_fwd": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _i32, _vp]),
     "vbh_rms_norm_fwd": (_i32, [_vp, _vp, _vp, _i64, _i64, _f32, _i32, _i32, _vp]),
     "vbh_softmax_fwd": (_i32, [_vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp]),
+    "vbh_softmax_fwd_ws": (_i32, [_vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp, _i64, _vp]),
+    "vbh_softmax_workspace_bytes": (_i64, [_i64, _i64, _i32]),
     "vbh_softmax_dim_fwd": (_i32, [_vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32, _vp]),
     "vbh_logsumexp_fwd": (_i32, [_vp, _vp, _i64, _i64, _i32, _i32, _vp]),
     "vbh_logsumexp_fwd_ws": (_i32, [_vp, _vp, _i64, _i64, _i32, _i32, _vp, _i64, _vp]),
@@ -82,7 +84,8 @@ SIGNATURES = {
 
 # entry points _vbhfast binds (every launching one)
 FAST_ENTRY_POINTS = (
-    "vbh_layer_norm_fwd", "vbh_rms_norm_fwd", "vbh_softmax_fwd", "vbh_softmax_dim_fwd",
+    "vbh_layer_norm_fwd", "vbh_rms_norm_fwd", "vbh_softmax_fwd", "vbh_softmax_fwd_ws",
+    "vbh_softmax_dim_fwd",
     "vbh_logsumexp_fwd", "vbh_logsumexp_fwd_ws", "vbh_cross_entropy_fwd",
     "vbh_cross_entropy_fwd_ws", "vbh_cross_entropy_bwd", "vbh_reduce_fwd", "vbh_reduce_fwd_ws",
     "vbh_stream_copy",
@@ -170,6 +173,7 @@ def tune_override(op: int, tpr: int = 0, block: int = 0, flags: int = 0) -> None
     call("vbh_tune_override", op, tpr, block, flags)
     # an overridden geometry turns the row split off (and back on when cleared)
     logsumexp_workspace_bytes.cache_clear()
+    softmax_workspace_bytes.cache_clear()
     reduce_workspace_bytes.cache_clear()
     cross_entropy_workspace_bytes.cache_clear()
 
@@ -178,6 +182,12 @@ def tune_override(op: int, tpr: int = 0, block: int = 0, flags: int = 0) -> None
 def logsumexp_workspace_bytes(rows: int, cols: int, in_dtype: int) -> int:
     """Workspace bytes that split a logsumexp launch (0: no split)."""
     return lib().vbh_logsumexp_workspace_bytes(rows, cols, in_dtype)
+
+
+@functools.lru_cache(maxsize=4096)
+def softmax_workspace_bytes(rows: int, cols: int, in_dtype: int) -> int:
+    """Workspace bytes that split a softmax / log_softmax launch (0: no split)."""
+    return lib().vbh_softmax_workspace_bytes(rows, cols, in_dtype)
 
 
 @functools.lru_cache(maxsize=4096)

@@ -81,7 +81,9 @@ constexpr int64_t kMidRowVecs = 256;
 // every width (fp32 +6 to +18%, bf16 +12 to +22% over 4), 16-bit logsumexp
 // above 256 vectors (+7% at 500, +12% at 2048), fp32 mean / max / argmax above
 // 256 vectors (+2 to +4%) and their 16-bit rows above 1024 vectors (+13% at
-// 2048); fp32 logsumexp keeps 4 up to 2048 vectors (within 1% either way).
+// 2048).  fp32 logsumexp takes 8 above 256 vectors as well: within 1% of 4
+// at 256 MB per launch (C3's 16384 x 4096: 6296-6385 GB/s either way) and
+// ahead at 64 MB (3072 columns 4689 -> 5164 GB/s, 8192 4673 -> 5088).
 // Short rows (at most kShortRowVecs vectors) want several lanes per row: one
 // or two lanes per row serialise each row's loads and leave the reductions
 // nothing to share.  There each op takes kItShort vectors per lane, halved
@@ -112,7 +114,7 @@ int it_target(int op, int64_t nvec, int vec) {
   if (op == VBH_OP_LAYER_NORM && vec == 8 && nvec > 1024 && nvec <= 1536) return 2;
   if (vec > 1) {
     if (op == VBH_OP_CROSS_ENTROPY) return 8;
-    if (op == VBH_OP_LOGSUMEXP && vec == 8 && nvec > kMidRowVecs) return 8;
+    if (op == VBH_OP_LOGSUMEXP && nvec > kMidRowVecs) return 8;
     if (op == VBH_OP_REDUCE && nvec > (vec == 8 ? int64_t(1024) : kMidRowVecs)) return 8;
   }
   if ((op == VBH_OP_LOGSUMEXP || op == VBH_OP_REDUCE) && nvec > kLongRowVecs) return 8;
@@ -204,6 +206,7 @@ constexpr int64_t kSplitLongVecs = 12288;   // ... of rows of at least this many
 constexpr int64_t kSplitTarget = 1024;      // segments per launch to aim for
 constexpr int64_t kSplitMinVecs = 512;      // 16-byte vectors per segment, at least
 constexpr int kSplitMaxSegs = 64;
+static_assert(kSplitMaxSegs <= kWave, "the split softmax combines one segment per lane");
 
 // Segments per row (a power of two dividing the row's vectors unless `even` is
 // false), or 1.  `long_from`: the op also splits launches of long_from to 511
@@ -496,8 +499,26 @@ static bool softmax_pair_ok(int idt, int odt) {
   return idt == odt || (odt == kF32 && idt != kF32);
 }
 
-int vbh_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols, int in_dtype,
-                    int out_dtype, int log_mode, void* stream) {
+// The split softmax reads x twice, so it pays only where the unsplit kernel
+// leaves most CUs idle: at most 128 rows (MI355X, log_softmax, split ->
+// unsplit: fp32 1 x 262144 62.7 -> 10.5 us, 8 x 131072 34.0 -> 9.7, 32 x
+// 128256 34.7 -> 14.7, 128 x 131072 48.0 -> 37.5, bf16 64 x 152064 28.5 ->
+// 17.9; but fp32 200 x 65536 22.8 -> 29.7, where 200 workgroups already
+// stream near the full HBM rate).
+constexpr int64_t kSplitMaxRowsSoftmax = 128;
+
+int64_t vbh_softmax_workspace_bytes(int64_t rows, int64_t cols, int in_dtype) {
+  if (!is_float(in_dtype) || rows <= 0 || cols <= 0 || cols > kMaxCols) return 0;
+  if (rows > kSplitMaxRowsSoftmax) return 0;
+  const int vn = 16 / elt_size(in_dtype);
+  if (cols % vn != 0 || g_tpr[VBH_OP_SOFTMAX].load() || g_block[VBH_OP_SOFTMAX].load()) return 0;
+  const int segs = split_segments(rows, cols / vn);
+  return segs > 1 ? rows * segs * static_cast<int64_t>(sizeof(float)) : 0;
+}
+
+int vbh_softmax_fwd_ws(const void* x, void* y, int64_t rows, int64_t cols, int in_dtype,
+                       int out_dtype, int log_mode, void* workspace, int64_t workspace_bytes,
+                       void* stream) {
   if (!softmax_pair_ok(in_dtype, out_dtype))
     return fail(VBH_E_DTYPE, "softmax: unsupported (in, out) dtype pair (%d, %d)", in_dtype,
                 out_dtype);
@@ -506,6 +527,7 @@ int vbh_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols, int in_d
   if (rows < 0 || cols < 0) return fail(VBH_E_INVALID, "softmax: negative size");
   if (cols > kMaxCols) return fail(VBH_E_RANGE, "softmax: cols %lld too large",
                                    static_cast<long long>(cols));
+  if (workspace_bytes < 0) return fail(VBH_E_INVALID, "softmax: negative workspace size");
   if (rows == 0 || cols == 0) return 0;
   if (!x || !y) return fail(VBH_E_INVALID, "softmax: null pointer");
   const int vn = 16 / elt_size(in_dtype);
@@ -513,12 +535,37 @@ int vbh_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols, int in_d
   const bool vec_ok = cols % vn == 0 && aligned;
   const bool mis_ok = !vec_ok && aligned && cols >= kMisMinVecs * vn;
   const int64_t out_bytes = mul_sat(mul_sat(rows, cols), elt_size(out_dtype));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t need = vbh_softmax_workspace_bytes(rows, cols, in_dtype);
+  if (need > 0 && vec_ok && workspace != nullptr && workspace_bytes >= need &&
+      aligned16(workspace)) {
+    // segment logsumexps (fp32) of the [rows * segs, cols / segs] view, then
+    // one pass over x that combines each row's segments and writes y
+    const int segs = split_segments(rows, cols / vn);
+    const int64_t units = rows * segs;
+    const int seg_cols = static_cast<int>(cols / segs);
+    const Geometry g1 = geometry_for(VBH_OP_LOGSUMEXP, seg_cols, vn, units);
+    if (int rc = check_grid(units, g1)) return rc;
+    const Geometry g2 = geometry_for(VBH_OP_SOFTMAX, cols, vn, rows, out_bytes);  // nt / wt
+    float* seg_lse = static_cast<float*>(workspace);
+    hipError_t e = launch_logsumexp(x, seg_lse, units, seg_cols, in_dtype, kF32, g1, s);
+    if (e == hipSuccess)
+      e = launch_softmax_apply(x, y, seg_lse, rows, static_cast<int>(cols), segs, in_dtype,
+                               out_dtype, log_mode, g2, s);
+    return hip_status(e, "softmax launch");
+  }
   Geometry g = geometry_for(VBH_OP_SOFTMAX, cols, vec_ok || mis_ok ? vn : 1, rows, out_bytes);
   if (mis_ok && !use_mis(g, vn)) g = geometry_for(VBH_OP_SOFTMAX, cols, 1, rows, out_bytes);
   if (int rc = check_grid(rows, g)) return rc;
   return hip_status(launch_softmax(x, y, rows, static_cast<int>(cols), in_dtype, out_dtype,
-                                   log_mode, g, static_cast<hipStream_t>(stream)),
+                                   log_mode, g, s),
                     "softmax launch");
+}
+
+int vbh_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols, int in_dtype,
+                    int out_dtype, int log_mode, void* stream) {
+  return vbh_softmax_fwd_ws(x, y, rows, cols, in_dtype, out_dtype, log_mode, nullptr, 0,
+                            stream);
 }
 
 int vbh_softmax_dim_fwd(const void* x, void* y, int64_t outer, int64_t n, int64_t inner,

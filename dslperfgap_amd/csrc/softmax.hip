@@ -205,6 +205,55 @@ __global__ __launch_bounds__(kMaxBlock) void logsumexp_rows(const Ti* __restrict
 }
 
 // ---------------------------------------------------------------------------
+// second stage of a split softmax / log_softmax (rows of whole vectors)
+//
+// The first stage writes the logsumexp of each of a row's `segs` equal
+// segments (logsumexp_rows over the [rows * segs, cols / segs] view).  Here
+// one kApplyLanes-lane workgroup owns one tile of kApplyLanes vectors of a row,
+// one 16-byte vector per lane (the copy kernel's shape).  Every wave combines
+// the row's segment results itself (segs <= 64: one per lane): M = their max,
+// log S = log(sum exp(l_k - M)), and writes (x - M) - log S or its exp.  A row
+// with a NaN segment, a +inf segment (a +inf element) or only -inf segments
+// (only -inf elements) is all NaN, as torch's softmax / log_softmax give.
+// ---------------------------------------------------------------------------
+
+template <typename Ti, typename To, int V, bool LOG, int SP>
+__global__ __launch_bounds__(kApplyLanes) void softmax_apply_tiles(
+    const Ti* __restrict__ x, To* __restrict__ y, const float* __restrict__ seg_lse, int cols,
+    int segs, uint32_t tiles_per_row) {
+  const uint32_t row32 = blockIdx.x / tiles_per_row;
+  const int tix = static_cast<int>(blockIdx.x - row32 * tiles_per_row);
+  const int64_t row = row32;
+  const int nvec = cols / V;
+  const int j0 = tix * kApplyLanes;
+  const int j = j0 + static_cast<int>(threadIdx.x);
+  typename Raw<Ti, V>::type r{};
+  if (j < nvec) r = load_raw<Ti, V, SP != kStoreCached>(x + row * cols + static_cast<int64_t>(j) * V);
+
+  const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+  const bool has = lane < segs;
+  const float l = has ? seg_lse[row * segs + lane] : kNegInf;
+  const float m = wave_allreduce<Max>(l, kWave);
+  const float nan = wave_allreduce<Max>(l != l ? 1.f : 0.f, kWave);
+  const bool bad = nan > 0.f || __builtin_isinf(m);
+  const float sum = wave_allreduce<Sum>(has && !bad ? fast_exp(l - m) : 0.f, kWave);
+  const float ls = fast_log(sum);
+
+  const int tile = nvec - j0 < kApplyLanes ? nvec - j0 : kApplyLanes;
+  To* yr = y + row * cols;
+  const OutWindow<To, SP> out(yr + static_cast<int64_t>(j0) * V, static_cast<int64_t>(tile) * V);
+  if (j < nvec) {
+    float o[V];
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      const float d = (raw_at<Ti, V>(r, k) - m) - ls;
+      o[k] = bad ? __builtin_nanf("") : (LOG ? d : fast_exp(d));
+    }
+    out.template store<V>(yr + static_cast<int64_t>(j) * V, static_cast<int>(threadIdx.x) * V, o);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // streaming (one workgroup per row)
 // ---------------------------------------------------------------------------
 
@@ -425,6 +474,30 @@ hipError_t launch_logsumexp(const void* x, void* y, int64_t rows, int cols, int 
   if (!dispatch_in_out(idt, odt, body) && idt == kF32)
     // second stage of a split logsumexp: fp32 segment results in, the output type out
     dispatch_float_type(odt, [&](auto t) { body(TypeTag<float>{}, t); });
+  return err;
+}
+
+hipError_t launch_softmax_apply(const void* x, void* y, const float* seg_lse, int64_t rows,
+                                int cols, int segs, int idt, int odt, int log_mode,
+                                const Geometry& g, hipStream_t s) {
+  hipError_t err = hipErrorInvalidValue;
+  dispatch_in_out(idt, odt, [&](auto ti, auto to) {
+    using Ti = typename decltype(ti)::type;
+    using To = typename decltype(to)::type;
+    constexpr int V = Vec<Ti>::n;
+    const int64_t tiles = (cols / V + kApplyLanes - 1) / kApplyLanes;
+    dispatch_store_policy<V>(g, [&](auto sp) {
+      constexpr int SP = decltype(sp)::value;
+      auto launch = [&](auto kern) {
+        hipLaunchKernelGGL(kern, dim3(rows * tiles), dim3(kApplyLanes), 0, s,
+                           static_cast<const Ti*>(x), static_cast<To*>(y), seg_lse, cols, segs,
+                           static_cast<uint32_t>(tiles));
+      };
+      if (log_mode) launch(softmax_apply_tiles<Ti, To, V, true, SP>);
+      else launch(softmax_apply_tiles<Ti, To, V, false, SP>);
+    });
+    err = hipGetLastError();
+  });
   return err;
 }
 

@@ -137,6 +137,14 @@ hipError_t launch_softmax(const void* x, void* y, int64_t rows, int cols, int id
 hipError_t launch_softmax_dim(const void* x, void* y, int64_t outer, int n,
                               int64_t inner, int idt, int odt, int log_mode,
                               hipStream_t s);
+// Second stage of a split softmax / log_softmax over rows of whole 16-byte
+// vectors: y from x and each row's `segs` (<= 64) segment logsumexps, one
+// kApplyLanes-lane workgroup per tile of kApplyLanes vectors; g.nt / g.wt
+// select the store policy.
+constexpr int kApplyLanes = 256;
+hipError_t launch_softmax_apply(const void* x, void* y, const float* seg_lse, int64_t rows,
+                                int cols, int segs, int idt, int odt, int log_mode,
+                                const Geometry& g, hipStream_t s);
 // segs > 1 (MIS geometry only): each of rows / segs rows of `cols` columns is
 // split into segs segments of seg_cols columns, the last one shorter.
 hipError_t launch_logsumexp(const void* x, void* y, int64_t rows, int cols, int idt,

@@ -98,6 +98,8 @@ ENTRY(vbh_rms_norm_fwd, "pppqqfiip",
       fn_vbh_rms_norm_fwd(P(0), P(1), P(2), Q(3), Q(4), F(5), I(6), I(7), P(8)))
 ENTRY(vbh_softmax_fwd, "ppqqiiip",
       fn_vbh_softmax_fwd(P(0), P(1), Q(2), Q(3), I(4), I(5), I(6), P(7)))
+ENTRY(vbh_softmax_fwd_ws, "ppqqiiipqp",
+      fn_vbh_softmax_fwd_ws(P(0), P(1), Q(2), Q(3), I(4), I(5), I(6), P(7), Q(8), P(9)))
 ENTRY(vbh_softmax_dim_fwd, "ppqqqiiip",
       fn_vbh_softmax_dim_fwd(P(0), P(1), Q(2), Q(3), Q(4), I(5), I(6), I(7), P(8)))
 ENTRY(vbh_logsumexp_fwd, "ppqqiip",
@@ -131,7 +133,7 @@ static const struct {
   const char* fmt;
 } slots[] = {
     SLOT(vbh_layer_norm_fwd),    SLOT(vbh_rms_norm_fwd),     SLOT(vbh_softmax_fwd),
-    SLOT(vbh_softmax_dim_fwd),   SLOT(vbh_logsumexp_fwd),    SLOT(vbh_logsumexp_fwd_ws),
+    SLOT(vbh_softmax_dim_fwd),   SLOT(vbh_logsumexp_fwd),    SLOT(vbh_logsumexp_fwd_ws), SLOT(vbh_softmax_fwd_ws),
     SLOT(vbh_cross_entropy_fwd), SLOT(vbh_cross_entropy_fwd_ws), SLOT(vbh_cross_entropy_bwd),
     SLOT(vbh_reduce_fwd),
     SLOT(vbh_reduce_fwd_ws),     SLOT(vbh_stream_copy),
@@ -167,7 +169,7 @@ static PyObject* py_bind(PyObject* self, PyObject* addrs) {
 static PyMethodDef methods[] = {
     {"bind", py_bind, METH_O, "bind({entry point name: address}) -- set the entry points"},
     METHOD(vbh_layer_norm_fwd),    METHOD(vbh_rms_norm_fwd),      METHOD(vbh_softmax_fwd),
-    METHOD(vbh_softmax_dim_fwd),   METHOD(vbh_logsumexp_fwd),     METHOD(vbh_logsumexp_fwd_ws),
+    METHOD(vbh_softmax_dim_fwd),   METHOD(vbh_logsumexp_fwd),     METHOD(vbh_logsumexp_fwd_ws), METHOD(vbh_softmax_fwd_ws),
     METHOD(vbh_cross_entropy_fwd), METHOD(vbh_cross_entropy_fwd_ws),
     METHOD(vbh_cross_entropy_bwd), METHOD(vbh_reduce_fwd),
     METHOD(vbh_reduce_fwd_ws),     METHOD(vbh_stream_copy),

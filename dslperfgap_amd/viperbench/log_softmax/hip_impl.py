@@ -6,7 +6,8 @@ Unified API of ViperBench/log_softmax/pytorch_impl.py:4-8:
 ``dtype`` casts the input before the computation, as F.log_softmax does.  A
 widening cast (fp16/bf16 -> fp32) is exact, so the kernel reads the narrow
 input directly and writes fp32; any other cast is applied to x first.
-The last dim uses the row kernel (``vbh_softmax_fwd``, log_mode 1); other dims
+The last dim uses the row kernel (``vbh_softmax_fwd``, log_mode 1; few long
+rows split through ``vbh_softmax_fwd_ws``); other dims
 use the middle-axis kernel (``vbh_softmax_dim_fwd``) on the [outer, n, inner]
 view, as the reference's Triton kernel does with its (M, N, K) strides
 (ViperBench/log_softmax/triton_impl.py:72-90).
@@ -20,7 +21,7 @@ if _ROOT not in sys.path:
 
 import torch  # noqa: E402
 
-from dslperfgap_amd import _bridge  # noqa: E402
+from dslperfgap_amd import _bridge, _lib  # noqa: E402
 
 
 def log_softmax(x, dim=-1, dtype=None):
@@ -46,8 +47,14 @@ def log_softmax(x, dim=-1, dtype=None):
     if d == ndim - 1:
         cols = shape[-1]
         rows = x.numel() // cols if cols else 0
-        _bridge.launch("vbh_softmax_fwd", dev, _bridge.ptr(x), _bridge.ptr(y), rows, cols, idt,
-                       odt, 1)
+        ws_bytes = _lib.softmax_workspace_bytes(rows, cols, idt) if rows else 0
+        if ws_bytes:  # few long rows: split each row over several workgroups
+            ws = _bridge.empty(x, (ws_bytes,), torch.uint8)
+            _bridge.launch("vbh_softmax_fwd_ws", dev, x.data_ptr(), y.data_ptr(), rows, cols,
+                           idt, odt, 1, ws.data_ptr(), ws_bytes)
+        else:
+            _bridge.launch("vbh_softmax_fwd", dev, _bridge.ptr(x), _bridge.ptr(y), rows, cols,
+                           idt, odt, 1)
     else:
         outer = _bridge.numel_prod(shape[:d])
         inner = _bridge.numel_prod(shape[d + 1:])

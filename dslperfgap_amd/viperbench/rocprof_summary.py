@@ -58,7 +58,7 @@ CONFIG_KERNELS = [
     ("C2_rms_norm", r"rms_norm_rowsIDF16bDF16bLi8ELi2ELi\dE"),
     ("C3_log_softmax", r"softmax_rows<float, float, 4, 2, true, \d(, false)?>"),
     ("C3_softmax", r"softmax_rows<float, float, 4, 2, false, \d(, false)?>"),
-    ("C3_logsumexp", r"logsumexp_rows<float, float, 4, 4, true(, false)?>"),
+    ("C3_logsumexp", r"logsumexp_rows<float, float, 4, 8, true(, false)?>"),
     ("C4_cross_entropy", r"ce_fwd_rows<float, 4, 8, true(, false)?>"),
     ("C4_cross_entropy_bwd", r"ce_bwd_tiles<float, 4, \d(, false)?>|ce_bwd_tilesIfLi4ELi\dE"),
     ("C5_layer_norm", r"layer_norm_pipeIDF16bDF16bLi8ELi4ELi\dELb1E"),

@@ -4,6 +4,8 @@ Unified API of ViperBench/softmax/pytorch_impl.py:4-6:
 ``softmax(x) -> Tensor`` = F.softmax(x, dim=-1), any rank, same dtype.
 
 One read and one write per call (libvbhip ``vbh_softmax_fwd``, log_mode 0).
+Few long rows go through ``vbh_softmax_fwd_ws`` with a small workspace: each
+row's segment logsumexps first, then a pass that reads x again and writes y.
 """
 import os
 import sys
@@ -14,7 +16,7 @@ if _ROOT not in sys.path:
 
 import torch  # noqa: E402
 
-from dslperfgap_amd import _bridge  # noqa: E402
+from dslperfgap_amd import _bridge, _lib  # noqa: E402
 
 
 def softmax(x):
@@ -25,5 +27,12 @@ def softmax(x):
     y = torch.empty_like(x)
     cols = x.shape[-1] if x.dim() > 0 else 1
     rows = x.numel() // cols if cols else 0
-    _bridge.launch("vbh_softmax_fwd", dev, _bridge.ptr(x), _bridge.ptr(y), rows, cols, dt, dt, 0)
+    ws_bytes = _lib.softmax_workspace_bytes(rows, cols, dt) if rows else 0
+    if ws_bytes:  # few long rows: split each row over several workgroups
+        ws = _bridge.empty(x, (ws_bytes,), torch.uint8)
+        _bridge.launch("vbh_softmax_fwd_ws", dev, x.data_ptr(), y.data_ptr(), rows, cols, dt, dt,
+                       0, ws.data_ptr(), ws_bytes)
+    else:
+        _bridge.launch("vbh_softmax_fwd", dev, _bridge.ptr(x), _bridge.ptr(y), rows, cols, dt,
+                       dt, 0)
     return y

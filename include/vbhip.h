@@ -84,6 +84,23 @@ int vbh_rms_norm_fwd(const void* x, const void* w, void* y,
 int vbh_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols,
                     int in_dtype, int out_dtype, int log_mode, void* stream);
 
+/* vbh_softmax_fwd with a caller-provided workspace (16-byte aligned).  Few
+ * long rows of whole 16-byte vectors split: a first launch writes the
+ * logsumexp of each row segment into the workspace (the two-stage shape of
+ * ViperBench/logsumexp/triton_impl.py:48-71), a second reads x again and
+ * writes y from each row's segments.  The workspace must hold
+ * vbh_softmax_workspace_bytes(rows, cols, in_dtype) bytes; when that is 0, or
+ * the workspace is null or smaller, this is vbh_softmax_fwd.  The workspace is
+ * scratch of this call (stream-ordered, as for vbh_logsumexp_fwd_ws). */
+int vbh_softmax_fwd_ws(const void* x, void* y, int64_t rows, int64_t cols,
+                       int in_dtype, int out_dtype, int log_mode, void* workspace,
+                       int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes vbh_softmax_fwd_ws splits such a launch with (0: it does
+ * not split).  A pure function of its arguments and of vbh_tune_override's
+ * state (an overridden softmax geometry disables the split). */
+int64_t vbh_softmax_workspace_bytes(int64_t rows, int64_t cols, int in_dtype);
+
 /* Softmax / log-softmax over the middle axis of a contiguous [outer, n, inner]
  * tensor (the `dim` argument of log_softmax when dim is not the last axis).
  * Replaces: the (M, N, K) stride handling of

@@ -748,6 +748,58 @@ def test_split_logsumexp_matches_the_unsplit_kernel(cols):
 
 
 # ---------------------------------------------------------------------------
+# softmax / log_softmax of few long rows: the split path
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("rows,cols", [(1, 262144), (3, 131072), (33, 131072), (128, 131072)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_split_softmax_family(rows, cols, dtype):
+    """Launches that split every row (segment logsumexps, then a pass that
+    writes y) match the oracle for softmax, log_softmax and, for 16-bit
+    inputs, log_softmax with an fp32 output; special rows: all -inf, one +inf
+    and one NaN element (all NaN, as torch), and a large value in one late
+    segment only."""
+    code = {torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}[dtype]
+    assert _lib.softmax_workspace_bytes(rows, cols, code) > 0
+    x = (3 * torch.randn(rows, cols, generator=_g(450 + rows))).to(dtype)
+    x[0, cols - 2] = 30.0
+    if rows > 1:
+        x[1, :] = float("-inf")
+    if rows > 2:
+        x[2, cols // 2] = float("inf")
+    if rows > 3:
+        x[3, 5] = float("nan")
+    xd = x.to(DEV)
+    what = f"split {rows}x{cols} {dtype}"
+    check(softmax(xd), ref.softmax(x), dtype, what="softmax " + what)
+    check(log_softmax(xd), ref.log_softmax(x), dtype, what="log_softmax " + what)
+    if dtype != torch.float32:
+        check(log_softmax(xd, -1, torch.float32), ref.log_softmax(x, -1, torch.float32),
+              torch.float32, what="log_softmax fp32 out " + what)
+
+
+@pytest.mark.parametrize("log_mode", [0, 1])
+def test_split_softmax_matches_the_unsplit_kernel(log_mode):
+    """One launch through vbh_softmax_fwd_ws with and without a workspace: the
+    split and unsplit results agree to fp32 rounding."""
+    rows, cols = 7, 131072
+    x = (3 * torch.randn(rows, cols, generator=_g(460))).to(DEV)
+    need = _lib.softmax_workspace_bytes(rows, cols, _lib.F32)
+    assert need > 0
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    outs = []
+    for w, nb in ((ws, need), (None, 0)):
+        y = torch.empty_like(x)
+        _lib.call("vbh_softmax_fwd_ws", x.data_ptr(), y.data_ptr(), rows, cols, _lib.F32,
+                  _lib.F32, log_mode, w.data_ptr() if w is not None else None, nb,
+                  torch.cuda.current_stream().cuda_stream)
+        outs.append(y.cpu())
+    if log_mode:
+        assert torch.allclose(outs[0], outs[1], atol=2e-5, rtol=1e-6), (outs[0] - outs[1]).abs().max()
+    else:
+        assert torch.allclose(outs[0], outs[1], atol=1e-12, rtol=2e-5), (outs[0] - outs[1]).abs().max()
+
+
+# ---------------------------------------------------------------------------
 # cross-entropy forward of few long rows (one column block): the split path
 # ---------------------------------------------------------------------------
 CE_SPLIT_PARAMS = [

@@ -255,6 +255,12 @@ def test_split_workspace_sizes():
     assert red(128, 131072, 1, _lib.F16, _lib.REDUCE_ARGMAX) == 128 * 8 * (8 + 2)
     assert red(300, 131072, 1, _lib.F32, _lib.REDUCE_MEAN) == 0  # long rows: logsumexp only
     assert red(128, 131072, 4, _lib.F32, _lib.REDUCE_MEAN) == 0  # middle axis: not split
+    sm = h.vbh_softmax_workspace_bytes
+    assert sm(128, 131072, _lib.F32) == 128 * 8 * 4       # as logsumexp's few-rows split
+    assert sm(8192, 4096, _lib.F32) == 0 and sm(300, 131072, _lib.F32) == 0
+    assert sm(200, 65536, _lib.F32) == 0                  # 129 rows or more: not split
+    assert sm(4, 65537, _lib.F32) == 0                    # rows not whole 16-byte vectors
+    assert sm(1, 131072, _lib.BF16) == 1 * 32 * 4
     ce = h.vbh_cross_entropy_workspace_bytes
     assert ce(64, 128256, 1 << 17, _lib.F32) == 3 * 64 * 16 * 4  # one block per row
     assert ce(64, 128256, 32768, _lib.F32) == 0           # several column blocks: not split
@@ -264,8 +270,12 @@ def test_split_workspace_sizes():
     try:
         _lib.tune_override(_lib.OP_LOGSUMEXP, 64, 0, 0)
         assert _lib.logsumexp_workspace_bytes(128, 131072, _lib.F32) == 0
+        _lib.tune_override(_lib.OP_SOFTMAX, 64, 0, 0)
+        assert _lib.softmax_workspace_bytes(128, 131072, _lib.F32) == 0
     finally:
         _lib.tune_override(_lib.OP_LOGSUMEXP, 0, 0, 0)
+        _lib.tune_override(_lib.OP_SOFTMAX, 0, 0, 0)
+    assert _lib.softmax_workspace_bytes(128, 131072, _lib.F32) == 128 * 8 * 4
     assert _lib.logsumexp_workspace_bytes(128, 131072, _lib.F32) == 128 * 8 * 4
 
 

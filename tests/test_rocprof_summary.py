@@ -77,8 +77,8 @@ CONFIG_SYMBOLS = {
                       "2, false>(float const*, float*, long, int, int)",
     "C3_softmax": "void vbh::(anonymous namespace)::softmax_rows<float, float, 4, 2, false, 2, "
                   "false>(float const*, float*, long, int, int)",
-    "C3_logsumexp": "void vbh::(anonymous namespace)::logsumexp_rows<float, float, 4, 4, true, "
-                    "false>(float const*, float*, long, int, int)",
+    "C3_logsumexp": "void vbh::(anonymous namespace)::logsumexp_rows<float, float, 4, 8, true, "
+                    "false>(float const*, float*, long, int, int, int, int)",
     "C4_cross_entropy": "void vbh::(anonymous namespace)::ce_fwd_rows<float, 4, 8, true, false>"
                         "(float const*, void const*, int, float*, float*, float*)",
     "C4_cross_entropy_bwd": "void vbh::(anonymous namespace)::ce_bwd_tiles<float, 4, 2, false>"
