@@ -211,8 +211,9 @@ static_assert(kSplitMaxSegs <= kWave, "the split softmax combines one segment pe
 // Segments per row (a power of two dividing the row's vectors unless `even` is
 // false), or 1.  `long_from`: the op also splits launches of long_from to 511
 // rows of long rows (0: it does not).
-int split_segments(int64_t rows, int64_t nvec, int64_t long_from = 0, bool even = true) {
-  const bool few = rows > 0 && rows < kSplitMaxRows && nvec >= kSplitRowVecs;
+int split_segments(int64_t rows, int64_t nvec, int64_t long_from = 0, bool even = true,
+                   int64_t min_vecs = kSplitRowVecs) {
+  const bool few = rows > 0 && rows < kSplitMaxRows && nvec >= min_vecs;
   const bool two_rounds = long_from > 0 && rows >= long_from && rows < kSplitMaxRowsLong &&
                           nvec >= kSplitLongVecs;
   if (!few && !two_rounds) return 1;
@@ -499,20 +500,30 @@ static bool softmax_pair_ok(int idt, int odt) {
   return idt == odt || (odt == kF32 && idt != kF32);
 }
 
-// The split softmax reads x twice, so it pays only where the unsplit kernel
-// leaves most CUs idle: at most 128 rows (MI355X, log_softmax, split ->
-// unsplit: fp32 1 x 262144 62.7 -> 10.5 us, 8 x 131072 34.0 -> 9.7, 32 x
-// 128256 34.7 -> 14.7, 128 x 131072 48.0 -> 37.5, bf16 64 x 152064 28.5 ->
-// 17.9; but fp32 200 x 65536 22.8 -> 29.7, where 200 workgroups already
-// stream near the full HBM rate).
-constexpr int64_t kSplitMaxRowsSoftmax = 128;
+// The split softmax reads x twice and adds a launch (about 6.5 us for both
+// launches of a small split), so it pays only where the unsplit kernel, one
+// workgroup per row, is bound by the time one workgroup takes to stream its
+// row: few rows, long enough.  MI355X, softmax, unsplit / split time:
+//   fp32 8192 columns (2048 vectors) 0.60-0.73 at every row count, 16384
+//   columns 0.74-0.91, 32000 1.09-1.18 up to 32 rows and 0.69-0.91 at 64-128,
+//   50304 1.38-1.72 up to 32 rows, 1.00 at 64, 0.79 at 128; 65536 1.46-1.75
+//   up to 32, 0.99 at 64, 0.91 at 128; 131072 at 128 rows 1.28, 8 rows 3.5;
+//   bf16 32000 columns (4000 vectors) 0.93-1.05, 50304 1.36-1.51 up to 32
+//   rows, 1.12 at 64, 0.81 at 128; 65536 1.39-1.62 up to 32, 1.19 at 64,
+//   0.77 at 128; fp32 200 x 65536 0.77.
+bool softmax_split_pays(int64_t rows, int64_t nvec, bool half) {
+  if (rows <= 32) return nvec >= 6144;
+  if (rows <= 64) return nvec >= (half ? 6144 : 32768);
+  if (rows <= 128) return nvec >= 32768;
+  return false;
+}
 
 int64_t vbh_softmax_workspace_bytes(int64_t rows, int64_t cols, int in_dtype) {
   if (!is_float(in_dtype) || rows <= 0 || cols <= 0 || cols > kMaxCols) return 0;
-  if (rows > kSplitMaxRowsSoftmax) return 0;
   const int vn = 16 / elt_size(in_dtype);
   if (cols % vn != 0 || g_tpr[VBH_OP_SOFTMAX].load() || g_block[VBH_OP_SOFTMAX].load()) return 0;
-  const int segs = split_segments(rows, cols / vn);
+  if (!softmax_split_pays(rows, cols / vn, vn == 8)) return 0;
+  const int segs = split_segments(rows, cols / vn, 0, true, 0);
   return segs > 1 ? rows * segs * static_cast<int64_t>(sizeof(float)) : 0;
 }
 
@@ -541,7 +552,7 @@ int vbh_softmax_fwd_ws(const void* x, void* y, int64_t rows, int64_t cols, int i
       aligned16(workspace)) {
     // segment logsumexps (fp32) of the [rows * segs, cols / segs] view, then
     // one pass over x that combines each row's segments and writes y
-    const int segs = split_segments(rows, cols / vn);
+    const int segs = split_segments(rows, cols / vn, 0, true, 0);
     const int64_t units = rows * segs;
     const int seg_cols = static_cast<int>(cols / segs);
     const Geometry g1 = geometry_for(VBH_OP_LOGSUMEXP, seg_cols, vn, units);

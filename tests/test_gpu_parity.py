@@ -750,7 +750,8 @@ def test_split_logsumexp_matches_the_unsplit_kernel(cols):
 # ---------------------------------------------------------------------------
 # softmax / log_softmax of few long rows: the split path
 # ---------------------------------------------------------------------------
-@pytest.mark.parametrize("rows,cols", [(1, 262144), (3, 131072), (33, 131072), (128, 131072)])
+@pytest.mark.parametrize("rows,cols", [(1, 262144), (3, 131072), (8, 50304), (33, 131072),
+                                       (100, 262144)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_split_softmax_family(rows, cols, dtype):
     """Launches that split every row (segment logsumexps, then a pass that

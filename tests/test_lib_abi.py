@@ -259,6 +259,10 @@ def test_split_workspace_sizes():
     assert sm(128, 131072, _lib.F32) == 128 * 8 * 4       # as logsumexp's few-rows split
     assert sm(8192, 4096, _lib.F32) == 0 and sm(300, 131072, _lib.F32) == 0
     assert sm(200, 65536, _lib.F32) == 0                  # 129 rows or more: not split
+    assert sm(64, 65536, _lib.F32) == 0                   # fp32 33-64 rows: 32768 vectors
+    assert sm(64, 65536, _lib.BF16) == 64 * 16 * 4        # 16-bit 33-64 rows: 6144 vectors
+    assert sm(8, 32000, _lib.F32) == 8 * 8 * 4            # a decode step over a 32000 vocabulary
+    assert sm(8, 16384, _lib.F32) == 0                    # 4096 vectors: not worth a split
     assert sm(4, 65537, _lib.F32) == 0                    # rows not whole 16-byte vectors
     assert sm(1, 131072, _lib.BF16) == 1 * 32 * 4
     ce = h.vbh_cross_entropy_workspace_bytes
