@@ -126,3 +126,30 @@ def test_committed_cliff_table_is_consistent():
         work = int(r["note"].split("essential bytes ")[1].split(";")[0])
         assert float(r["roofline_frac_opt"]) == pytest.approx(work / (t_opt * 1e-3) / 8e12,
                                                               abs=2e-4)
+
+
+def test_committed_width_scan_is_complete():
+    """The row-width scan holds every kernel of width_scan.KERNELS at every
+    width of width_scan.WIDTHS once, at about 64 MiB of input per call, with
+    hip_over_torch the ratio of its own two rates."""
+    import torch
+
+    from dslperfgap_amd.viperbench import width_scan
+
+    path = RESULTS / "AMD_gfx950" / "width_scan.csv"
+    with open(path, newline="") as f:
+        reader = csv.DictReader(f)
+        assert reader.fieldnames == ["kernel", "dtype", "rows", "cols", "hip_GBps", "torch_GBps",
+                                     "hip_over_torch"]
+        rows = list(reader)
+    want = {(k, w) for k, *_ in width_scan.KERNELS for w in width_scan.WIDTHS}
+    got = [(r["kernel"], int(r["cols"])) for r in rows]
+    assert len(got) == len(set(got)) and set(got) == want
+    dtypes = {k: str(dt).replace("torch.", "") for k, _, dt, _ in width_scan.KERNELS}
+    for r in rows:
+        assert r["dtype"] == dtypes[r["kernel"]]
+        elt = torch.empty(0, dtype=getattr(torch, r["dtype"])).element_size()
+        assert int(r["rows"]) == max(1, (64 << 20) // (int(r["cols"]) * elt))
+        hip, ref = float(r["hip_GBps"]), float(r["torch_GBps"])
+        assert 0 < hip < 8000 and 0 < ref < 8000
+        assert float(r["hip_over_torch"]) == pytest.approx(hip / ref, rel=2e-3)
