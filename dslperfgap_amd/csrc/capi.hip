@@ -518,13 +518,25 @@ bool softmax_split_pays(int64_t rows, int64_t nvec, bool half) {
   return false;
 }
 
+// Segments of a split softmax: equal ones for rows of whole vectors, else
+// segments of a whole number of vectors with the last one shorter (the MIS
+// kernels run them); segs == 1: no split.
+RowSplit softmax_split(int64_t rows, int64_t cols, int vn) {
+  const int64_t nvec = cols / vn;
+  if (!softmax_split_pays(rows, nvec, vn == 8)) return RowSplit{1, cols};
+  const bool even = cols % vn == 0;
+  const int segs = split_segments(rows, nvec, 0, even, 0);
+  if (segs == 1 || even) return RowSplit{segs, cols / segs};
+  const int64_t seg_cols = ((cols + segs - 1) / segs + vn - 1) / vn * vn;
+  return RowSplit{static_cast<int>((cols + seg_cols - 1) / seg_cols), seg_cols};
+}
+
 int64_t vbh_softmax_workspace_bytes(int64_t rows, int64_t cols, int in_dtype) {
   if (!is_float(in_dtype) || rows <= 0 || cols <= 0 || cols > kMaxCols) return 0;
   const int vn = 16 / elt_size(in_dtype);
-  if (cols % vn != 0 || g_tpr[VBH_OP_SOFTMAX].load() || g_block[VBH_OP_SOFTMAX].load()) return 0;
-  if (!softmax_split_pays(rows, cols / vn, vn == 8)) return 0;
-  const int segs = split_segments(rows, cols / vn, 0, true, 0);
-  return segs > 1 ? rows * segs * static_cast<int64_t>(sizeof(float)) : 0;
+  if (g_tpr[VBH_OP_SOFTMAX].load() || g_block[VBH_OP_SOFTMAX].load()) return 0;
+  const RowSplit sp = softmax_split(rows, cols, vn);
+  return sp.segs > 1 ? rows * sp.segs * static_cast<int64_t>(sizeof(float)) : 0;
 }
 
 int vbh_softmax_fwd_ws(const void* x, void* y, int64_t rows, int64_t cols, int in_dtype,
@@ -548,22 +560,30 @@ int vbh_softmax_fwd_ws(const void* x, void* y, int64_t rows, int64_t cols, int i
   const int64_t out_bytes = mul_sat(mul_sat(rows, cols), elt_size(out_dtype));
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t need = vbh_softmax_workspace_bytes(rows, cols, in_dtype);
-  if (need > 0 && vec_ok && workspace != nullptr && workspace_bytes >= need &&
+  if (need > 0 && (vec_ok || mis_ok) && workspace != nullptr && workspace_bytes >= need &&
       aligned16(workspace)) {
-    // segment logsumexps (fp32) of the [rows * segs, cols / segs] view, then
-    // one pass over x that combines each row's segments and writes y
-    const int segs = split_segments(rows, cols / vn, 0, true, 0);
+    // segment logsumexps (fp32): the [rows * segs, cols / segs] view, or the
+    // MIS kernel's segment mode; then one pass over x that combines each row's
+    // segments and writes y
+    const RowSplit sp = softmax_split(rows, cols, vn);
+    const int segs = sp.segs;
     const int64_t units = rows * segs;
-    const int seg_cols = static_cast<int>(cols / segs);
-    const Geometry g1 = geometry_for(VBH_OP_LOGSUMEXP, seg_cols, vn, units);
-    if (int rc = check_grid(units, g1)) return rc;
-    const Geometry g2 = geometry_for(VBH_OP_SOFTMAX, cols, vn, rows, out_bytes);  // nt / wt
-    float* seg_lse = static_cast<float*>(workspace);
-    hipError_t e = launch_logsumexp(x, seg_lse, units, seg_cols, in_dtype, kF32, g1, s);
-    if (e == hipSuccess)
-      e = launch_softmax_apply(x, y, seg_lse, rows, static_cast<int>(cols), segs, in_dtype,
-                               out_dtype, log_mode, g2, s);
-    return hip_status(e, "softmax launch");
+    const int seg_cols = static_cast<int>(sp.seg_cols);
+    Geometry g1 = geometry_for(VBH_OP_LOGSUMEXP, seg_cols, vn, units);
+    Geometry g2 = geometry_for(VBH_OP_SOFTMAX, cols, vn, rows, out_bytes);  // nt / wt
+    g2.mis = !vec_ok;
+    if (vec_ok || use_mis(g1, vn)) {
+      if (int rc = check_grid(units, g1)) return rc;
+      float* seg_lse = static_cast<float*>(workspace);
+      hipError_t e =
+          vec_ok ? launch_logsumexp(x, seg_lse, units, seg_cols, in_dtype, kF32, g1, s)
+                 : launch_logsumexp(x, seg_lse, units, static_cast<int>(cols), in_dtype, kF32,
+                                    g1, s, segs, seg_cols);
+      if (e == hipSuccess)
+        e = launch_softmax_apply(x, y, seg_lse, rows, static_cast<int>(cols), segs, in_dtype,
+                                 out_dtype, log_mode, g2, s);
+      return hip_status(e, "softmax launch");
+    }
   }
   Geometry g = geometry_for(VBH_OP_SOFTMAX, cols, vec_ok || mis_ok ? vn : 1, rows, out_bytes);
   if (mis_ok && !use_mis(g, vn)) g = geometry_for(VBH_OP_SOFTMAX, cols, 1, rows, out_bytes);

@@ -215,20 +215,26 @@ __global__ __launch_bounds__(kMaxBlock) void logsumexp_rows(const Ti* __restrict
 // log S = log(sum exp(l_k - M)), and writes (x - M) - log S or its exp.  A row
 // with a NaN segment, a +inf segment (a +inf element) or only -inf segments
 // (only -inf elements) is all NaN, as torch's softmax / log_softmax give.
+// MIS rows (not whole vectors; the first stage ran the MIS segment mode): the
+// tiles cover each row's aligned body, and tile 0 also writes the row's scalar
+// head and tail (lanes t < head, t < tail).
 // ---------------------------------------------------------------------------
 
-template <typename Ti, typename To, int V, bool LOG, int SP>
+template <typename Ti, typename To, int V, bool LOG, int SP, bool MIS>
 __global__ __launch_bounds__(kApplyLanes) void softmax_apply_tiles(
     const Ti* __restrict__ x, To* __restrict__ y, const float* __restrict__ seg_lse, int cols,
     int segs, uint32_t tiles_per_row) {
   const uint32_t row32 = blockIdx.x / tiles_per_row;
   const int tix = static_cast<int>(blockIdx.x - row32 * tiles_per_row);
   const int64_t row = row32;
-  const int nvec = cols / V;
+  const int64_t start = row * cols;
+  const MisRow mr = MIS ? mis_row<V>(start, cols) : MisRow{0, cols / V, 0};
+  const int nvec = mr.nvec;
+  const Ti* xb = x + start + mr.head;  // 16-byte aligned body
   const int j0 = tix * kApplyLanes;
   const int j = j0 + static_cast<int>(threadIdx.x);
   typename Raw<Ti, V>::type r{};
-  if (j < nvec) r = load_raw<Ti, V, SP != kStoreCached>(x + row * cols + static_cast<int64_t>(j) * V);
+  if (j < nvec) r = load_raw<Ti, V, SP != kStoreCached>(xb + static_cast<int64_t>(j) * V);
 
   const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
   const bool has = lane < segs;
@@ -239,17 +245,31 @@ __global__ __launch_bounds__(kApplyLanes) void softmax_apply_tiles(
   const float sum = wave_allreduce<Sum>(has && !bad ? fast_exp(l - m) : 0.f, kWave);
   const float ls = fast_log(sum);
 
-  const int tile = nvec - j0 < kApplyLanes ? nvec - j0 : kApplyLanes;
-  To* yr = y + row * cols;
-  const OutWindow<To, SP> out(yr + static_cast<int64_t>(j0) * V, static_cast<int64_t>(tile) * V);
+  auto value = [&](float v) {
+    const float d = (v - m) - ls;
+    return bad ? __builtin_nanf("") : (LOG ? d : fast_exp(d));
+  };
+  const int tile = nvec - j0 < kApplyLanes ? nvec - j0 : kApplyLanes;  // <= 0: no body here
+  To* yb = y + start + mr.head;
+  const OutWindow<To, SP> out(yb + static_cast<int64_t>(j0) * V,
+                              static_cast<int64_t>(tile > 0 ? tile : 0) * V);
   if (j < nvec) {
     float o[V];
 #pragma unroll
-    for (int k = 0; k < V; ++k) {
-      const float d = (raw_at<Ti, V>(r, k) - m) - ls;
-      o[k] = bad ? __builtin_nanf("") : (LOG ? d : fast_exp(d));
+    for (int k = 0; k < V; ++k) o[k] = value(raw_at<Ti, V>(r, k));
+    out.template store<V>(yb + static_cast<int64_t>(j) * V, static_cast<int>(threadIdx.x) * V, o);
+  }
+  if (MIS && tix == 0) {
+    const int t = static_cast<int>(threadIdx.x);
+    if (t < mr.head) {
+      const float o = value(static_cast<float>(x[start + t]));
+      store_from_f32<To, 1>(y + start + t, &o);
     }
-    out.template store<V>(yr + static_cast<int64_t>(j) * V, static_cast<int>(threadIdx.x) * V, o);
+    if (t < mr.tail) {
+      const int64_t k = static_cast<int64_t>(nvec) * V + t;
+      const float o = value(static_cast<float>(xb[k]));
+      store_from_f32<To, 1>(yb + k, &o);
+    }
   }
 }
 
@@ -480,6 +500,7 @@ hipError_t launch_logsumexp(const void* x, void* y, int64_t rows, int cols, int 
 hipError_t launch_softmax_apply(const void* x, void* y, const float* seg_lse, int64_t rows,
                                 int cols, int segs, int idt, int odt, int log_mode,
                                 const Geometry& g, hipStream_t s) {
+  // MIS rows: the tiles cover at most cols / V body vectors per row
   hipError_t err = hipErrorInvalidValue;
   dispatch_in_out(idt, odt, [&](auto ti, auto to) {
     using Ti = typename decltype(ti)::type;
@@ -493,8 +514,13 @@ hipError_t launch_softmax_apply(const void* x, void* y, const float* seg_lse, in
                            static_cast<const Ti*>(x), static_cast<To*>(y), seg_lse, cols, segs,
                            static_cast<uint32_t>(tiles));
       };
-      if (log_mode) launch(softmax_apply_tiles<Ti, To, V, true, SP>);
-      else launch(softmax_apply_tiles<Ti, To, V, false, SP>);
+      if (g.mis) {
+        if (log_mode) launch(softmax_apply_tiles<Ti, To, V, true, SP, true>);
+        else launch(softmax_apply_tiles<Ti, To, V, false, SP, true>);
+      } else {
+        if (log_mode) launch(softmax_apply_tiles<Ti, To, V, true, SP, false>);
+        else launch(softmax_apply_tiles<Ti, To, V, false, SP, false>);
+      }
     });
     err = hipGetLastError();
   });

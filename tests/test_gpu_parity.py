@@ -751,14 +751,15 @@ def test_split_logsumexp_matches_the_unsplit_kernel(cols):
 # softmax / log_softmax of few long rows: the split path
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("rows,cols", [(1, 262144), (3, 131072), (8, 50304), (33, 131072),
-                                       (100, 262144)])
+                                       (100, 262144), (8, 50257), (3, 131075)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_split_softmax_family(rows, cols, dtype):
     """Launches that split every row (segment logsumexps, then a pass that
     writes y) match the oracle for softmax, log_softmax and, for 16-bit
     inputs, log_softmax with an fp32 output; special rows: all -inf, one +inf
     and one NaN element (all NaN, as torch), and a large value in one late
-    segment only."""
+    segment only.  Rows that are not whole 16-byte vectors (50257, 131075
+    columns) split into segments with their own head and tail."""
     code = {torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}[dtype]
     assert _lib.softmax_workspace_bytes(rows, cols, code) > 0
     x = (3 * torch.randn(rows, cols, generator=_g(450 + rows))).to(dtype)
@@ -778,11 +779,12 @@ def test_split_softmax_family(rows, cols, dtype):
               torch.float32, what="log_softmax fp32 out " + what)
 
 
+@pytest.mark.parametrize("cols", [131072, 50257])
 @pytest.mark.parametrize("log_mode", [0, 1])
-def test_split_softmax_matches_the_unsplit_kernel(log_mode):
+def test_split_softmax_matches_the_unsplit_kernel(log_mode, cols):
     """One launch through vbh_softmax_fwd_ws with and without a workspace: the
     split and unsplit results agree to fp32 rounding."""
-    rows, cols = 7, 131072
+    rows = 7
     x = (3 * torch.randn(rows, cols, generator=_g(460))).to(DEV)
     need = _lib.softmax_workspace_bytes(rows, cols, _lib.F32)
     assert need > 0

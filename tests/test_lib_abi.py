@@ -263,7 +263,8 @@ def test_split_workspace_sizes():
     assert sm(64, 65536, _lib.BF16) == 64 * 16 * 4        # 16-bit 33-64 rows: 6144 vectors
     assert sm(8, 32000, _lib.F32) == 8 * 8 * 4            # a decode step over a 32000 vocabulary
     assert sm(8, 16384, _lib.F32) == 0                    # 4096 vectors: not worth a split
-    assert sm(4, 65537, _lib.F32) == 0                    # rows not whole 16-byte vectors
+    assert sm(4, 65537, _lib.F32) == 4 * 32 * 4           # rows not whole vectors: 2052-column segments
+    assert sm(8, 50257, _lib.F32) == 8 * 16 * 4           # GPT-2's vocabulary, 16 x 3144 columns
     assert sm(1, 131072, _lib.BF16) == 1 * 32 * 4
     ce = h.vbh_cross_entropy_workspace_bytes
     assert ce(64, 128256, 1 << 17, _lib.F32) == 3 * 64 * 16 * 4  # one block per row
