@@ -85,7 +85,8 @@ int vbh_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols,
                     int in_dtype, int out_dtype, int log_mode, void* stream);
 
 /* vbh_softmax_fwd with a caller-provided workspace (16-byte aligned).  Few
- * long rows of whole 16-byte vectors split: a first launch writes the
+ * long rows split into segments (of whole 16-byte vectors, the last one
+ * shorter where rows are not whole vectors): a first launch writes the
  * logsumexp of each row segment into the workspace (the two-stage shape of
  * ViperBench/logsumexp/triton_impl.py:48-71), a second reads x again and
  * writes y from each row's segments.  The workspace must hold
