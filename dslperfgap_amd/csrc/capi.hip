@@ -335,7 +335,7 @@ Geometry reduce_geometry(int64_t n, int vec, int64_t units) {
 
 }  // namespace
 
-int64_t resident_blocks(const void* kernel, int block) {
+int64_t resident_blocks(const void* kernel, int block, int max_per_cu) {
   static std::mutex mu;
   static std::unordered_map<uint64_t, int> per_cu;  // (kernel, block) -> blocks per CU
   static int cus[64] = {0};
@@ -361,7 +361,7 @@ int64_t resident_blocks(const void* kernel, int block) {
       nb = 1;
     per_cu.emplace(key, nb);
   }
-  return static_cast<int64_t>(nb) * cus[dev];
+  return static_cast<int64_t>(std::min(nb, max_per_cu)) * cus[dev];
 }
 
 Geometry pick_geometry(int64_t cols, int vec, int it_target, int tpr_override,

@@ -627,13 +627,25 @@ bool pipe_full(const Geometry& g, int64_t nvec, int it) {
          nvec == static_cast<int64_t>(it) * g.tpr;
 }
 
+// Input bytes a CU's resident persistent workgroups may hold in flight (each
+// row group loads its next row while it reduces the current one).  Uncapped,
+// small fp32 kernels put 3 workgroups on a CU; capped (MI355X, 64 MB per
+// call): fp32 RMSNorm 5120 columns +17.6%, LayerNorm 4608 / 5120 +13%, bf16
+// RMSNorm 10240 +10%, bf16 LayerNorm 8192 columns +0.8%, C1 / C5 and the other
+// shapes within 0.4%.  A 64 KiB cap starved fp32 LayerNorm (-12%).
+constexpr int64_t kPipeBytesPerCu = int64_t(96) << 10;
+
 // Launch the register-resident kernel (one row group per row) or the
-// persistent one (grid capped at the resident capacity) through `launch`.
+// persistent one (grid capped at the resident capacity, and at
+// kPipeBytesPerCu of rows in flight per CU) through `launch`.
 template <class RowsK, class PipeK, class Launch>
 hipError_t launch_rows_or_pipe(RowsK rows_k, PipeK pipe_k, bool persist, int64_t rows,
-                               const Geometry& g, Launch&& launch) {
+                               const Geometry& g, Launch&& launch, int64_t row_bytes) {
   if (persist) {
-    const int64_t cap = resident_blocks(reinterpret_cast<const void*>(pipe_k), g.block);
+    const int64_t per_block = 2 * (g.block / g.tpr) * row_bytes;  // current + next rows
+    const int max_per_cu =
+        static_cast<int>(std::max<int64_t>(1, kPipeBytesPerCu / std::max<int64_t>(per_block, 1)));
+    const int64_t cap = resident_blocks(reinterpret_cast<const void*>(pipe_k), g.block, max_per_cu);
     launch(pipe_k, std::min<int64_t>(grid_for(rows, g), std::max<int64_t>(cap, 1)));
   } else {
     launch(rows_k, grid_for(rows, g));
@@ -689,7 +701,7 @@ hipError_t launch_layer_norm(const void* x, const void* w, const void* b, void* 
                                        static_cast<const T*>(x), static_cast<const TW*>(w),
                                        static_cast<const TW*>(b), static_cast<T*>(y), rows,
                                        cols, g.tpr, eps);
-                  });
+                  }, static_cast<int64_t>(cols) * sizeof(T));
             });
           }
         });
@@ -745,7 +757,7 @@ hipError_t launch_rms_norm(const void* x, const void* w, void* y, int64_t rows, 
                     hipLaunchKernelGGL(kern, dim3(grid), dim3(g.block), 0, s,
                                        static_cast<const T*>(x), static_cast<const TW*>(w),
                                        static_cast<T*>(y), rows, cols, g.tpr, eps);
-                  });
+                  }, static_cast<int64_t>(cols) * sizeof(T));
             });
           }
         });

@@ -57,8 +57,9 @@ constexpr int kFlagAll = 63;
 constexpr int kPipeMaxIt = 4;
 
 // Number of workgroups of `block` lanes of `kernel` that are resident on the
-// whole current device at once (occupancy x compute units), cached.
-int64_t resident_blocks(const void* kernel, int block);
+// whole current device at once (occupancy, at most max_per_cu, x compute
+// units); the occupancy is cached.
+int64_t resident_blocks(const void* kernel, int block, int max_per_cu = 1 << 30);
 
 // Register budget per lane for a register-resident row: 64 values (the
 // compiler widens every 16-bit value it reuses to an fp32 register), i.e. 16
