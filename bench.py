@@ -5,12 +5,17 @@ Metric: achieved HBM GB/s per kernel, as a fraction of the
 measured MI355X stream-copy peak; latency in microseconds.
 
 A "step" is one launch of the hot-path kernel over one batch of the workload.
-The default workload is the one the headline metric is quoted on (configs[1]:
-RMSNorm bf16 [8192, 4096], eps 1e-6).  Inputs are generated on the CPU with a
-fixed seed and copied to HBM before timing; the timed launches cycle through
-enough copies (>= 2 GiB in total) that no launch finds its data in the
-256 MB Infinity Cache.  ``value`` = algorithmic bytes x steps / elapsed time of
-the back-to-back timed region (device events on the launch stream).
+BASELINE.json's metric is quoted per kernel, on no single config, so the
+default workload is the largest single-GPU config: C4, the cross-entropy
+forward over fp32 logits [8192, 32000] (configs[3], 1.05 GB per launch).
+Inputs are generated on the CPU with a fixed seed and copied to HBM before
+timing; the launches cycle through enough copies (>= 2 GiB in total) that no
+launch finds its data in the 256 MB Infinity Cache.  Before the timed region
+the kernel runs back to back for 0.5 s (every copy touched, clocks at steady
+state), then for W warm-up launches; the K timed launches follow, bracketed by
+device events on the launch stream and by a roctx range
+``vbh-timed:<workload>:<K>`` that profiles select their dispatches by.
+``value`` = algorithmic bytes x K / event time of the timed region.
 
   python bench.py [--steps K] [--warmup W] [--workload KEY] [--all] [--no-cpu]
 
@@ -30,7 +35,7 @@ from pathlib import Path
 
 import torch
 
-from dslperfgap_amd import _lib, harness
+from dslperfgap_amd import _lib, _roctx, harness
 from dslperfgap_amd.workloads import HEADLINE, WORKLOADS
 
 METRIC = "achieved HBM GB/s and % of measured MI355X peak per kernel; latency µs"
@@ -99,21 +104,29 @@ def cpu_baseline(w, cpu_args, budget_s: float) -> dict:
     }
 
 
-def run_workload(key, steps, warmup, peak_measured, with_cpu, cpu_budget):
+DEVICE_WARM_S = 0.5
+
+
+def run_workload(key, steps, warmup, peaks, with_cpu, cpu_budget):
     w = WORKLOADS[key]
     log(f"[bench] {key}: generating inputs")
     cpu_args = w.make()
     rot = harness.make_rotation(w, cpu_args, "cuda:0")
     log(f"[bench] {key}: {rot.copies} HBM copies, {w.bytes_per_launch} B per launch")
+    # median of single launches (each fenced by its own events), before the
+    # timed region so that the timed launches are the workload's last dispatches
+    single = harness.time_kernel(rot.launch, reps=50, warmup=5)
     # steady state before timing: 0.5 s of back-to-back launches (clocks, page
-    # tables), then `warmup` more launches, at least two per HBM copy
-    harness.warm_gpu(rot.launch, 0.5)
-    warmup = max(warmup, 2 * rot.copies)
-    r = harness.time_back_to_back(rot.launch, steps, warmup)
+    # tables, every HBM copy touched), then the `warmup` launches inside
+    # time_back_to_back, then the timed region
+    harness.warm_gpu(rot.launch, DEVICE_WARM_S)
+    r = harness.time_back_to_back(rot.launch, steps, warmup,
+                                  fence=_roctx.range_(f"vbh-timed:{key}:{steps}"))
     per_launch_ms = r["event_ms"] / steps
     value = w.bytes_per_launch * steps / (r["event_ms"] * 1e-3) / 1e9
-    single = harness.time_kernel(rot.launch, reps=50, warmup=5)
     vendor_peak = VENDOR_PEAK_GBPS
+    peak_kind = w.peak_kind
+    peak_measured = peaks[peak_kind]
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -121,6 +134,7 @@ def run_workload(key, steps, warmup, peak_measured, with_cpu, cpu_budget):
         "n_gpus": 1,
         "steps": steps,
         "warmup": warmup,
+        "device_warm_s": DEVICE_WARM_S,
         "ms_per_step": round(r["wall_ms"] / steps, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -141,8 +155,11 @@ def run_workload(key, steps, warmup, peak_measured, with_cpu, cpu_budget):
             "traffic_source": f"rocprofv3 FETCH_SIZE/WRITE_SIZE, {TRAFFIC_FILE.name}",
             "algorithmic_bytes": w.bytes_per_launch,
         },
-        "measured_copy_peak_GBps": round(peak_measured / 1e9, 2),
+        "measured_copy_peak_GBps": round(peaks["copy"] / 1e9, 2),
+        "measured_read_peak_GBps": round(peaks["read"] / 1e9, 2),
+        "measured_peak_kind": peak_kind,
         "frac_of_measured_peak": round(value * 1e9 / peak_measured, 4),
+        "timed_range": f"vbh-timed:{key}:{steps}" if _roctx.available() else None,
     }
     del rot
     torch.cuda.empty_cache()
@@ -174,11 +191,12 @@ def main():
         sys.exit(1)
     _lib.lib()
     log(f"[bench] device: {torch.cuda.get_device_name(0)}")
-    peak = harness.copy_peak("cuda:0")
-    log(f"[bench] measured stream-copy peak: {peak / 1e9:.1f} GB/s")
+    peaks = {"copy": harness.copy_peak("cuda:0"), "read": harness.read_peak("cuda:0")}
+    log(f"[bench] measured stream-copy peak: {peaks['copy'] / 1e9:.1f} GB/s (read + write), "
+        f"stream-read peak: {peaks['read'] / 1e9:.1f} GB/s")
     keys = sorted(WORKLOADS) if args.all else [args.workload]
     for key in keys:
-        line = run_workload(key, args.steps, args.warmup, peak, not args.no_cpu, args.cpu_budget)
+        line = run_workload(key, args.steps, args.warmup, peaks, not args.no_cpu, args.cpu_budget)
         print(json.dumps(line), flush=True)
 
 

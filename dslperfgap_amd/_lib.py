@@ -78,6 +78,8 @@ SIGNATURES = {
                                  _vp]),
     "vbh_reduce_workspace_bytes": (_i64, [_i64, _i64, _i64, _i32, _i32]),
     "vbh_stream_copy": (_i32, [_vp, _vp, _i64, _vp]),
+    "vbh_stream_read": (_i32, [_vp, _i64, _vp, _i64, _vp]),
+    "vbh_stream_read_partial_bytes": (_i64, [_i64]),
     "vbh_tune_override": (_i32, [_i32, _i32, _i32, _i32]),
 }
 
@@ -88,7 +90,7 @@ FAST_ENTRY_POINTS = (
     "vbh_softmax_dim_fwd",
     "vbh_logsumexp_fwd", "vbh_logsumexp_fwd_ws", "vbh_cross_entropy_fwd",
     "vbh_cross_entropy_fwd_ws", "vbh_cross_entropy_bwd", "vbh_reduce_fwd", "vbh_reduce_fwd_ws",
-    "vbh_stream_copy",
+    "vbh_stream_copy", "vbh_stream_read",
 )
 
 

@@ -942,4 +942,27 @@ int vbh_stream_copy(const void* src, void* dst, int64_t bytes, void* stream) {
                     "stream_copy launch");
 }
 
+int64_t vbh_stream_read_partial_bytes(int64_t bytes) {
+  if (bytes <= 0 || bytes % 16 != 0 || bytes / 16 > kMaxWorkItems) return 0;
+  return 4 * stream_read_tiles(bytes);
+}
+
+int vbh_stream_read(const void* src, int64_t bytes, void* partial, int64_t partial_bytes,
+                    void* stream) {
+  if (bytes < 0 || bytes % 16 != 0)
+    return fail(VBH_E_INVALID, "stream_read: bytes must be a non-negative multiple of 16");
+  if (bytes == 0) return 0;
+  if (bytes / 16 > kMaxWorkItems) return fail(VBH_E_RANGE, "stream_read: more than 64 GiB");
+  if (!src || !aligned16(src) || !partial || (reinterpret_cast<uintptr_t>(partial) & 3u) != 0)
+    return fail(VBH_E_INVALID,
+                "stream_read: src must be non-null and 16-byte aligned, partial non-null and "
+                "4-byte aligned");
+  const int64_t need = vbh_stream_read_partial_bytes(bytes);
+  if (partial_bytes < need)
+    return fail(VBH_E_INVALID, "stream_read: partial holds %lld bytes, %lld needed",
+                static_cast<long long>(partial_bytes), static_cast<long long>(need));
+  return hip_status(launch_stream_read(src, partial, bytes, static_cast<hipStream_t>(stream)),
+                    "stream_read launch");
+}
+
 }  // extern "C"

@@ -1,9 +1,18 @@
-// Device-to-device copy used to measure the sustainable HBM rate of one GPU.
-// Each 256-lane workgroup moves one contiguous 4 KiB tile (one 16-byte access
-// per lane); the grid covers the buffer once.  Loads are nontemporal; stores
-// are nontemporal and written through the L2 at device scope (the row kernels'
-// kStoreThrough policy), the fastest store form measured on MI355X for a 4 GiB
-// copy: 6657 GB/s against 6467 with nontemporal stores kept in the L2.
+// The two yardstick kernels of the measured HBM rates of one GPU.
+//
+// copy_kernel: device-to-device copy (read + write).  Each 256-lane workgroup
+// moves one contiguous 4 KiB tile (one 16-byte access per lane); the grid
+// covers the buffer once.  Loads are nontemporal; stores are nontemporal and
+// written through the L2 at device scope (the row kernels' kStoreThrough
+// policy), the fastest store form measured on MI355X for a 4 GiB copy: 6657
+// GB/s against 6467 with nontemporal stores kept in the L2.
+//
+// read_kernel: streaming read (the yardstick of kernels that read far more
+// than they write: logsumexp, the cross-entropy forward, mean / max / argmax).
+// Each 256-lane workgroup reads a contiguous tile of kReadUnroll * 4 KiB with
+// nontemporal 16-byte loads (lane t takes vectors t, t + 256, ...), folds them
+// with XOR and writes one 32-bit word per workgroup, so every load is used and
+// the writes are 1/4096 of the bytes read at the default tile.
 #include "vbh_device.h"
 #include "vbh_launch.h"
 
@@ -29,7 +38,49 @@ __global__ __launch_bounds__(256) void copy_kernel(const u32x4* __restrict__ src
         static_cast<int>(threadIdx.x * sizeof(u32x4)), 0, kCacheNtSc1);
 }
 
+constexpr int kReadBlock = 256;
+
+template <int U>
+__global__ __launch_bounds__(kReadBlock) void read_kernel(const u32x4* __restrict__ src,
+                                                          uint32_t* __restrict__ partial,
+                                                          int64_t n) {
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * kReadBlock * U;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  u32x4 v[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t i = first + u * kReadBlock + threadIdx.x;
+    v[u] = i < n ? __builtin_nontemporal_load(src + i) : u32x4{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) acc ^= v[u];
+  uint32_t x = acc.x ^ acc.y ^ acc.z ^ acc.w;
+#pragma unroll
+  for (int m = kWave / 2; m >= 1; m /= 2) x ^= __shfl_xor(x, m, kWave);
+  __shared__ uint32_t lds[kReadBlock / kWave];
+  if ((threadIdx.x & (kWave - 1)) == 0) lds[threadIdx.x / kWave] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t r = 0;
+#pragma unroll
+    for (int w = 0; w < kReadBlock / kWave; ++w) r ^= lds[w];
+    partial[blockIdx.x] = r;
+  }
+}
+
 }  // namespace
+
+int64_t stream_read_tiles(int64_t bytes) {
+  const int64_t tile = int64_t(kReadBlock) * kReadUnroll * 16;
+  return (bytes + tile - 1) / tile;
+}
+
+hipError_t launch_stream_read(const void* src, void* partial, int64_t bytes, hipStream_t s) {
+  const int64_t n = bytes / 16;
+  hipLaunchKernelGGL(read_kernel<kReadUnroll>, dim3(stream_read_tiles(bytes)), dim3(kReadBlock),
+                     0, s, static_cast<const u32x4*>(src), static_cast<uint32_t*>(partial), n);
+  return hipGetLastError();
+}
 
 hipError_t launch_stream_copy(const void* src, void* dst, int64_t bytes, hipStream_t s) {
   const int64_t n = bytes / 16;

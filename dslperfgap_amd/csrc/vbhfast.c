@@ -75,12 +75,17 @@ static int parse(PyObject* const* args, Py_ssize_t n, const char* fmt, arg_t* ou
 #define I(k) ((int)a[k].q)
 #define F(k) ((float)a[k].f)
 
+/* Most arguments any entry point takes (parse() fills one arg_t per format
+ * character, after checking that the call passed exactly that many). */
+#define MAX_ARGS 24
+
 /* `call` invokes the entry point through fn_<name>, set by bind(). */
 #define ENTRY(name, fmt, call)                                                   \
+  _Static_assert(sizeof(fmt) - 1 <= MAX_ARGS, #name ": too many arguments");     \
   static __typeof__(&name) fn_##name = NULL;                                     \
   static const char fmt_##name[] = fmt;                                          \
   static PyObject* py_##name(PyObject* self, PyObject* const* args, Py_ssize_t n) { \
-    arg_t a[24];                                                                 \
+    arg_t a[MAX_ARGS];                                                           \
     int rc;                                                                      \
     (void)self;                                                                  \
     if (fn_##name == NULL) {                                                     \
@@ -122,6 +127,7 @@ ENTRY(vbh_reduce_fwd_ws, "pppqqqiiipqp",
       fn_vbh_reduce_fwd_ws(P(0), P(1), P(2), Q(3), Q(4), Q(5), I(6), I(7), I(8), P(9), Q(10),
                            P(11)))
 ENTRY(vbh_stream_copy, "ppqp", fn_vbh_stream_copy(P(0), P(1), Q(2), P(3)))
+ENTRY(vbh_stream_read, "pqpqp", fn_vbh_stream_read(P(0), Q(1), P(2), Q(3), P(4)))
 
 #define METHOD(name) {#name, (PyCFunction)(void (*)(void))py_##name, METH_FASTCALL, NULL}
 
@@ -136,7 +142,7 @@ static const struct {
     SLOT(vbh_softmax_dim_fwd),   SLOT(vbh_logsumexp_fwd),    SLOT(vbh_logsumexp_fwd_ws), SLOT(vbh_softmax_fwd_ws),
     SLOT(vbh_cross_entropy_fwd), SLOT(vbh_cross_entropy_fwd_ws), SLOT(vbh_cross_entropy_bwd),
     SLOT(vbh_reduce_fwd),
-    SLOT(vbh_reduce_fwd_ws),     SLOT(vbh_stream_copy),
+    SLOT(vbh_reduce_fwd_ws),     SLOT(vbh_stream_copy),      SLOT(vbh_stream_read),
 };
 #define N_SLOTS (sizeof(slots) / sizeof(slots[0]))
 
@@ -172,7 +178,7 @@ static PyMethodDef methods[] = {
     METHOD(vbh_softmax_dim_fwd),   METHOD(vbh_logsumexp_fwd),     METHOD(vbh_logsumexp_fwd_ws), METHOD(vbh_softmax_fwd_ws),
     METHOD(vbh_cross_entropy_fwd), METHOD(vbh_cross_entropy_fwd_ws),
     METHOD(vbh_cross_entropy_bwd), METHOD(vbh_reduce_fwd),
-    METHOD(vbh_reduce_fwd_ws),     METHOD(vbh_stream_copy),
+    METHOD(vbh_reduce_fwd_ws),     METHOD(vbh_stream_copy),       METHOD(vbh_stream_read),
     {NULL, NULL, 0, NULL},
 };
 

@@ -14,7 +14,11 @@ MI355X counterparts of the reference's timing and roofline helpers:
 * ``Rotation``       HBM-resident copies of a workload's inputs and outputs that
                      successive launches cycle through, so that no launch finds its
                      data in the 256 MB Infinity Cache (MALL) or the L2;
-* ``copy_peak``      the sustained device-to-device copy rate (vbh_stream_copy).
+* ``copy_peak``      the sustained device-to-device copy rate (vbh_stream_copy),
+                     the yardstick of kernels that read and write about as much;
+* ``read_peak``      the sustained streaming-read rate (vbh_stream_read), the
+                     yardstick of kernels that write almost nothing (logsumexp,
+                     the cross-entropy forward, mean / max / argmax).
 
 The timed launches go straight through the C ABI with preallocated buffers
 (what ``hip_impl`` calls after its checks and allocation), so host overhead per
@@ -159,21 +163,28 @@ def time_kernel(launch: Callable[[int], None], reps: int = 50, warmup: int = 15,
             "min_ms": times[0], "reps": reps}
 
 
-def time_back_to_back(launch: Callable[[int], None], steps: int, warmup: int) -> dict:
+def time_back_to_back(launch: Callable[[int], None], steps: int, warmup: int,
+                      fence=None) -> dict:
     """`steps` launches back to back, bracketed by synchronize and device events.
 
-    Returns the event time and the wall time of the whole timed region (ms)."""
+    `fence`, if given, is a context manager entered after the warm-up launches
+    have completed and left once the timed launches have (a profiler range that
+    holds exactly the timed dispatches).  Returns the event time and the wall
+    time of the whole timed region (ms)."""
+    import contextlib
+
     for i in range(warmup):
         launch(i)
     torch.cuda.synchronize()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    s.record()
-    for i in range(steps):
-        launch(warmup + i)
-    e.record()
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) * 1e3
+    with fence if fence is not None else contextlib.nullcontext():
+        t0 = time.perf_counter()
+        s.record()
+        for i in range(steps):
+            launch(warmup + i)
+        e.record()
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e3
     return {"event_ms": s.elapsed_time(e), "wall_ms": wall, "steps": steps}
 
 
@@ -205,6 +216,24 @@ def copy_peak(device, nbytes: int = 4 << 30, reps: int = 20) -> float:
     r = time_back_to_back(launch, reps, 3)
     del src, dst
     return 2.0 * nbytes * reps / (r["event_ms"] * 1e-3)
+
+
+def read_peak(device, nbytes: int = 4 << 30, reps: int = 20) -> float:
+    """Sustained streaming-read rate in bytes/s (bytes read; the one 32-bit
+    word written per 16 KiB tile is not counted)."""
+    src = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    src.fill_(1)
+    pbytes = _lib.lib().vbh_stream_read_partial_bytes(nbytes)
+    partial = torch.empty(pbytes, dtype=torch.uint8, device=device)
+    stream = _bridge.stream(torch.device(device))
+
+    def launch(_):
+        _lib.call("vbh_stream_read", src.data_ptr(), nbytes, partial.data_ptr(), pbytes, stream)
+
+    warm_gpu(launch, 0.3)
+    r = time_back_to_back(launch, reps, 3)
+    del src, partial
+    return 1.0 * nbytes * reps / (r["event_ms"] * 1e-3)
 
 
 def copy_rate_at(device, traffic_bytes: int, reps: int = 200,

@@ -128,15 +128,23 @@ def read_stats(path, kernels) -> dict:
     return out
 
 
-def read_counter(path, kernels) -> dict:
-    """{workload: (mean counter value per dispatch, dispatches)} from a counter_collection.csv."""
-    acc = collections.defaultdict(list)
+def read_counter(path, kernels, tail: int = 0) -> dict:
+    """{workload: (mean counter value per dispatch, dispatches)} from a
+    counter_collection.csv; with `tail`, over the last `tail` dispatches of
+    each workload's kernel only (the copy kernel always over all of them)."""
+    acc = collections.defaultdict(lambda: collections.defaultdict(float))
     with open(path, newline="") as f:
         for r in csv.DictReader(f):
             key = classify(r["Kernel_Name"], kernels)
             if key:
-                acc[key].append(float(r["Counter_Value"]))
-    return {k: (sum(v) / len(v), len(v)) for k, v in acc.items()}
+                acc[key][int(r["Dispatch_Id"])] += float(r["Counter_Value"])
+    out = {}
+    for k, per in acc.items():
+        ids = sorted(per)
+        if tail and k != COPY:
+            ids = ids[-tail:]
+        out[k] = (sum(per[i] for i in ids) / len(ids), len(ids))
+    return out
 
 
 def trace_table(stats: dict, alg: dict, order) -> list[dict]:
@@ -227,14 +235,14 @@ def _dir_prefix(path, suffix: str) -> tuple[str, str]:
     return str(p.parent), name[:-len(suffix)] if name.endswith(suffix) else name
 
 
-def render(preset: str, trace, fetch, write) -> tuple[str, str]:
+def render(preset: str, trace, fetch, write, tail: int = 0) -> tuple[str, str]:
     """The trace summary and the traffic summary, headed by the commands that
     wrote the input files (directories and prefixes taken from their paths)."""
     p = PRESETS[preset]
     kernels, alg = p["kernels"], p["alg"]()
     order = [k for k, _ in kernels]
     stats = read_stats(trace, kernels)
-    fetched, written = read_counter(fetch, kernels), read_counter(write, kernels)
+    fetched, written = read_counter(fetch, kernels, tail), read_counter(write, kernels, tail)
     # a renamed kernel template must not drop a workload from the summaries
     # (bench.py reads the traffic lines)
     missing = [k for k in order if k not in stats or k not in fetched or k not in written]
@@ -270,62 +278,167 @@ def render(preset: str, trace, fetch, write) -> tuple[str, str]:
     return trace_txt, head + format_traffic(rows, fs, ws, p["machine"])
 
 
-HEADLINE_FILE = "rms_norm_rows_C2_trace.txt"
+TIMED_PREFIX = "vbh-timed:"
 
 
-def render_headline(trace, bench_line) -> str:
-    """C2's kernel (and the copy kernel) from the trace of `bench.py --no-cpu`,
-    with bench.py's own line from the same run."""
+def read_dispatches(path) -> list[dict]:
+    """Kernel dispatches of a ``<prefix>_kernel_trace.csv``: name, start, end (ns)."""
+    out = []
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            out.append(dict(name=r["Kernel_Name"], start=int(r["Start_Timestamp"]),
+                            end=int(r["End_Timestamp"]), dispatch=int(r["Dispatch_Id"])))
+    return out
+
+
+def read_ranges(path) -> list[dict]:
+    """bench.py's timed roctx ranges from a ``<prefix>_marker_api_trace.csv``:
+    the rows whose function (the range's message) starts with ``vbh-timed:``."""
+    out = []
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            msg = r.get("Function") or r.get("Message") or ""
+            if msg.startswith(TIMED_PREFIX):
+                _, key, steps = msg.split(":")
+                out.append(dict(workload=key, steps=int(steps), start=int(r["Start_Timestamp"]),
+                                end=int(r["End_Timestamp"])))
+    return out
+
+
+def timed_row(dispatches: list[dict], rng: dict, alg_bytes: int) -> dict:
+    """Statistics of the dominant kernel (most device time) among the dispatches
+    that ran entirely inside the timed range."""
+    inside = [d for d in dispatches if d["start"] >= rng["start"] and d["end"] <= rng["end"]]
+    if not inside:
+        raise ValueError(f"no kernel dispatch inside the timed range of {rng['workload']}")
+    by_name = collections.defaultdict(list)
+    for d in inside:
+        by_name[d["name"]].append(d)
+    name, ds = max(by_name.items(), key=lambda kv: sum(d["end"] - d["start"] for d in kv[1]))
+    ds.sort(key=lambda d: d["start"])
+    dur = sorted(d["end"] - d["start"] for d in ds)
+    n = len(dur)
+    avg = sum(dur) / n
+    span = ds[-1]["end"] - ds[0]["start"]
+    return dict(workload=rng["workload"], steps=rng["steps"], kernel=name, calls=n,
+                others=len(inside) - n, avg_ns=avg, min_ns=dur[0], max_ns=dur[-1],
+                median_ns=dur[n // 2], period_ns=span / n, alg_bytes=alg_bytes,
+                gbps=alg_bytes / avg, gbps_period=alg_bytes / (span / n))
+
+
+def timed_file(workload: str, kernel: str) -> str:
+    """``<kernel>_<workload>_timed_trace.txt`` (kernel = the template's base name)."""
+    m = re.search(r"(?:::|_)(\w+?)(?:<|I[A-Z]|\()", kernel) or re.search(r"(\w+)", kernel)
+    base = m.group(1) if m else "kernel"
+    m2 = re.search(r"N_\d+(\d\d)?([a-z_]+?)I", kernel)
+    if kernel.startswith("_Z") and m2:
+        base = m2.group(2)
+    return f"{base}_{workload}_timed_trace.txt"
+
+
+def render_timed(kernel_trace, markers, bench_lines) -> tuple[str, dict]:
+    """Summary of the kernel dispatches inside each timed range of
+    ``bench.py`` (one range per workload), next to bench.py's own lines from
+    the same run.  Returns the combined text and {workload: (file name, text)}."""
     import json
 
-    tdir, tpre = _dir_prefix(trace, "_kernel_stats.csv")
-    with open(trace, newline="") as f:
-        rows = [r for r in csv.DictReader(f)
-                if re.search(r"rms_norm_rows|copy_kernel\(", r["Name"])]
-    line = json.loads(Path(bench_line).read_text().strip().splitlines()[-1])
-    alg = WORKLOADS["C2_rms_norm"].bytes_per_launch
-    out = [f"rocprofv3 kernel trace -- headline workload C2 (RMSNorm bf16 [8192, 4096], eps 1e-6)", "",
-           "Command (from the repository root, after `cd /tmp && export TMPDIR=/tmp`):",
-           f"  rocprofv3 --kernel-trace --stats --output-format csv -d {tdir} -o {tpre} -- \\",
-           "      python3 -u bench.py --no-cpu",
-           "Summary: python -m dslperfgap_amd.viperbench.rocprof_summary headline ...", "",
-           "bench.py's line in the same run reports latency_us (device events over the 1000",
-           "back-to-back timed launches / 1000); the trace average covers every dispatch of",
-           "the kernel (warm-up included).", "",
-           f"{'calls':>7}{'avg_ns':>11}{'min_ns':>9}{'max_ns':>9}{'stddev':>9}{'GB/s':>8}  kernel"]
+    dispatches = read_dispatches(kernel_trace)
+    ranges = read_ranges(markers)
+    if not ranges:
+        raise ValueError(f"{markers}: no {TIMED_PREFIX} range (was bench.py run under "
+                         "rocprofv3 --marker-trace?)")
+    lines = {}
+    for ln in Path(bench_lines).read_text().splitlines():
+        ln = ln.strip()
+        if ln.startswith("{"):
+            d = json.loads(ln)
+            lines[d["config"]["workload"]] = d
+    tdir, tpre = _dir_prefix(kernel_trace, "_kernel_trace.csv")
+    rows = [timed_row(dispatches, r, WORKLOADS[r["workload"]].bytes_per_launch) for r in ranges]
+    keys = [r["workload"] for r in rows]
+    args = "--all" if len(rows) > 1 else (
+        "" if keys == ["C4_cross_entropy"] else f"--workload {keys[0]}")
+    steps = rows[0]["steps"]
+    step_arg = "" if steps == 1000 else f" --steps {steps}"
+    cmd = f"python3 -u bench.py {args}{step_arg} --no-cpu".replace("  ", " ")
+    head = [f"rocprofv3 kernel trace of bench.py's timed regions (MI355X, gfx950)", "",
+            "Command (from the repository root, after `cd /tmp && export TMPDIR=/tmp`):",
+            f"  rocprofv3 --kernel-trace --marker-trace --output-format csv -d {tdir} -o {tpre} -- \\",
+            f"      {cmd} > BENCH_LINES",
+            f"Summary: python -m dslperfgap_amd.viperbench.rocprof_summary timed \\",
+            f"      --kernel-trace {kernel_trace} --markers {markers} --bench-lines BENCH_LINES", "",
+            "Only dispatches that ran entirely inside bench.py's roctx range",
+            "vbh-timed:<workload>:<steps> are counted: the timed launches, nothing of the",
+            "warm-up.  avg_ns = mean kernel duration; period_ns = (end of the last - start of",
+            "the first) / calls, the per-launch time the device events of bench.py measure",
+            "(kernel + gap to the next launch).  GB/s = algorithmic bytes / avg_ns;",
+            "GB/s_period = algorithmic bytes / period_ns.", ""]
+    table = [f"{'workload':<21}{'calls':>6}{'avg_ns':>10}{'med_ns':>10}{'min_ns':>9}{'max_ns':>9}"
+             f"{'period_ns':>11}{'GB/s':>7}{'GB/s_period':>12}{'bench_us':>10}{'period/bench':>13}"]
     for r in rows:
-        avg = float(r["AverageNs"])
-        b = alg if "rms_norm" in r["Name"] else COPY_BYTES
-        out.append(f"{int(r['Calls']):>7}{avg:>11.0f}{float(r['MinNs']):>9.0f}"
-                   f"{float(r['MaxNs']):>9.0f}{float(r['StdDev']):>9.0f}{b / avg:>8.0f}"
-                   f"  {r['Name'][:100]}")
-    out += ["", f"bench.py line of the traced run: value {line['value']} GB/s, "
-                f"latency_us {line['latency_us']}",
-            f"GB/s from the trace = {alg:,} B / avg_ns"]
-    return "\n".join(out) + "\n"
+        b = lines.get(r["workload"], {})
+        lat = b.get("latency_us")
+        r["bench_latency_us"] = lat
+        r["agree"] = (r["period_ns"] / 1e3) / lat if lat else float("nan")
+        table.append(f"{r['workload']:<21}{r['calls']:>6}{r['avg_ns']:>10.0f}{r['median_ns']:>10.0f}"
+                     f"{r['min_ns']:>9.0f}{r['max_ns']:>9.0f}{r['period_ns']:>11.0f}"
+                     f"{r['gbps']:>7.0f}{r['gbps_period']:>12.0f}"
+                     f"{lat if lat is not None else float('nan'):>10.3f}{r['agree']:>13.4f}")
+    kernels = ["", "Kernels:"] + [f"  {r['workload']}: {r['kernel'][:150]}"
+                                  + (f"  (+{r['others']} other dispatches in the range)"
+                                     if r["others"] else "")
+                                  + (f"  (range named {r['steps']} steps, {r['calls']} dispatches)"
+                                     if r["calls"] != r["steps"] else "") for r in rows]
+    bench = ["", "bench.py lines of the traced run (value GB/s, latency_us, roofline.frac):"]
+    for k in keys:
+        b = lines.get(k)
+        if b:
+            bench.append(f"  {k}: {b['value']} GB/s, {b['latency_us']} us, "
+                         f"frac {b['roofline']['frac']}, of measured {b['measured_peak_kind']} "
+                         f"peak {b['frac_of_measured_peak']}")
+    combined = "\n".join(head + table + kernels + bench) + "\n"
+    per = {}
+    for r in rows:
+        i = keys.index(r["workload"])
+        one = "\n".join(head + [table[0], table[1 + i], "", "Kernel:", f"  {r['kernel']}"]
+                        + [b for b in bench[:1] + [x for x in bench[1:]
+                                                   if x.startswith(f"  {r['workload']}:")]]) + "\n"
+        per[r["workload"]] = (timed_file(r["workload"], r["kernel"]), one)
+    return combined, per
 
 
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
-    ap.add_argument("preset", choices=sorted(PRESETS) + ["headline"])
-    ap.add_argument("--trace", required=True, help="<prefix>_kernel_stats.csv")
+    ap.add_argument("preset", choices=sorted(PRESETS) + ["timed"])
+    ap.add_argument("--trace", help="<prefix>_kernel_stats.csv")
+    ap.add_argument("--kernel-trace", help="timed: <prefix>_kernel_trace.csv")
+    ap.add_argument("--markers", help="timed: <prefix>_marker_api_trace.csv")
+    ap.add_argument("--combined-name", default=None,
+                    help="timed: also write the table of every range under this file name")
     ap.add_argument("--fetch", help="FETCH_SIZE <prefix>_counter_collection.csv")
     ap.add_argument("--write", help="WRITE_SIZE <prefix>_counter_collection.csv")
-    ap.add_argument("--bench-line", help="headline: the JSON line bench.py printed in the run")
+    ap.add_argument("--bench-lines", help="timed: the JSON lines bench.py printed in the run")
+    ap.add_argument("--tail", type=int, default=0,
+                    help="counters: only the last TAIL dispatches of each workload's kernel "
+                         "(bench.py's timed launches are each workload's last ones)")
     ap.add_argument("--out-dir", default=None, help="write the summaries here (else print)")
     args = ap.parse_args(argv)
-    if args.preset == "headline":
-        if not args.bench_line:
-            ap.error("headline needs --bench-line")
-        txt = render_headline(args.trace, args.bench_line)
+    if args.preset == "timed":
+        if not (args.kernel_trace and args.markers and args.bench_lines):
+            ap.error("timed needs --kernel-trace, --markers and --bench-lines")
+        combined, per = render_timed(args.kernel_trace, args.markers, args.bench_lines)
         if args.out_dir:
-            Path(args.out_dir, HEADLINE_FILE).write_text(txt)
+            for name, txt in per.values():
+                Path(args.out_dir, name).write_text(txt)
+            if args.combined_name:
+                Path(args.out_dir, args.combined_name).write_text(combined)
         else:
-            sys.stdout.write(txt)
+            sys.stdout.write(combined)
         return 0
-    if not (args.fetch and args.write):
-        ap.error(f"{args.preset} needs --fetch and --write")
-    trace_txt, traffic_txt = render(args.preset, args.trace, args.fetch, args.write)
+    if not (args.trace and args.fetch and args.write):
+        ap.error(f"{args.preset} needs --trace, --fetch and --write")
+    trace_txt, traffic_txt = render(args.preset, args.trace, args.fetch, args.write,
+                                    tail=args.tail)
     if args.out_dir:
         names = PRESETS[args.preset]["files"]
         Path(args.out_dir, names[0]).write_text(trace_txt)

@@ -228,6 +228,21 @@ int64_t vbh_reduce_workspace_bytes(int64_t outer, int64_t n, int64_t inner, int 
  *           (no AMD entry there) with a measured figure. */
 int vbh_stream_copy(const void* src, void* dst, int64_t bytes, void* stream);
 
+/* Streaming read of `bytes` (16-byte aligned pointer, multiple of 16): every
+ * 16-byte vector is loaded once and folded into one 32-bit word per 16 KiB
+ * tile, written to `partial` (4-byte aligned, at least
+ * vbh_stream_read_partial_bytes(bytes) bytes).  Its sustained rate is the
+ * measured read peak that read-dominated kernels (logsumexp, cross-entropy
+ * forward, mean / max / argmax) are quoted against.
+ * Replaces: the vendor-spec PEAKS table of experiments/exp_cliff_roofline.py:192-218,
+ *           as vbh_stream_copy does, for kernels that write almost nothing. */
+int vbh_stream_read(const void* src, int64_t bytes, void* partial, int64_t partial_bytes,
+                    void* stream);
+
+/* Bytes of `partial` vbh_stream_read needs for a read of `bytes` (0 for an
+ * invalid or empty size). */
+int64_t vbh_stream_read_partial_bytes(int64_t bytes);
+
 /* Launch-geometry override for sweeps: threads per row `tpr` (a power of two
  * up to 64, or a multiple of 64 up to 1024) and workgroup size `block`
  * (64..1024, a multiple of 64 and of tpr)

@@ -143,3 +143,82 @@ def test_bench_reads_traffic_of_every_config_from_the_committed_summary():
         t = bench.measured_traffic(key)
         assert t is not None, key
         assert 0.99 < t / w.bytes_per_launch < 1.01, (key, t)
+
+
+# ---------------------------------------------------------------------------
+# timed mode: dispatches inside bench.py's roctx range only
+# ---------------------------------------------------------------------------
+CE = ("void vbh::(anonymous namespace)::ce_fwd_rows<float, 4, 8, true, false>"
+      "(float const*, void const*, int, float*, float*, float*)")
+
+
+def _timed_fixture(tmp_path, steps=4):
+    kt_hdr = ["Kind", "Agent_Id", "Queue_Id", "Stream_Id", "Thread_Id", "Dispatch_Id", "Kernel_Id",
+              "Kernel_Name", "Correlation_Id", "Start_Timestamp", "End_Timestamp"]
+    rows, t, did = [], 1000, 0
+
+    def disp(name, dur, gap=1000):
+        nonlocal t, did
+        did += 1
+        rows.append(["KERNEL_DISPATCH", "Agent 1", 1, 0, 1, did, 7, name, did, t, t + dur])
+        t += dur + gap
+
+    for _ in range(3):             # warm-up: long launches that must not count
+        disp(CE, 900_000)
+    start = t - 500
+    for i in range(steps):         # timed launches: 150, 160, 170, 180 us
+        disp(CE, 150_000 + 10_000 * i)
+    disp(OTHER, 10)                # a stray kernel inside the range, not the dominant one
+    end = t + 500
+    disp(CE, 900_000)              # after the range
+    kt = _write(tmp_path / "run" / "c4" / "c4_kernel_trace.csv", kt_hdr, rows)
+    mk = _write(tmp_path / "run" / "c4" / "c4_marker_api_trace.csv",
+                ["Domain", "Function", "Process_Id", "Thread_Id", "Correlation_Id",
+                 "Start_Timestamp", "End_Timestamp"],
+                [["MARKER_CORE_RANGE_API", "unrelated", 1, 1, 1, 0, 10**12],
+                 ["MARKER_CORE_RANGE_API", f"vbh-timed:C4_cross_entropy:{steps}", 1, 1, 2, start,
+                  end]])
+    span = rows[3 + steps - 1][10] - rows[3][9]
+    line = {"config": {"workload": "C4_cross_entropy"}, "value": 1.0,
+            "latency_us": span / steps / 1e3, "roofline": {"frac": 0.5},
+            "measured_peak_kind": "read", "frac_of_measured_peak": 0.9}
+    bl = tmp_path / "run" / "c4_line.jsonl"
+    bl.write_text("progress text\n" + __import__("json").dumps(line) + "\n")
+    return kt, mk, bl, span
+
+
+def test_timed_summary_counts_only_the_timed_dispatches(tmp_path):
+    kt, mk, bl, span = _timed_fixture(tmp_path)
+    combined, per = rs.render_timed(kt, mk, bl)
+    (name, txt), = per.values()
+    assert name == "ce_fwd_rows_C4_cross_entropy_timed_trace.txt"
+    row = rs.timed_row(rs.read_dispatches(kt), rs.read_ranges(mk)[0],
+                       WORKLOADS["C4_cross_entropy"].bytes_per_launch)
+    assert row["calls"] == 4 and row["others"] == 1
+    assert row["avg_ns"] == pytest.approx(165_000)
+    assert row["min_ns"] == 150_000 and row["max_ns"] == 180_000
+    assert row["period_ns"] == pytest.approx(span / 4)
+    assert row["gbps"] == pytest.approx(1_048_739_840 / 165_000)
+    # the bench line's latency equals span / steps here, so they agree exactly
+    assert " 1.0000" in txt
+    assert f"-d {kt.parent} -o c4 -- " in combined
+
+
+def test_timed_summary_needs_the_range(tmp_path):
+    kt, mk, bl, _ = _timed_fixture(tmp_path)
+    empty = _write(tmp_path / "m2.csv", ["Domain", "Function", "Start_Timestamp",
+                                         "End_Timestamp"], [])
+    with pytest.raises(ValueError, match="no vbh-timed"):
+        rs.render_timed(kt, empty, bl)
+
+
+def test_counter_tail_keeps_the_last_dispatches(tmp_path):
+    hdr = ["Correlation_Id", "Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"]
+    f = _write(tmp_path / "c.csv", hdr,
+               [[i, i, C2, "FETCH_SIZE", 1000.0 if i < 5 else 10.0] for i in range(1, 9)]
+               + [[9, 9, COPYK, "FETCH_SIZE", 4.0], [10, 10, COPYK, "FETCH_SIZE", 6.0]])
+    all_ = rs.read_counter(f, rs.CONFIG_KERNELS)
+    tail = rs.read_counter(f, rs.CONFIG_KERNELS, tail=3)
+    assert all_["C2_rms_norm"] == (pytest.approx((4 * 1000 + 4 * 10) / 8), 8)
+    assert tail["C2_rms_norm"] == (pytest.approx(10.0), 3)
+    assert tail[rs.COPY] == (pytest.approx(5.0), 2)   # the copy kernel keeps every dispatch
