@@ -14,7 +14,10 @@ tuning hook and the error message all reach one instance, whichever file
 ``VBHIP_LIB`` names.
 
 There is no non-HIP fallback: if the library or the binding module is
-missing, :func:`lib` raises ``ImportError`` naming the build command.
+missing, :func:`lib` raises ``ImportError`` naming the build command.  So does
+a library built from other sources than the ones on disk: the build records
+the SHA-256 of ``csrc/`` and ``include/`` in ``libvbhip.srchash`` next to the
+library, and :func:`lib` compares it with the tree before loading.
 """
 from __future__ import annotations
 
@@ -26,7 +29,8 @@ from pathlib import Path
 
 import torch  # noqa: F401  (loads the HIP runtime the library must share)
 
-LIB_PATH = Path(os.environ.get("VBHIP_LIB", Path(__file__).resolve().parent / "libvbhip.so"))
+PKG_DIR = Path(__file__).resolve().parent
+LIB_PATH = Path(os.environ.get("VBHIP_LIB", PKG_DIR / "libvbhip.so"))
 
 ABI_VERSION = 1
 
@@ -107,6 +111,24 @@ _lib: ctypes.CDLL | None = None
 _fns: dict = {}
 
 
+def check_provenance(lib_path: Path = None) -> None:
+    """Raise ImportError unless the hash recorded next to the library equals
+    the hash of the sources in this tree (the library is what they build)."""
+    from .build import source_hash
+
+    lib_path = Path(lib_path or LIB_PATH)
+    hash_path = lib_path.with_suffix(".srchash")
+    if not hash_path.exists():
+        raise ImportError(f"{hash_path} is missing, so {lib_path.name} cannot be tied to the "
+                          "sources: rebuild with `python -m dslperfgap_amd.build`")
+    recorded = hash_path.read_text().strip()
+    current = source_hash(PKG_DIR)
+    if recorded != current:
+        raise ImportError(f"{lib_path.name} was built from other sources than the ones in "
+                          f"{PKG_DIR / 'csrc'} and include/ (hash {recorded[:12]} vs "
+                          f"{current[:12]}): rebuild with `python -m dslperfgap_amd.build`")
+
+
 def lib() -> ctypes.CDLL:
     """Load (once) and return the bound library."""
     global _lib
@@ -118,6 +140,7 @@ def lib() -> ctypes.CDLL:
                 raise ImportError(
                     f"{LIB_PATH} is missing: build it with `python -m dslperfgap_amd.build` "
                     "(there is no non-HIP fallback)")
+            check_provenance(LIB_PATH)
             handle = ctypes.CDLL(str(LIB_PATH))
             for name, (res, args) in SIGNATURES.items():
                 fn = getattr(handle, name)

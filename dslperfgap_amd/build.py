@@ -6,10 +6,16 @@ binding of its launching entry points (``csrc/vbhfast.c``) is then compiled
 with the host C compiler into ``dslperfgap_amd/_vbhfast*.so``, linked against
 that library.  Both are rebuilt on every call (the caller asked for a build).
 
+Provenance: the build writes ``libvbhip.srchash`` next to the library, the
+SHA-256 of every file under ``csrc/`` and ``include/`` (names and contents) it
+was built from.  ``_lib.lib()`` refuses a library whose hash differs from the
+sources on disk, so a stale binary cannot run in place of the code in the tree.
+
 Usage: ``python -m dslperfgap_amd.build`` or ``build()`` from Python.
 """
 from __future__ import annotations
 
+import hashlib
 import os
 import shutil
 import subprocess
@@ -22,6 +28,7 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 BUILD_DIR = PKG_DIR / "_build"
 LIB_PATH = PKG_DIR / "libvbhip.so"
+HASH_PATH = PKG_DIR / "libvbhip.srchash"
 FAST_PATH = PKG_DIR / ("_vbhfast" + sysconfig.get_config_var("EXT_SUFFIX"))
 REPO_ROOT = PKG_DIR.parent
 
@@ -38,6 +45,19 @@ DEVICE_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{REPO_ROOT / 'include'}",
 ]
+
+
+def source_hash(pkg_dir: Path = PKG_DIR, include_dir: Path | None = None) -> str:
+    """SHA-256 over the relative path and content of every file under the
+    package's ``csrc/`` and the repository's ``include/``, in sorted order."""
+    include_dir = include_dir or pkg_dir.parent / "include"
+    h = hashlib.sha256()
+    for base, tag in ((pkg_dir / "csrc", "csrc"), (include_dir, "include")):
+        for f in sorted(p for p in base.rglob("*") if p.is_file()):
+            h.update(f"{tag}/{f.relative_to(base).as_posix()}\0".encode())
+            h.update(f.read_bytes())
+            h.update(b"\0")
+    return h.hexdigest()
 
 
 def _hipcc() -> str:
@@ -64,6 +84,8 @@ def _compile(hipcc: str, src: Path) -> Path:
 def build(verbose: bool = True) -> Path:
     """Compile every HIP source for gfx950 and link libvbhip.so; return its path."""
     hipcc = _hipcc()
+    digest = source_hash()
+    HASH_PATH.unlink(missing_ok=True)  # no hash while the library is being replaced
     BUILD_DIR.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
@@ -78,6 +100,7 @@ def build(verbose: bool = True) -> Path:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, LIB_PATH)
     build_fast()
+    HASH_PATH.write_text(digest + "\n")
     if verbose:
         print(f"built {LIB_PATH} from {len(sources)} sources, and {FAST_PATH.name}",
               file=sys.stderr)

@@ -1,7 +1,10 @@
 """Drop-in API of the hip_impl modules (CPU tier).
 
-* each hip_impl function has exactly the signature of the reference golden
-  (restated in oracle/pytorch_impl.py: same names, order and defaults);
+* each hip_impl function has exactly the signature of the reference golden:
+  same parameter names, order, kinds and defaults as the reference's own source
+  text (tests/golden/reference_signatures.json, parsed from
+  ViperBench/<kernel>/pytorch_impl.py with ``ast`` by
+  tests/golden/make_ref_signatures.py), and as the oracle's restatement;
 * the modules load by file path, as ViperBench's harness loads impls
   (benchmark.py:61-67, experiments/_harness.py:152-167);
 * the host-side checks raise the reference's exceptions, and CPU tensors are
@@ -9,6 +12,7 @@
 """
 import importlib.util
 import inspect
+import json
 from pathlib import Path
 
 import pytest
@@ -36,6 +40,37 @@ def _load(kernel):
     mod = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(mod)
     return mod
+
+
+REF_SIGS = json.loads((Path(__file__).resolve().parent / "golden" /
+                       "reference_signatures.json").read_text())
+_KINDS = {"positional_or_keyword": inspect.Parameter.POSITIONAL_OR_KEYWORD,
+          "var_positional": inspect.Parameter.VAR_POSITIONAL,
+          "keyword_only": inspect.Parameter.KEYWORD_ONLY,
+          "var_keyword": inspect.Parameter.VAR_KEYWORD}
+
+
+def test_fixture_covers_every_unified_api_function():
+    assert set(REF_SIGS) == {fn for fns in FUNCS.values() for fn in fns}
+    for fn, sig in REF_SIGS.items():
+        assert sig["file"].startswith(f"ViperBench/{sig['kernel']}/pytorch_impl.py:"), fn
+
+
+@pytest.mark.parametrize("kernel", sorted(FUNCS))
+def test_signatures_match_the_reference_source(kernel):
+    """hip_impl against the reference's text (the committed ast fixture)."""
+    mod = _load(kernel)
+    for fn in FUNCS[kernel]:
+        got = list(inspect.signature(getattr(mod, fn)).parameters.values())
+        want = REF_SIGS[fn]["params"]
+        assert [p.name for p in got] == [p["name"] for p in want], fn
+        for g, w in zip(got, want):
+            assert g.kind == _KINDS[w["kind"]], (fn, g.name)
+            if "default" in w:
+                assert g.default == w["default"] and type(g.default) is type(w["default"]), (
+                    fn, g.name)
+            else:
+                assert g.default is inspect.Parameter.empty, (fn, g.name)
 
 
 @pytest.mark.parametrize("kernel", sorted(FUNCS))
