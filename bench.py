@@ -56,6 +56,13 @@ def measured_traffic(key: str):
     return None
 
 
+def lib_srchash() -> str:
+    """First 16 hex digits of the source hash the loaded library was built from
+    (checked against the tree by _lib.lib())."""
+    p = _lib.LIB_PATH.with_suffix(".srchash")
+    return p.read_text().strip()[:16] if p.exists() else None
+
+
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
@@ -160,6 +167,7 @@ def run_workload(key, steps, warmup, peaks, with_cpu, cpu_budget):
         "measured_peak_kind": peak_kind,
         "frac_of_measured_peak": round(value * 1e9 / peak_measured, 4),
         "timed_range": f"vbh-timed:{key}:{steps}" if _roctx.available() else None,
+        "lib_srchash": lib_srchash(),
     }
     del rot
     torch.cuda.empty_cache()
@@ -167,6 +175,36 @@ def run_workload(key, steps, warmup, peaks, with_cpu, cpu_budget):
         log(f"[bench] {key}: CPU baseline")
         line["cpu_baseline"] = cpu_baseline(w, cpu_args, cpu_budget)
     return line
+
+
+def run_copy_at(nbytes, steps, warmup, peaks):
+    """The stream copy moving `nbytes` per launch (half read, half written),
+    rotated through >= 2 GiB and timed like a workload: the yardstick of what a
+    kernel of that size can reach."""
+    launch, moved, copies = harness.copy_rotation("cuda:0", nbytes)
+    key = f"copy@{moved}"
+    harness.warm_gpu(launch, DEVICE_WARM_S)
+    r = harness.time_back_to_back(launch, steps, warmup,
+                                  fence=_roctx.range_(f"vbh-timed:{key}:{steps}"))
+    value = moved * steps / (r["event_ms"] * 1e-3) / 1e9
+    return {
+        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps,
+        "warmup": warmup, "device_warm_s": DEVICE_WARM_S,
+        "ms_per_step": round(r["wall_ms"] / steps, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "u8", "data": "synthetic (constant bytes)",
+        "config": {"workload": key, "desc": f"vbh_stream_copy of {moved // 2} B per launch "
+                                            f"(read + write {moved} B), {copies} buffer pairs"},
+        "latency_us": round(r["event_ms"] / steps * 1e3, 3),
+        "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": VENDOR_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(value / VENDOR_PEAK_GBPS, 4), "traffic": None,
+                     "algorithmic_bytes": moved},
+        "measured_copy_peak_GBps": round(peaks["copy"] / 1e9, 2),
+        "measured_read_peak_GBps": round(peaks["read"] / 1e9, 2),
+        "measured_peak_kind": "copy",
+        "frac_of_measured_peak": round(value * 1e9 / peaks["copy"], 4),
+        "timed_range": f"vbh-timed:{key}:{steps}" if _roctx.available() else None,
+        "lib_srchash": lib_srchash(),
+    }
 
 
 def main():
@@ -179,6 +217,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="seconds of timed CPU work for the CPU baseline")
+    ap.add_argument("--copy-at", type=int, nargs="+", metavar="BYTES",
+                    help="instead of workloads: the stream copy moving BYTES per launch "
+                         "(read + write), one line per size")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -194,6 +235,10 @@ def main():
     peaks = {"copy": harness.copy_peak("cuda:0"), "read": harness.read_peak("cuda:0")}
     log(f"[bench] measured stream-copy peak: {peaks['copy'] / 1e9:.1f} GB/s (read + write), "
         f"stream-read peak: {peaks['read'] / 1e9:.1f} GB/s")
+    if args.copy_at:
+        for nbytes in args.copy_at:
+            print(json.dumps(run_copy_at(nbytes, args.steps, args.warmup, peaks)), flush=True)
+        return
     keys = sorted(WORKLOADS) if args.all else [args.workload]
     for key in keys:
         line = run_workload(key, args.steps, args.warmup, peaks, not args.no_cpu, args.cpu_budget)

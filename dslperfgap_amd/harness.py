@@ -236,11 +236,10 @@ def read_peak(device, nbytes: int = 4 << 30, reps: int = 20) -> float:
     return 1.0 * nbytes * reps / (r["event_ms"] * 1e-3)
 
 
-def copy_rate_at(device, traffic_bytes: int, reps: int = 200,
-                 min_footprint: int = 2 << 30) -> float:
-    """Copy rate (bytes/s, read + write) when one launch moves `traffic_bytes`
-    (half read, half written), cycling through enough buffers that no launch
-    hits the Infinity Cache: the achievable rate at a kernel's own size."""
+def copy_rotation(device, traffic_bytes: int, min_footprint: int = 2 << 30):
+    """(launch, bytes moved per launch, copies): stream copies that each move
+    `traffic_bytes` (half read, half written, rounded down to 16-byte vectors),
+    cycling through enough buffers that no launch hits the Infinity Cache."""
     half = max(16, (traffic_bytes // 2) // 16 * 16)
     copies = max(2, math.ceil(min_footprint / (2 * half)))
     bufs = [(torch.empty(half, dtype=torch.uint8, device=device),
@@ -253,10 +252,20 @@ def copy_rate_at(device, traffic_bytes: int, reps: int = 200,
         a, b = bufs[k % copies]
         _lib.call("vbh_stream_copy", a.data_ptr(), b.data_ptr(), half, stream)
 
+    launch.buffers = bufs  # keep the buffers alive as long as the launcher
+    return launch, 2 * half, copies
+
+
+def copy_rate_at(device, traffic_bytes: int, reps: int = 200,
+                 min_footprint: int = 2 << 30) -> float:
+    """Copy rate (bytes/s, read + write) when one launch moves `traffic_bytes`
+    (half read, half written), cycling through enough buffers that no launch
+    hits the Infinity Cache: the achievable rate at a kernel's own size."""
+    launch, moved, copies = copy_rotation(device, traffic_bytes, min_footprint)
     warm_gpu(launch, 0.3)
     r = time_back_to_back(launch, reps, 2 * copies)
-    del bufs
-    return 2.0 * half * reps / (r["event_ms"] * 1e-3)
+    del launch
+    return 1.0 * moved * reps / (r["event_ms"] * 1e-3)
 
 
 @dataclass

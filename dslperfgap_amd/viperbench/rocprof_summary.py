@@ -212,10 +212,13 @@ PRESETS = {
         kernels=CONFIG_KERNELS, alg=config_bytes, machine=True,
         files=("row_kernels_all_configs_trace.txt", "row_kernels_all_configs_hbm_traffic.txt"),
         what="every measured workload (C1-C5, bench.py --all)",
-        trace_cmd="python3 -u bench.py --all --no-cpu",
+        trace_cmd="python3 -u bench.py --all --no-cpu --steps 50",
         pmc_cmd="python3 -u bench.py --all --no-cpu --steps 50",
-        source_note=("Calls include the 0.5 s warm-up, the warm-up launches and the 1000 timed\n"
-                     "launches of bench.py; every input cycles through >= 2 GiB of HBM copies.")),
+        source_note=("Trace calls include the single-launch timing, the 0.5 s warm-up, the warm-up\n"
+                     "launches and the 50 timed launches of bench.py (the timed region alone is in\n"
+                     "the *_timed_trace.txt summaries); the counters are averaged over the last 50\n"
+                     "dispatches of each workload's kernel (--tail 50), which are bench.py's timed\n"
+                     "launches.  Every input cycles through >= 2 GiB of HBM copies.")),
     "reference": dict(
         kernels=REFERENCE_KERNELS, alg=reference_bytes, machine=False,
         files=("reference_shapes_kernels_trace.txt", "reference_shapes_hbm_traffic.txt"),
@@ -273,7 +276,7 @@ def render(preset: str, trace, fetch, write, tail: int = 0) -> tuple[str, str]:
             f"Commands (from the repository root, after `cd /tmp && export TMPDIR=/tmp`), one\n"
             f"counter per run:\n{pmc}\n"
             f"Summary: python -m dslperfgap_amd.viperbench.rocprof_summary {preset} ...\n\n"
-            f"Counter values are KiB per dispatch, averaged over every dispatch of the kernel,\n"
+            f"Counter values are KiB per dispatch, averaged over the dispatches named above,\n"
             f"scaled by what each counter reads for the 4 GiB copy kernel of the same runs.\n\n")
     return trace_txt, head + format_traffic(rows, fs, ws, p["machine"])
 
@@ -305,6 +308,14 @@ def read_ranges(path) -> list[dict]:
     return out
 
 
+def alg_bytes_of(key: str) -> int:
+    """Algorithmic bytes per launch of a workload key, or of ``copy@N`` (the
+    stream copy moving N bytes per launch, read + write)."""
+    if key.startswith("copy@"):
+        return int(key.split("@", 1)[1])
+    return WORKLOADS[key].bytes_per_launch
+
+
 def timed_row(dispatches: list[dict], rng: dict, alg_bytes: int) -> dict:
     """Statistics of the dominant kernel (most device time) among the dispatches
     that ran entirely inside the timed range."""
@@ -326,14 +337,26 @@ def timed_row(dispatches: list[dict], rng: dict, alg_bytes: int) -> dict:
                 gbps=alg_bytes / avg, gbps_period=alg_bytes / (span / n))
 
 
+def kernel_base(kernel: str) -> str:
+    """Base name of a kernel symbol: ``ce_fwd_rows`` for
+    ``void vbh::(anonymous namespace)::ce_fwd_rows<float, ...>(...)`` and for
+    the Itanium-mangled ``_ZN3vbh12_GLOBAL__N_111ce_fwd_rowsI...``."""
+    if kernel.startswith("_ZN"):
+        i, last = 3, None
+        while i < len(kernel) and kernel[i].isdigit():
+            j = i
+            while kernel[j].isdigit():
+                j += 1
+            n = int(kernel[i:j])
+            last, i = kernel[j:j + n], j + n
+        return last or "kernel"
+    head = kernel.replace("(anonymous namespace)", "").split("(")[0].split("<")[0]
+    return head.split("::")[-1].split()[-1] if head.strip() else "kernel"
+
+
 def timed_file(workload: str, kernel: str) -> str:
-    """``<kernel>_<workload>_timed_trace.txt`` (kernel = the template's base name)."""
-    m = re.search(r"(?:::|_)(\w+?)(?:<|I[A-Z]|\()", kernel) or re.search(r"(\w+)", kernel)
-    base = m.group(1) if m else "kernel"
-    m2 = re.search(r"N_\d+(\d\d)?([a-z_]+?)I", kernel)
-    if kernel.startswith("_Z") and m2:
-        base = m2.group(2)
-    return f"{base}_{workload}_timed_trace.txt"
+    """``<kernel>_<workload>_timed_trace.txt`` (kernel = the symbol's base name)."""
+    return f"{kernel_base(kernel)}_{workload.replace('@', '_')}_timed_trace.txt"
 
 
 def render_timed(kernel_trace, markers, bench_lines) -> tuple[str, dict]:
@@ -354,10 +377,13 @@ def render_timed(kernel_trace, markers, bench_lines) -> tuple[str, dict]:
             d = json.loads(ln)
             lines[d["config"]["workload"]] = d
     tdir, tpre = _dir_prefix(kernel_trace, "_kernel_trace.csv")
-    rows = [timed_row(dispatches, r, WORKLOADS[r["workload"]].bytes_per_launch) for r in ranges]
+    rows = [timed_row(dispatches, r, alg_bytes_of(r["workload"])) for r in ranges]
     keys = [r["workload"] for r in rows]
-    args = "--all" if len(rows) > 1 else (
-        "" if keys == ["C4_cross_entropy"] else f"--workload {keys[0]}")
+    if all(k.startswith("copy@") for k in keys):
+        args = "--copy-at " + " ".join(k.split("@", 1)[1] for k in keys)
+    else:
+        args = "--all" if len(rows) > 1 else (
+            "" if keys == ["C4_cross_entropy"] else f"--workload {keys[0]}")
     steps = rows[0]["steps"]
     step_arg = "" if steps == 1000 else f" --steps {steps}"
     cmd = f"python3 -u bench.py {args}{step_arg} --no-cpu".replace("  ", " ")
@@ -389,6 +415,10 @@ def render_timed(kernel_trace, markers, bench_lines) -> tuple[str, dict]:
                                      if r["others"] else "")
                                   + (f"  (range named {r['steps']} steps, {r['calls']} dispatches)"
                                      if r["calls"] != r["steps"] else "") for r in rows]
+    hashes = sorted({b.get("lib_srchash") for b in lines.values() if b.get("lib_srchash")})
+    if hashes:
+        head.insert(1, f"Library source hash (libvbhip.srchash, csrc/ + include/): "
+                       f"{', '.join(hashes)}")
     bench = ["", "bench.py lines of the traced run (value GB/s, latency_us, roofline.frac):"]
     for k in keys:
         b = lines.get(k)
@@ -401,8 +431,8 @@ def render_timed(kernel_trace, markers, bench_lines) -> tuple[str, dict]:
     for r in rows:
         i = keys.index(r["workload"])
         one = "\n".join(head + [table[0], table[1 + i], "", "Kernel:", f"  {r['kernel']}"]
-                        + [b for b in bench[:1] + [x for x in bench[1:]
-                                                   if x.startswith(f"  {r['workload']}:")]]) + "\n"
+                        + bench[:2] + [x for x in bench[2:]
+                                       if x.startswith(f"  {r['workload']}:")]) + "\n"
         per[r["workload"]] = (timed_file(r["workload"], r["kernel"]), one)
     return combined, per
 
@@ -428,8 +458,11 @@ def main(argv=None) -> int:
             ap.error("timed needs --kernel-trace, --markers and --bench-lines")
         combined, per = render_timed(args.kernel_trace, args.markers, args.bench_lines)
         if args.out_dir:
-            for name, txt in per.values():
-                Path(args.out_dir, name).write_text(txt)
+            # one range: a file named for its kernel and workload; several: the
+            # combined table under --combined-name
+            if len(per) == 1 or not args.combined_name:
+                for name, txt in per.values():
+                    Path(args.out_dir, name).write_text(txt)
             if args.combined_name:
                 Path(args.out_dir, args.combined_name).write_text(combined)
         else:

@@ -222,3 +222,13 @@ def test_counter_tail_keeps_the_last_dispatches(tmp_path):
     assert all_["C2_rms_norm"] == (pytest.approx((4 * 1000 + 4 * 10) / 8), 8)
     assert tail["C2_rms_norm"] == (pytest.approx(10.0), 3)
     assert tail[rs.COPY] == (pytest.approx(5.0), 2)   # the copy kernel keeps every dispatch
+
+
+def test_kernel_base_names():
+    assert rs.kernel_base(CE) == "ce_fwd_rows"
+    assert rs.kernel_base(C2) == "rms_norm_rows"
+    assert rs.kernel_base(COPYK) == "copy_kernel"
+    assert rs.kernel_base(CONFIG_SYMBOLS["C5_layer_norm"]) == "layer_norm_pipe"
+    assert rs.timed_file("copy@33562624", COPYK) == "copy_kernel_copy_33562624_timed_trace.txt"
+    assert rs.alg_bytes_of("copy@33562624") == 33562624
+    assert rs.alg_bytes_of("C1_layer_norm") == WORKLOADS["C1_layer_norm"].bytes_per_launch
