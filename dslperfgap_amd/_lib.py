@@ -72,6 +72,11 @@ SIGNATURES = {
          _i64, _i64, _i32, _i32, _vp, _i64, _vp],
     ),
     "vbh_cross_entropy_workspace_bytes": (_i64, [_i64, _i64, _i64, _i32]),
+    "vbh_cross_entropy_fwd_noalloc": (
+        _i32,
+        [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _f32, _f32, _i64, _i64,
+         _i64, _i64, _i32, _i32, _vp],
+    ),
     "vbh_cross_entropy_bwd": (
         _i32,
         [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _f32,
@@ -93,8 +98,8 @@ FAST_ENTRY_POINTS = (
     "vbh_layer_norm_fwd", "vbh_rms_norm_fwd", "vbh_softmax_fwd", "vbh_softmax_fwd_ws",
     "vbh_softmax_dim_fwd",
     "vbh_logsumexp_fwd", "vbh_logsumexp_fwd_ws", "vbh_cross_entropy_fwd",
-    "vbh_cross_entropy_fwd_ws", "vbh_cross_entropy_bwd", "vbh_reduce_fwd", "vbh_reduce_fwd_ws",
-    "vbh_stream_copy", "vbh_stream_read",
+    "vbh_cross_entropy_fwd_ws", "vbh_cross_entropy_fwd_noalloc", "vbh_cross_entropy_bwd",
+    "vbh_reduce_fwd", "vbh_reduce_fwd_ws", "vbh_stream_copy", "vbh_stream_read",
 )
 
 

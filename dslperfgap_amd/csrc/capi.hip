@@ -409,6 +409,47 @@ Geometry pick_geometry(int64_t cols, int vec, int it_target, int tpr_override,
   return g;
 }
 
+// ---------------------------------------------------------------------------
+// Static scratch of vbh_cross_entropy_fwd_noalloc: the split cross entropy's
+// segment results (loss, lse, z_loss per segment) for callers that cannot
+// allocate device memory.  Each GPU holds its own copy of `scratch` from the
+// first use until the process ends.  Host code never passes `scratch` itself
+// (in host code the name is a host-side stand-in, not a device address): it
+// passes the device address hipGetSymbolAddress returned for the current GPU,
+// looked up once per device with that device current.  Calls that overlap on
+// one GPU share this memory and race; calls on one stream do not overlap.
+// Every call writes the segment results it reads, so nothing must start at zero.
+// ---------------------------------------------------------------------------
+constexpr int64_t kNoAllocScratchBytes = int64_t(32) << 10;
+static_assert(kNoAllocScratchBytes >= 3 * 2 * kSplitTarget * int64_t(sizeof(float)),
+              "a split launch has fewer than 2 * kSplitTarget segments of 3 floats");
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices] = {nullptr};
+
+// The current GPU's copy of `scratch` (looked up on first use per device).
+static int noalloc_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, "noalloc scratch: hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(VBH_E_RANGE, "noalloc scratch: device %d beyond the %d the library tracks", dev,
+                kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_status(e, "noalloc scratch: hipGetSymbolAddress");
+    if (p == nullptr || (reinterpret_cast<uintptr_t>(p) & 255u) != 0)
+      return fail(VBH_E_INVALID, "noalloc scratch: symbol address %p not 256-byte aligned", p);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
 }  // namespace vbh
 
 using namespace vbh;
@@ -780,6 +821,31 @@ int vbh_cross_entropy_fwd(const void* logits, const void* labels, int logits_dty
                                   n_rows, n_cols, row_stride, smoothing, logit_scale,
                                   lse_square_scale, ignored_index, total_classes,
                                   class_start_idx, block_size, has_smoothing, split, nullptr, 0,
+                                  stream);
+}
+
+int vbh_cross_entropy_fwd_noalloc(const void* logits, const void* labels, int logits_dtype,
+                                  int label_dtype, void* loss, void* lse, void* z_loss,
+                                  int64_t n_rows, int64_t n_cols, int64_t row_stride,
+                                  float smoothing, float logit_scale, float lse_square_scale,
+                                  int64_t ignored_index, int64_t total_classes,
+                                  int64_t class_start_idx, int64_t block_size, int has_smoothing,
+                                  int split, void* stream) {
+  const int64_t need =
+      vbh_cross_entropy_workspace_bytes(n_rows, n_cols, block_size, logits_dtype);
+  if (need > kNoAllocScratchBytes)
+    return fail(VBH_E_RANGE,
+                "cross_entropy_fwd_noalloc: the row split needs %lld bytes of scratch, more than "
+                "the %lld bytes of the library's static scratch",
+                static_cast<long long>(need), static_cast<long long>(kNoAllocScratchBytes));
+  void* ws = nullptr;
+  if (need > 0) {
+    if (int rc = noalloc_scratch(&ws)) return rc;
+  }
+  return vbh_cross_entropy_fwd_ws(logits, labels, logits_dtype, label_dtype, loss, lse, z_loss,
+                                  n_rows, n_cols, row_stride, smoothing, logit_scale,
+                                  lse_square_scale, ignored_index, total_classes,
+                                  class_start_idx, block_size, has_smoothing, split, ws, need,
                                   stream);
 }
 

@@ -118,6 +118,10 @@ ENTRY(vbh_cross_entropy_fwd_ws, "ppiipppqqqfffqqqqiipqp",
       fn_vbh_cross_entropy_fwd_ws(P(0), P(1), I(2), I(3), P(4), P(5), P(6), Q(7), Q(8), Q(9),
                                   F(10), F(11), F(12), Q(13), Q(14), Q(15), Q(16), I(17), I(18),
                                   P(19), Q(20), P(21)))
+ENTRY(vbh_cross_entropy_fwd_noalloc, "ppiipppqqqfffqqqqiip",
+      fn_vbh_cross_entropy_fwd_noalloc(P(0), P(1), I(2), I(3), P(4), P(5), P(6), Q(7), Q(8), Q(9),
+                                       F(10), F(11), F(12), Q(13), Q(14), Q(15), Q(16), I(17),
+                                       I(18), P(19)))
 ENTRY(vbh_cross_entropy_bwd, "pppppiiqqqqqfffqqqip",
       fn_vbh_cross_entropy_bwd(P(0), P(1), P(2), P(3), P(4), I(5), I(6), Q(7), Q(8), Q(9), Q(10),
                             Q(11), F(12), F(13), F(14), Q(15), Q(16), Q(17), I(18), P(19)))
@@ -141,6 +145,7 @@ static const struct {
     SLOT(vbh_layer_norm_fwd),    SLOT(vbh_rms_norm_fwd),     SLOT(vbh_softmax_fwd),
     SLOT(vbh_softmax_dim_fwd),   SLOT(vbh_logsumexp_fwd),    SLOT(vbh_logsumexp_fwd_ws), SLOT(vbh_softmax_fwd_ws),
     SLOT(vbh_cross_entropy_fwd), SLOT(vbh_cross_entropy_fwd_ws), SLOT(vbh_cross_entropy_bwd),
+    SLOT(vbh_cross_entropy_fwd_noalloc),
     SLOT(vbh_reduce_fwd),
     SLOT(vbh_reduce_fwd_ws),     SLOT(vbh_stream_copy),      SLOT(vbh_stream_read),
 };
@@ -177,6 +182,7 @@ static PyMethodDef methods[] = {
     METHOD(vbh_layer_norm_fwd),    METHOD(vbh_rms_norm_fwd),      METHOD(vbh_softmax_fwd),
     METHOD(vbh_softmax_dim_fwd),   METHOD(vbh_logsumexp_fwd),     METHOD(vbh_logsumexp_fwd_ws), METHOD(vbh_softmax_fwd_ws),
     METHOD(vbh_cross_entropy_fwd), METHOD(vbh_cross_entropy_fwd_ws),
+    METHOD(vbh_cross_entropy_fwd_noalloc),
     METHOD(vbh_cross_entropy_bwd), METHOD(vbh_reduce_fwd),
     METHOD(vbh_reduce_fwd_ws),     METHOD(vbh_stream_copy),       METHOD(vbh_stream_read),
     {NULL, NULL, 0, NULL},

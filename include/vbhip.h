@@ -178,6 +178,26 @@ int vbh_cross_entropy_fwd_ws(const void* logits, const void* labels, int logits_
 int64_t vbh_cross_entropy_workspace_bytes(int64_t n_rows, int64_t n_cols, int64_t block_size,
                                           int logits_dtype);
 
+/* vbh_cross_entropy_fwd for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No reference counterpart: the reference's implementations
+ * allocate their outputs and temporaries through torch.  Same arguments and
+ * results as vbh_cross_entropy_fwd_ws with the split taken whenever it pays,
+ * but the split's segment results go to a static scratch buffer of the library
+ * (32 KiB per GPU, held from the first call on a GPU until the process ends),
+ * so the call allocates nothing.  A launch whose split would need more than
+ * that returns VBH_E_RANGE (none does under the current split rule: at most
+ * 24 KiB).  Every call on one GPU shares that GPU's scratch: calls that overlap
+ * on one GPU (different streams, or different host threads without ordering)
+ * race and must not be issued; calls on one stream are ordered and safe. */
+int vbh_cross_entropy_fwd_noalloc(const void* logits, const void* labels, int logits_dtype,
+                                  int label_dtype, void* loss, void* lse, void* z_loss,
+                                  int64_t n_rows, int64_t n_cols, int64_t row_stride,
+                                  float smoothing, float logit_scale, float lse_square_scale,
+                                  int64_t ignored_index, int64_t total_classes,
+                                  int64_t class_start_idx, int64_t block_size,
+                                  int has_smoothing, int split, void* stream);
+
 /* Cross-entropy backward: dlogits[r, c] = dloss[r] * logit_scale *
  * (p + 2 * lse_square_scale * lse[r] * p - target), p = exp(logit_scale * x - lse[r]).
  * dloss is read at dloss[r * dloss_stride]; ignored rows get dlogits = 0 * (...).
