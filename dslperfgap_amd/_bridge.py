@@ -94,7 +94,12 @@ def launch(name: str, idx: int, *args) -> None:
     current stream on device `idx` (every launching entry point takes the
     stream last), with that device current during the call; raise
     ``_lib.VbhError`` on a nonzero status."""
-    fn = _lib.entry(name)
+    launch_fn(_lib.entry(name), name, idx, *args)
+
+
+def launch_fn(fn, name: str, idx: int, *args) -> None:
+    """:func:`launch` with the bound entry point `fn` (``_lib.entry(name)``)
+    already looked up."""
     if idx == _raw_device():
         rc = fn(*args, _raw_stream(idx))
     else:

@@ -197,6 +197,11 @@ TUNE_PERSIST, TUNE_NO_PERSIST, TUNE_NONTEMPORAL, TUNE_TEMPORAL = 1, 2, 4, 8
 TUNE_WRITE_THROUGH, TUNE_NO_WRITE_THROUGH = 16, 32
 
 
+# caches of host-side plans that depend on the geometry (and so on
+# vbh_tune_override); modules that keep one append its lru_cache here
+GEOMETRY_CACHES: list = []
+
+
 def tune_override(op: int, tpr: int = 0, block: int = 0, flags: int = 0) -> None:
     """Force threads-per-row / workgroup size / kernel flags for one op
     (all zero restores the built-in heuristic)."""
@@ -206,6 +211,8 @@ def tune_override(op: int, tpr: int = 0, block: int = 0, flags: int = 0) -> None
     softmax_workspace_bytes.cache_clear()
     reduce_workspace_bytes.cache_clear()
     cross_entropy_workspace_bytes.cache_clear()
+    for cache in GEOMETRY_CACHES:
+        cache.cache_clear()
 
 
 @functools.lru_cache(maxsize=4096)

@@ -30,11 +30,13 @@ def norm_dims(dim, ndim: int, what: str) -> list[int]:
 
 
 @functools.lru_cache(maxsize=1024)
-def plan(shape: tuple, dims: tuple, keepdim: bool, zero_d: bool) -> tuple:
-    """(outer, n, inner, permutation or None, output shape, output strides) of
-    a reduction over the sorted `dims` of a tensor of `shape`.  Adjacent dims collapse into one
-    axis of the contiguous [outer, n, inner] view; otherwise the reduced dims are
-    moved last (one extra copy pass)."""
+def plan(shape: tuple, dims: tuple, keepdim: bool, zero_d: bool, idt: int, op: int) -> tuple:
+    """(outer, n, inner, permutation or None, output shape, output strides,
+    workspace bytes, entry point) of a reduction over the sorted `dims` of a
+    tensor of `shape`.  Adjacent dims collapse into one axis of the contiguous
+    [outer, n, inner] view; otherwise the reduced dims are moved last (one
+    extra copy pass).  A nonzero workspace size means the launch splits its
+    rows (``vbh_reduce_fwd_ws``)."""
     if dims[-1] - dims[0] == len(dims) - 1:
         outer = _bridge.numel_prod(shape[:dims[0]])
         n = _bridge.numel_prod(shape[dims[0]:dims[-1] + 1])
@@ -52,7 +54,14 @@ def plan(shape: tuple, dims: tuple, keepdim: bool, zero_d: bool) -> tuple:
         out_shape = tuple(1 if d in dims else s for d, s in enumerate(shape))
     else:
         out_shape = tuple(s for d, s in enumerate(shape) if d not in dims)
-    return outer, n, inner, perm, out_shape, _bridge.contiguous_strides(out_shape)
+    ws = _lib.reduce_workspace_bytes(outer, n, inner, idt, op) if outer * inner else 0
+    name = "vbh_reduce_fwd_ws" if ws else "vbh_reduce_fwd"
+    return (outer, n, inner, perm, out_shape, _bridge.contiguous_strides(out_shape), ws,
+            _lib.entry(name), name)
+
+
+# an overridden launch geometry changes the split decision
+_lib.GEOMETRY_CACHES.append(plan)
 
 
 def reduce(x: torch.Tensor, dims: list[int], keepdim: bool, op: int, out_dtype, what: str):
@@ -62,25 +71,28 @@ def reduce(x: torch.Tensor, dims: list[int], keepdim: bool, op: int, out_dtype, 
     odt = _bridge.FLOAT_CODES[out_dtype]
     zero_d = x.dim() == 0
     shape = (1,) if zero_d else tuple(x.shape)
-    outer, n, inner, perm, out_shape, out_strides = plan(shape, tuple(dims), bool(keepdim),
-                                                          zero_d)
+    outer, n, inner, perm, out_shape, out_strides, ws_bytes, fn, name = plan(
+        shape, tuple(dims), bool(keepdim), zero_d, idt, op)
     xc = x.reshape(shape) if zero_d else x
     if perm is not None:
         xc = xc.permute(perm)
     if not xc.is_contiguous():
         xc = xc.contiguous()
-    vals = None if op == _lib.REDUCE_ARGMAX else x.new_empty_strided(out_shape, out_strides,
-                                                                       dtype=out_dtype)
+    if op == _lib.REDUCE_ARGMAX:
+        vals = None
+    elif out_dtype is x.dtype:
+        vals = x.new_empty_strided(out_shape, out_strides)
+    else:
+        vals = x.new_empty_strided(out_shape, out_strides, dtype=out_dtype)
     idx = None if op == _lib.REDUCE_MEAN else x.new_empty_strided(out_shape, out_strides,
                                                                  dtype=torch.int64)
     if outer * inner == 0:
         return vals, idx
-    ws_bytes = _lib.reduce_workspace_bytes(outer, n, inner, idt, op)
     if ws_bytes:  # few long rows: split each row over several workgroups
         ws = _bridge.empty(x, (ws_bytes,), torch.uint8)
-        _bridge.launch("vbh_reduce_fwd_ws", dev, xc.data_ptr(), _bridge.ptr(vals),
-                       _bridge.ptr(idx), outer, n, inner, idt, odt, op, ws.data_ptr(), ws_bytes)
+        _bridge.launch_fn(fn, name, dev, xc.data_ptr(), _bridge.ptr(vals), _bridge.ptr(idx),
+                          outer, n, inner, idt, odt, op, ws.data_ptr(), ws_bytes)
     else:
-        _bridge.launch("vbh_reduce_fwd", dev, xc.data_ptr(), _bridge.ptr(vals), _bridge.ptr(idx),
-                       outer, n, inner, idt, odt, op)
+        _bridge.launch_fn(fn, name, dev, xc.data_ptr(), _bridge.ptr(vals), _bridge.ptr(idx),
+                          outer, n, inner, idt, odt, op)
     return vals, idx

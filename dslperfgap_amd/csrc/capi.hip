@@ -335,6 +335,54 @@ Geometry reduce_geometry(int64_t n, int vec, int64_t units) {
 
 }  // namespace
 
+// function_for's cache: per device, an open-addressing table from kernel
+// address to hipFunction_t.  Readers probe without a lock (a slot's function is
+// stored before its key, with release / acquire ordering); inserts take the mutex.
+namespace {
+constexpr int kFnDevices = 16;
+constexpr int kFnSlots = 2048;  // a power of two, well above the library's kernel count
+struct FnSlot {
+  std::atomic<const void*> key{nullptr};
+  std::atomic<hipFunction_t> fn{nullptr};
+};
+FnSlot g_fn[kFnDevices][kFnSlots];
+std::mutex g_fn_mu;
+
+inline uint64_t fn_hash(const void* k) {
+  return (static_cast<uint64_t>(reinterpret_cast<uintptr_t>(k)) >> 4) * 0x9E3779B97F4A7C15ull;
+}
+}  // namespace
+
+hipFunction_t function_for(const void* kernel) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kFnDevices) return nullptr;
+  FnSlot* table = g_fn[dev];
+  const uint64_t h = fn_hash(kernel);
+  for (int i = 0; i < kFnSlots; ++i) {
+    FnSlot& sl = table[(h + i) & (kFnSlots - 1)];
+    const void* k = sl.key.load(std::memory_order_acquire);
+    if (k == kernel) return sl.fn.load(std::memory_order_relaxed);
+    if (k == nullptr) break;
+  }
+  std::lock_guard<std::mutex> lock(g_fn_mu);
+  for (int i = 0; i < kFnSlots; ++i) {
+    FnSlot& sl = table[(h + i) & (kFnSlots - 1)];
+    const void* k = sl.key.load(std::memory_order_relaxed);
+    if (k == kernel) return sl.fn.load(std::memory_order_relaxed);
+    if (k == nullptr) {
+      hipFunction_t f = nullptr;
+      if (hipGetFuncBySymbol(&f, kernel) != hipSuccess || f == nullptr) {
+        (void)hipGetLastError();  // the fallback launch reports its own status
+        return nullptr;
+      }
+      sl.fn.store(f, std::memory_order_relaxed);
+      sl.key.store(kernel, std::memory_order_release);
+      return f;
+    }
+  }
+  return nullptr;  // table full: the runtime's own lookup
+}
+
 int64_t resident_blocks(const void* kernel, int block, int max_per_cu) {
   static std::mutex mu;
   static std::unordered_map<uint64_t, int> per_cu;  // (kernel, block) -> blocks per CU
@@ -390,6 +438,10 @@ Geometry pick_geometry(int64_t cols, int vec, int it_target, int tpr_override,
       }
     }
   }
+  // the store policy follows the op's flags whether or not the row streams
+  // (the streaming kernels ignore it; the split softmax's second stage, which
+  // takes its policy from the full row's geometry, does not)
+  g.nt = (flags & kFlagNontemporal) != 0;
   const int64_t it = tpr > 0 ? (nvec + tpr - 1) / tpr : cap + 1;
   if (it > cap) {
     g.stream = true;
@@ -405,7 +457,6 @@ Geometry pick_geometry(int64_t cols, int vec, int it_target, int tpr_override,
   else block = tpr < 128 ? 256 : tpr;
   g.block = block;
   g.persist = (flags & kFlagPersist) != 0 && g.maxit <= kPipeMaxIt;
-  g.nt = (flags & kFlagNontemporal) != 0;
   return g;
 }
 

@@ -424,7 +424,7 @@ hipError_t launch_cross_entropy_fwd(const CeArgs& a, const Geometry& g, hipStrea
     auto go = [&](auto vc) {
       constexpr int V = decltype(vc)::value;
       if (g.stream) {
-        hipLaunchKernelGGL((ce_fwd_stream<T, V>), dim3(nseg), dim3(g.block), 0, s,
+        launch_kernel((ce_fwd_stream<T, V>), dim3(nseg), dim3(g.block), 0, s,
                            static_cast<const T*>(a.logits), a.labels, a.label_i64, a.loss,
                            a.lse, a.z_loss, a.n_rows, a.n_cols, a.ld, a.block_size, a.ncb,
                            c);
@@ -435,7 +435,7 @@ hipError_t launch_cross_entropy_fwd(const CeArgs& a, const Geometry& g, hipStrea
         constexpr int M = decltype(mc)::value;
         if constexpr (M <= lane_cap(V)) {
           auto launch = [&](auto kern) {
-            hipLaunchKernelGGL(kern, dim3(grid_for(nseg, g)), dim3(g.block), 0, s,
+            launch_kernel(kern, dim3(grid_for(nseg, g)), dim3(g.block), 0, s,
                                static_cast<const T*>(a.logits), a.labels, a.label_i64, a.loss,
                                a.lse, a.z_loss, a.n_rows, a.n_cols, a.ld, a.block_size, a.ncb,
                                g.tpr, c);
@@ -458,7 +458,7 @@ hipError_t launch_cross_entropy_combine(const CeArgs& a, const float* seg_loss,
   const CeScalars c =
       make_scalars(a.smoothing, a.logit_scale, a.lse_square_scale, a.total_classes,
                    a.ignored_index, a.class_start, a.has_smoothing, a.split);
-  hipLaunchKernelGGL(ce_combine, dim3((a.n_rows + 255) / 256), dim3(256), 0, s, seg_loss,
+  launch_kernel(ce_combine, dim3((a.n_rows + 255) / 256), dim3(256), 0, s, seg_loss,
                      seg_lse, a.labels, a.label_i64, a.loss, a.lse, a.z_loss, a.n_rows,
                      a.n_cols, segs, c);
   return hipGetLastError();
@@ -482,7 +482,7 @@ hipError_t launch_cross_entropy_bwd(const CeBwdArgs& a, hipStream_t s) {
       dispatch_store_policy<V>(g, [&](auto sp) {
         constexpr int SP = decltype(sp)::value;
         auto launch = [&](auto kern) {
-          hipLaunchKernelGGL(kern, dim3(a.n_rows * tiles), dim3(kBwdLanes), 0, s, a.dloss,
+          launch_kernel(kern, dim3(a.n_rows * tiles), dim3(kBwdLanes), 0, s, a.dloss,
                              static_cast<const T*>(a.logits), a.lse, a.labels, a.label_i64,
                              static_cast<T*>(a.dlogits), a.n_cols, static_cast<uint32_t>(tiles),
                              a.ld_logits, a.ld_dlogits, a.dloss_stride, c);

@@ -276,7 +276,7 @@ hipError_t launch_reduce(const void* x, void* vals, int64_t* idx, int64_t outer,
       constexpr int OP = decltype(opc)::value;
       if (inner == 1) {
         auto launch = [&](auto kern) {
-          hipLaunchKernelGGL(kern, dim3(grid_for(outer, g)), dim3(g.block), 0, s,
+          launch_kernel(kern, dim3(grid_for(outer, g)), dim3(g.block), 0, s,
                              static_cast<const Ti*>(x), vals, idx, outer, n, g.tpr);
         };
         if (g.v == 1) launch(reduce_rows<Ti, To, 1, OP, false>);
@@ -284,7 +284,7 @@ hipError_t launch_reduce(const void* x, void* vals, int64_t* idx, int64_t outer,
         else launch(reduce_rows<Ti, To, VN, OP, false>);
       } else {
         const int64_t cols = outer * inner;
-        hipLaunchKernelGGL((reduce_cols<Ti, To, OP>), dim3((cols + 255) / 256), dim3(256), 0, s,
+        launch_kernel((reduce_cols<Ti, To, OP>), dim3((cols + 255) / 256), dim3(256), 0, s,
                            static_cast<const Ti*>(x), vals, idx, outer, n, inner);
       }
       err = hipGetLastError();
@@ -312,10 +312,10 @@ hipError_t launch_reduce_combine(const void* pvals, const int64_t* pidx, void* v
   dispatch_float_type(dt, [&](auto t) {
     using T = typename decltype(t)::type;
     if (op == 1)
-      hipLaunchKernelGGL((reduce_combine_vi<T, 1>), dim3(grid), dim3(256), 0, s,
+      launch_kernel((reduce_combine_vi<T, 1>), dim3(grid), dim3(256), 0, s,
                          static_cast<const T*>(pvals), pidx, vals, idx, rows, segs, segn);
     else
-      hipLaunchKernelGGL((reduce_combine_vi<T, 2>), dim3(grid), dim3(256), 0, s,
+      launch_kernel((reduce_combine_vi<T, 2>), dim3(grid), dim3(256), 0, s,
                          static_cast<const T*>(pvals), pidx, vals, idx, rows, segs, segn);
     err = hipGetLastError();
   });

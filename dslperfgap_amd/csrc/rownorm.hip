@@ -675,7 +675,7 @@ hipError_t launch_layer_norm(const void* x, const void* w, const void* b, void* 
       auto go = [&](auto vc) {
         constexpr int V = decltype(vc)::value;
         if (g.stream) {
-          hipLaunchKernelGGL((layer_norm_stream<T, TW, V>), dim3(rows), dim3(g.block), 0, s,
+          launch_kernel((layer_norm_stream<T, TW, V>), dim3(rows), dim3(g.block), 0, s,
                              static_cast<const T*>(x), static_cast<const TW*>(w),
                              static_cast<const TW*>(b), static_cast<T*>(y), cols, eps);
           err = hipGetLastError();
@@ -688,7 +688,7 @@ hipError_t launch_layer_norm(const void* x, const void* w, const void* b, void* 
               constexpr int SP = decltype(sp)::value;
               if constexpr (V > 1) {
                 if (g.mis) {
-                  hipLaunchKernelGGL((norm_rows_mis<T, TW, V, M, SP, false>),
+                  launch_kernel((norm_rows_mis<T, TW, V, M, SP, false>),
                                      dim3(grid_for(rows, g)), dim3(g.block), 0, s,
                                      static_cast<const T*>(x), static_cast<const TW*>(w),
                                      static_cast<const TW*>(b), static_cast<T*>(y), rows, cols,
@@ -705,7 +705,7 @@ hipError_t launch_layer_norm(const void* x, const void* w, const void* b, void* 
               err = launch_rows_or_pipe(
                   layer_norm_rows<T, TW, V, M, SP>, pipe_k,
                   g.persist && M <= PC, rows, g, [&](auto kern, int64_t grid) {
-                    hipLaunchKernelGGL(kern, dim3(grid), dim3(g.block), 0, s,
+                    launch_kernel(kern, dim3(grid), dim3(g.block), 0, s,
                                        static_cast<const T*>(x), static_cast<const TW*>(w),
                                        static_cast<const TW*>(b), static_cast<T*>(y), rows,
                                        cols, g.tpr, eps);
@@ -732,7 +732,7 @@ hipError_t launch_rms_norm(const void* x, const void* w, void* y, int64_t rows, 
       auto go = [&](auto vc) {
         constexpr int V = decltype(vc)::value;
         if (g.stream) {
-          hipLaunchKernelGGL((rms_norm_stream<T, TW, V>), dim3(rows), dim3(g.block), 0, s,
+          launch_kernel((rms_norm_stream<T, TW, V>), dim3(rows), dim3(g.block), 0, s,
                              static_cast<const T*>(x), static_cast<const TW*>(w),
                              static_cast<T*>(y), cols, eps);
           err = hipGetLastError();
@@ -745,7 +745,7 @@ hipError_t launch_rms_norm(const void* x, const void* w, void* y, int64_t rows, 
               constexpr int SP = decltype(sp)::value;
               if constexpr (V > 1) {
                 if (g.mis) {
-                  hipLaunchKernelGGL((norm_rows_mis<T, TW, V, M, SP, true>),
+                  launch_kernel((norm_rows_mis<T, TW, V, M, SP, true>),
                                      dim3(grid_for(rows, g)), dim3(g.block), 0, s,
                                      static_cast<const T*>(x), static_cast<const TW*>(w),
                                      static_cast<const TW*>(nullptr), static_cast<T*>(y), rows,
@@ -762,7 +762,7 @@ hipError_t launch_rms_norm(const void* x, const void* w, void* y, int64_t rows, 
               err = launch_rows_or_pipe(
                   rms_norm_rows<T, TW, V, M, SP>, pipe_k,
                   g.persist && M <= PC, rows, g, [&](auto kern, int64_t grid) {
-                    hipLaunchKernelGGL(kern, dim3(grid), dim3(g.block), 0, s,
+                    launch_kernel(kern, dim3(grid), dim3(g.block), 0, s,
                                        static_cast<const T*>(x), static_cast<const TW*>(w),
                                        static_cast<T*>(y), rows, cols, g.tpr, eps);
                   }, static_cast<int64_t>(cols) * sizeof(T));

@@ -423,7 +423,7 @@ hipError_t launch_softmax(const void* x, void* y, int64_t rows, int cols, int id
       constexpr int V = decltype(vc)::value;
       constexpr bool LOG = decltype(lc)::value;
       if (g.stream) {
-        hipLaunchKernelGGL((softmax_stream<Ti, To, V, LOG>), dim3(rows), dim3(g.block), 0, s,
+        launch_kernel((softmax_stream<Ti, To, V, LOG>), dim3(rows), dim3(g.block), 0, s,
                            static_cast<const Ti*>(x), static_cast<To*>(y), cols);
         err = hipGetLastError();
         return;
@@ -434,12 +434,12 @@ hipError_t launch_softmax(const void* x, void* y, int64_t rows, int cols, int id
           dispatch_store_policy<V>(g, [&](auto sp) {
             constexpr int SP = decltype(sp)::value;
             if (V > 1 && g.mis)
-              hipLaunchKernelGGL((softmax_rows<Ti, To, V, M, LOG, SP, V != 1>),
+              launch_kernel((softmax_rows<Ti, To, V, M, LOG, SP, V != 1>),
                                  dim3(grid_for(rows, g)), dim3(g.block), 0, s,
                                  static_cast<const Ti*>(x), static_cast<To*>(y), rows, cols,
                                  g.tpr);
             else
-              hipLaunchKernelGGL((softmax_rows<Ti, To, V, M, LOG, SP, false>),
+              launch_kernel((softmax_rows<Ti, To, V, M, LOG, SP, false>),
                                  dim3(grid_for(rows, g)), dim3(g.block), 0, s,
                                  static_cast<const Ti*>(x), static_cast<To*>(y), rows, cols,
                                  g.tpr);
@@ -468,7 +468,7 @@ hipError_t launch_logsumexp(const void* x, void* y, int64_t rows, int cols, int 
     auto go = [&](auto vc) {
       constexpr int V = decltype(vc)::value;
       if (g.stream) {
-        hipLaunchKernelGGL((logsumexp_stream<Ti, To, V>), dim3(rows), dim3(g.block), 0, s,
+        launch_kernel((logsumexp_stream<Ti, To, V>), dim3(rows), dim3(g.block), 0, s,
                            static_cast<const Ti*>(x), static_cast<To*>(y), cols);
         err = hipGetLastError();
         return;
@@ -477,7 +477,7 @@ hipError_t launch_logsumexp(const void* x, void* y, int64_t rows, int cols, int 
         constexpr int M = decltype(mc)::value;
         if constexpr (M <= lane_cap(V)) {
           auto launch = [&](auto kern) {
-            hipLaunchKernelGGL(kern, dim3(grid_for(rows, g)), dim3(g.block), 0, s,
+            launch_kernel(kern, dim3(grid_for(rows, g)), dim3(g.block), 0, s,
                                static_cast<const Ti*>(x), static_cast<To*>(y), rows, cols,
                                g.tpr, segs, seg_cols);
           };
@@ -510,7 +510,7 @@ hipError_t launch_softmax_apply(const void* x, void* y, const float* seg_lse, in
     dispatch_store_policy<V>(g, [&](auto sp) {
       constexpr int SP = decltype(sp)::value;
       auto launch = [&](auto kern) {
-        hipLaunchKernelGGL(kern, dim3(rows * tiles), dim3(kApplyLanes), 0, s,
+        launch_kernel(kern, dim3(rows * tiles), dim3(kApplyLanes), 0, s,
                            static_cast<const Ti*>(x), static_cast<To*>(y), seg_lse, cols, segs,
                            static_cast<uint32_t>(tiles));
       };
@@ -537,10 +537,10 @@ hipError_t launch_softmax_dim(const void* x, void* y, int64_t outer, int n, int6
     using Ti = typename decltype(ti)::type;
     using To = typename decltype(to)::type;
     if (log_mode)
-      hipLaunchKernelGGL((softmax_mid<Ti, To, true>), dim3(grid), dim3(block), 0, s,
+      launch_kernel((softmax_mid<Ti, To, true>), dim3(grid), dim3(block), 0, s,
                          static_cast<const Ti*>(x), static_cast<To*>(y), outer, n, inner);
     else
-      hipLaunchKernelGGL((softmax_mid<Ti, To, false>), dim3(grid), dim3(block), 0, s,
+      launch_kernel((softmax_mid<Ti, To, false>), dim3(grid), dim3(block), 0, s,
                          static_cast<const Ti*>(x), static_cast<To*>(y), outer, n, inner);
     err = hipGetLastError();
   });

@@ -77,7 +77,7 @@ int64_t stream_read_tiles(int64_t bytes) {
 
 hipError_t launch_stream_read(const void* src, void* partial, int64_t bytes, hipStream_t s) {
   const int64_t n = bytes / 16;
-  hipLaunchKernelGGL(read_kernel<kReadUnroll>, dim3(stream_read_tiles(bytes)), dim3(kReadBlock),
+  launch_kernel(read_kernel<kReadUnroll>, dim3(stream_read_tiles(bytes)), dim3(kReadBlock),
                      0, s, static_cast<const u32x4*>(src), static_cast<uint32_t*>(partial), n);
   return hipGetLastError();
 }
@@ -86,7 +86,7 @@ hipError_t launch_stream_copy(const void* src, void* dst, int64_t bytes, hipStre
   const int64_t n = bytes / 16;
   const int block = 256;
   const int64_t grid = (n + block - 1) / block;
-  hipLaunchKernelGGL(copy_kernel, dim3(grid), dim3(block), 0, s,
+  launch_kernel(copy_kernel, dim3(grid), dim3(block), 0, s,
                      static_cast<const u32x4*>(src), static_cast<u32x4*>(dst), n);
   return hipGetLastError();
 }

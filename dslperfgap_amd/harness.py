@@ -55,6 +55,18 @@ def select_peak(device_name: str):
     return None, f"no peak-table entry for '{device_name}'"
 
 
+# kernels that write almost nothing: quoted against the measured streaming-read
+# rate; every other kernel reads and writes about as much and is quoted against
+# the measured copy rate
+READ_DOMINATED = frozenset({"logsumexp", "cross_entropy", "argmax", "max_reduction",
+                            "mean_reduction"})
+
+
+def peak_kind(kernel: str) -> str:
+    """"read" or "copy": the measured yardstick of a kernel."""
+    return "read" if kernel in READ_DOMINATED else "copy"
+
+
 def essential_work(kernel: str, inputs) -> int:
     """Algorithmic HBM bytes of one call: every input read once, every output written once."""
     el = lambda t: t.element_size() * t.numel()  # noqa: E731

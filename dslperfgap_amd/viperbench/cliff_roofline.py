@@ -19,11 +19,14 @@ with logsumexp and cross_entropy byte models that the reference lacks
 (exp_cliff_roofline.py:263).
 
 The reference protocol reuses one input set, so a working set under the 256 MB
-Infinity Cache is partly served from it.  Three columns are appended: the
+Infinity Cache is partly served from it.  Four columns are appended: the
 median device time with inputs cycled through >= 2 GiB of HBM copies
 (``t_opt_hbm_ms``), the roofline fraction from it (``roofline_frac_opt_hbm``),
-and the same achieved rate as a fraction of the stream-copy rate measured at
-the start of the run (``frac_of_measured_copy_hbm``; 4 GiB copy, read + write).
+the measured yardstick of the kernel (``measured_peak``: the 4 GiB stream copy,
+read + write, for kernels that read and write about as much; the 4 GiB
+streaming read for logsumexp, cross entropy and mean / max / argmax, which
+write almost nothing), and the achieved rate as a fraction of it
+(``frac_of_measured_peak_hbm``).
 
     python -m dslperfgap_amd.viperbench.cliff_roofline [--kernels a,b] [--out PATH]
 """
@@ -47,7 +50,7 @@ RESULTS = Path(__file__).resolve().parent / "results"
 FIELDS = ["kernel", "dsl", "dtype", "shape", "t_lib_ms", "t_naive_ms", "t_opt_ms",
           "E_lib_naive", "E_lib_opt", "cliff", "roofline_bound_type", "roofline_peak_assumed",
           "roofline_frac_opt", "note", "t_opt_hbm_ms", "roofline_frac_opt_hbm",
-          "frac_of_measured_copy_hbm"]
+          "measured_peak", "frac_of_measured_peak_hbm"]
 META = ["gpu_name", "sm", "timestamp_utc"]
 
 
@@ -121,8 +124,11 @@ def time_ref_protocol(fn, args, warmup: int = 15, reps: int = 50) -> float:
 
 
 def make_row(kernel: str, t_lib: float | None, t_opt: float, t_hbm: float | None,
-             work: int, peak: float, peak_note: str, copy_peak: float | None = None) -> dict:
-    """One cliff_roofline row (times in ms, work in bytes, peak in bytes/s)."""
+             work: int, peak: float, peak_note: str, peaks: dict | None = None) -> dict:
+    """One cliff_roofline row (times in ms, work in bytes, peak in bytes/s;
+    `peaks`: the measured {"copy": ..., "read": ...} rates in bytes/s)."""
+    kind = harness.peak_kind(kernel)
+    measured = peaks.get(kind) if peaks else None
     _fn, dtype, shape, _make, lines = ENTRIES[kernel]
     frac = work / (t_opt * 1e-3) / peak
     note = (f"hip_impl (gfx950 HIP); shape from AKO4ALL/prepare_kernel.py:{lines}; no naive "
@@ -137,8 +143,9 @@ def make_row(kernel: str, t_lib: float | None, t_opt: float, t_hbm: float | None
         "roofline_frac_opt": round(frac, 4), "note": note,
         "t_opt_hbm_ms": round(t_hbm, 5) if t_hbm else "",
         "roofline_frac_opt_hbm": round(work / (t_hbm * 1e-3) / peak, 4) if t_hbm else "",
-        "frac_of_measured_copy_hbm":
-            round(work / (t_hbm * 1e-3) / copy_peak, 4) if t_hbm and copy_peak else "",
+        "measured_peak": f"{kind} {measured / 1e9:.1f} GB/s" if measured else "",
+        "frac_of_measured_peak_hbm":
+            round(work / (t_hbm * 1e-3) / measured, 4) if t_hbm and measured else "",
     }
 
 
@@ -167,11 +174,12 @@ def main(argv=None) -> int:
         print(peak_note, file=sys.stderr)
         return 2
     kernels = args.kernels.split(",") if args.kernels else list(ENTRIES)
-    copy_peak = harness.copy_peak("cuda:0")
-    print(f"measured stream-copy rate: {copy_peak / 1e9:.1f} GB/s", flush=True)
+    peaks = {"copy": harness.copy_peak("cuda:0"), "read": harness.read_peak("cuda:0")}
+    print(f"measured stream-copy rate: {peaks['copy'] / 1e9:.1f} GB/s, streaming read: "
+          f"{peaks['read'] / 1e9:.1f} GB/s", flush=True)
     rows = []
     print(f"{'kernel':<15}{'dtype':<6}{'t_lib':>10}{'t_opt':>10}{'E_lib_opt':>10}"
-          f"{'roof_opt':>10}{'t_hbm':>10}{'roof_hbm':>10}{'of_copy':>9}", flush=True)
+          f"{'roof_opt':>10}{'t_hbm':>10}{'roof_hbm':>10}{'of_meas':>9}", flush=True)
     for kernel in kernels:
         fn_name, dtype, _shape, make, _lines = ENTRIES[kernel]
         cpu_args = make()
@@ -184,11 +192,11 @@ def main(argv=None) -> int:
         del dev
         torch.cuda.empty_cache()
         t_hbm = device_time_us(hip, cpu_args, work) * 1e-3
-        row = make_row(kernel, t_lib, t_opt, t_hbm, work, peak, peak_note, copy_peak)
+        row = make_row(kernel, t_lib, t_opt, t_hbm, work, peak, peak_note, peaks)
         rows.append(row)
         print(f"{kernel:<15}{dtype:<6}{t_lib:>10.4f}{t_opt:>10.4f}{row['E_lib_opt']:>10}"
               f"{row['roofline_frac_opt']:>10}{t_hbm:>10.4f}{row['roofline_frac_opt_hbm']:>10}"
-              f"{row['frac_of_measured_copy_hbm']:>9}",
+              f"{row['frac_of_measured_peak_hbm']:>9}",
               flush=True)
     out = Path(args.out) if args.out else RESULTS / device_slug(meta["gpu_name"], meta["sm"]) / \
         "cliff_roofline.csv"
