@@ -112,6 +112,14 @@ int it_target(int op, int64_t nvec, int vec) {
   // 896 vectors 2 per lane loses 1-8%, from 1664 vectors on 13 or more waves
   // per row lose 6%)
   if (op == VBH_OP_LAYER_NORM && vec == 8 && nvec > 1024 && nvec <= 1536) return 2;
+  // fp32 LayerNorm rows of 128 or 256 vectors (512 / 1024 columns): 2 vectors
+  // per lane, so 1024 columns take a 2-wave row group, persistent in 512-lane
+  // workgroups (below).  MI355X, 4 -> 2 per lane: 1024 columns 4575 -> 4720
+  // GB/s at 33.6 MB per call (C1), 5282 -> 5497 at 134 MB; 512 columns +1 to
+  // +2%.  Rows that do not fill whole 2-vector lanes lose (768 columns -1 to -6%).
+  if (op == VBH_OP_LAYER_NORM && vec == 4 && nvec > kWave && nvec <= 256 &&
+      (nvec & (nvec - 1)) == 0)
+    return 2;
   if (vec > 1) {
     if (op == VBH_OP_CROSS_ENTROPY) return 8;
     if (op == VBH_OP_LOGSUMEXP && nvec > kMidRowVecs) return 8;
@@ -264,6 +272,12 @@ Geometry geometry_for(int op, int64_t cols, int vec, int64_t units, int64_t out_
   Geometry g = pick_geometry(cols, vec, fill_it(it_target(op, nvec, vec), nvec, units),
                              g_tpr[op].load(), g_block[op].load(), flags);
   if (g.persist && !(over & kFlagPersist) && g.tpr < kPersistMinTpr[op]) g.persist = false;
+  // LayerNorm row groups of exactly 2 waves run 4 to a 512-lane workgroup
+  // instead of one per 128-lane workgroup.  MI355X, persistent kernel, default
+  // -> 512 lanes: fp32 2048 columns 5314 -> 5558 GB/s at 134 MB per call, bf16
+  // 4096 5207 -> 5303, fp32 1536 4161 -> 4414 at 33.6 MB (5416 -> 5386 at 134 MB).
+  if (op == VBH_OP_LAYER_NORM && !g.stream && g.tpr == 2 * kWave && g_block[op].load() <= 0)
+    g.block = 8 * kWave;
   const bool full_output =
       op == VBH_OP_LAYER_NORM || op == VBH_OP_RMS_NORM || op == VBH_OP_SOFTMAX;
   bool wt = full_output && write_through_ok(out_bytes, units);
