@@ -54,7 +54,8 @@ COPY_KIB_EACH_WAY = (4 << 30) // 1024
 # The row kernels carry their output store policy as an int template argument
 # (0 cached, 1 nontemporal, 2 write-through), matched as any digit.
 CONFIG_KERNELS = [
-    ("C1_layer_norm", r"layer_norm_rows<float, float, 4, 4, \d>|layer_norm_rowsIffLi4ELi4ELi\dE"),
+    ("C1_layer_norm", r"layer_norm_pipe<float, float, 4, 2, \d, false>|"
+                      r"layer_norm_pipeIffLi4ELi2ELi\dELb0E"),
     ("C2_rms_norm", r"rms_norm_rowsIDF16bDF16bLi8ELi2ELi\dE"),
     ("C3_log_softmax", r"softmax_rows<float, float, 4, 2, true, \d(, false)?>"),
     ("C3_softmax", r"softmax_rows<float, float, 4, 2, false, \d(, false)?>"),

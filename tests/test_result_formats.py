@@ -15,6 +15,8 @@ from pathlib import Path
 
 import pytest
 
+from dslperfgap_amd import harness
+
 from dslperfgap_amd.viperbench import benchmark, cliff_roofline, elib
 
 RESULTS = Path(__file__).resolve().parents[1] / "dslperfgap_amd" / "viperbench" / "results"
@@ -81,6 +83,16 @@ def test_committed_elib_agrees_with_committed_profile():
         assert got[key] == pytest.approx(e, abs=0.006), key
 
 
+def test_cliff_row_uses_the_kernels_measured_yardstick():
+    peaks = {"copy": 6.6e12, "read": 7.0e12}
+    r = cliff_roofline.make_row("logsumexp", 0.5, 0.1, 0.1, 5e8, 8.0e12, "n", peaks)
+    assert r["measured_peak"] == "read 7000.0 GB/s"
+    assert r["frac_of_measured_peak_hbm"] == pytest.approx(5e8 / 1e-4 / 7.0e12, abs=1e-4)
+    r = cliff_roofline.make_row("softmax", 0.5, 0.1, 0.1, 5e8, 8.0e12, "n", peaks)
+    assert r["measured_peak"] == "copy 6600.0 GB/s"
+    assert harness.peak_kind("cross_entropy") == "read" and harness.peak_kind("rms_norm") == "copy"
+
+
 def test_cliff_row_format(tmp_path):
     row = cliff_roofline.make_row("rms_norm", 0.5, 0.05, 0.06, 268_451_840, 8.0e12, "n")
     assert list(row)[:14] == CLIFF_COLUMNS
@@ -126,6 +138,14 @@ def test_committed_cliff_table_is_consistent():
         work = int(r["note"].split("essential bytes ")[1].split(";")[0])
         assert float(r["roofline_frac_opt"]) == pytest.approx(work / (t_opt * 1e-3) / 8e12,
                                                               abs=2e-4)
+        # the measured yardstick fits the kernel: the streaming read for the
+        # read-dominated kernels, the copy otherwise; no fraction exceeds it
+        kind, rate = r["measured_peak"].split()[:2]
+        assert kind == harness.peak_kind(r["kernel"]), r["kernel"]
+        t_hbm = float(r["t_opt_hbm_ms"])
+        frac = float(r["frac_of_measured_peak_hbm"])
+        assert frac == pytest.approx(work / (t_hbm * 1e-3) / (float(rate) * 1e9), rel=2e-3)
+        assert 0 < frac <= 1.0, (r["kernel"], frac)
 
 
 def test_committed_width_scan_is_complete():

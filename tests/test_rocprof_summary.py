@@ -71,8 +71,9 @@ def test_trace_and_traffic_arithmetic(tmp_path):
 
 # a symbol of every config's kernel as rocprofv3 printed them
 CONFIG_SYMBOLS = {
-    "C1_layer_norm": "void vbh::(anonymous namespace)::layer_norm_rows<float, float, 4, 4, 1>"
-                     "(float const*, float const*, float const*, float*, long, int, int, float)",
+    "C1_layer_norm": "void vbh::(anonymous namespace)::layer_norm_pipe<float, float, 4, 2, 1, "
+                     "false>(float const*, float const*, float const*, float*, long, int, int, "
+                     "float)",
     "C3_log_softmax": "void vbh::(anonymous namespace)::softmax_rows<float, float, 4, 2, true, "
                       "2, false>(float const*, float*, long, int, int)",
     "C3_softmax": "void vbh::(anonymous namespace)::softmax_rows<float, float, 4, 2, false, 2, "
