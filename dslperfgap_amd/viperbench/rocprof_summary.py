@@ -48,6 +48,9 @@ from dslperfgap_amd.workloads import WORKLOADS
 
 COPY = "stream_copy_4GiB"
 COPY_BYTES = 2 * (4 << 30)         # read + written by one 4 GiB copy dispatch
+READ = "stream_read_4GiB"
+READ_BYTES = 4 << 30               # read by one 4 GiB streaming-read dispatch
+YARDSTICKS = (COPY, READ)
 COPY_KIB_EACH_WAY = (4 << 30) // 1024
 
 # workload -> symbol patterns (demangled or mangled; rocprofv3 prints either).
@@ -64,6 +67,7 @@ CONFIG_KERNELS = [
     ("C4_cross_entropy_bwd", r"ce_bwd_tiles<float, 4, \d(, false)?>|ce_bwd_tilesIfLi4ELi\dE"),
     ("C5_layer_norm", r"layer_norm_pipeIDF16bDF16bLi8ELi4ELi\dELb1E"),
     (COPY, r"copy_kernel\("),
+    (READ, r"read_kernel<|read_kernelILi"),
 ]
 REFERENCE_KERNELS = [
     ("layer_norm", r"layer_norm_pipeIDF16bDF16bLi8ELi4ELi\dELb1E"),
@@ -76,6 +80,7 @@ REFERENCE_KERNELS = [
     ("max_reduction", r"reduce_rowsIDF16_DF16_Li8ELi1E"),
     ("mean_reduction", r"reduce_rows<float, float, 4, 0(, false)?>"),
     (COPY, r"copy_kernel\("),
+    (READ, r"read_kernel<|read_kernelILi"),
 ]
 
 
@@ -101,12 +106,14 @@ def reference_bytes() -> dict:
         "max_reduction": ew("max_reduction", [_meta(wide, hf), 1]),
         "mean_reduction": ew("mean_reduction", [_meta(wide), 1]),
         COPY: COPY_BYTES,
+        READ: READ_BYTES,
     }
 
 
 def config_bytes() -> dict:
     out = {k: w.bytes_per_launch for k, w in WORKLOADS.items()}
     out[COPY] = COPY_BYTES
+    out[READ] = READ_BYTES
     return out
 
 
@@ -148,17 +155,32 @@ def read_counter(path, kernels, tail: int = 0) -> dict:
     return out
 
 
+def peak_kind_of(key: str) -> str:
+    """The measured yardstick of a workload or reference kernel: "read" for the
+    kernels that write almost nothing, else "copy" (the yardsticks themselves
+    are measured against their own kind)."""
+    if key == READ:
+        return "read"
+    if key == COPY:
+        return "copy"
+    if key in WORKLOADS:
+        return WORKLOADS[key].peak_kind
+    return harness.peak_kind(key)
+
+
 def trace_table(stats: dict, alg: dict, order) -> list[dict]:
-    copy_rate = alg[COPY] / stats[COPY][2] if COPY in stats else None
+    rates = {kind: alg[y] / stats[y][2] for kind, y in (("copy", COPY), ("read", READ))
+             if y in stats}
     rows = []
     for key in order:
         if key not in stats:
             continue
         name, calls, avg, mn, mx = stats[key]
         gbs = alg[key] / avg
+        kind = peak_kind_of(key)
         rows.append(dict(workload=key, kernel=name, calls=calls, avg_ns=avg, min_ns=mn,
-                         max_ns=mx, alg_bytes=alg[key], gbps=gbs,
-                         of_copy=gbs / copy_rate if copy_rate else float("nan")))
+                         max_ns=mx, alg_bytes=alg[key], gbps=gbs, peak=kind,
+                         of_peak=gbs / rates[kind] if kind in rates else float("nan")))
     return rows
 
 
@@ -180,11 +202,11 @@ def traffic_table(fetch: dict, write: dict, alg: dict, order):
 
 def format_trace(rows) -> str:
     out = [f"{'workload':<18}{'calls':>7}{'avg_ns':>11}{'min_ns':>9}{'max_ns':>9}{'alg_bytes':>12}"
-           f"{'GB/s':>8}{'of_copy':>8}  kernel"]
+           f"{'GB/s':>8}{'peak':>6}{'of_peak':>8}  kernel"]
     for r in rows:
         out.append(f"{r['workload']:<18}{r['calls']:>7}{r['avg_ns']:>11.0f}{r['min_ns']:>9.0f}"
-                   f"{r['max_ns']:>9.0f}{r['alg_bytes']:>12}{r['gbps']:>8.0f}{r['of_copy']:>8.3f}"
-                   f"  {r['kernel'][:100]}")
+                   f"{r['max_ns']:>9.0f}{r['alg_bytes']:>12}{r['gbps']:>8.0f}{r['peak']:>6}"
+                   f"{r['of_peak']:>8.3f}  {r['kernel'][:100]}")
     return "\n".join(out) + "\n"
 
 
@@ -204,7 +226,7 @@ def format_traffic(rows, fs, ws, machine_lines: bool) -> str:
         out += ["", "Machine-readable (bench.py reads these lines):"]
         out += [f"TRAFFIC {r['workload']} bytes_per_launch={r['traffic']:.0f} "
                 f"fetch_kib={r['fetch_kib']:.1f} write_kib={r['write_kib']:.1f}"
-                for r in rows if r["workload"] != COPY]
+                for r in rows if r["workload"] not in YARDSTICKS]
     return "\n".join(out) + "\n"
 
 
@@ -249,7 +271,8 @@ def render(preset: str, trace, fetch, write, tail: int = 0) -> tuple[str, str]:
     fetched, written = read_counter(fetch, kernels, tail), read_counter(write, kernels, tail)
     # a renamed kernel template must not drop a workload from the summaries
     # (bench.py reads the traffic lines)
-    missing = [k for k in order if k not in stats or k not in fetched or k not in written]
+    missing = [k for k in order if k != READ and
+               (k not in stats or k not in fetched or k not in written)]
     if missing:
         raise ValueError(f"{preset}: no kernel in the rocprofv3 files matched {missing}; "
                          "update the symbol patterns")
@@ -263,8 +286,10 @@ def render(preset: str, trace, fetch, write, tail: int = 0) -> tuple[str, str]:
             f"      {cmd}\n"
             f"Summary: python -m dslperfgap_amd.viperbench.rocprof_summary {preset} ...\n\n"
             f"{p['source_note']}\n"
-            f"achieved = algorithmic bytes / AverageNs (ns); of_copy = achieved / the 4 GiB copy\n"
-            f"kernel's rate in the same run.\n\n")
+            f"achieved = algorithmic bytes / AverageNs (ns); of_peak = achieved / the rate of the\n"
+            f"kernel's measured yardstick in the same run (peak: copy = the 4 GiB stream copy,\n"
+            f"read + write; read = the 4 GiB streaming read, for the kernels that write almost\n"
+            f"nothing).\n\n")
     trace_txt = head + format_trace(tr)
     rows, fs, ws = traffic_table(fetched, written, alg, order)
     pmc = []
@@ -424,9 +449,10 @@ def render_timed(kernel_trace, markers, bench_lines) -> tuple[str, dict]:
     for k in keys:
         b = lines.get(k)
         if b:
+            of = (f", of measured {b['measured_peak_kind']} peak {b['frac_of_measured_peak']}"
+                  if "measured_peak_kind" in b else "")
             bench.append(f"  {k}: {b['value']} GB/s, {b['latency_us']} us, "
-                         f"frac {b['roofline']['frac']}, of measured {b['measured_peak_kind']} "
-                         f"peak {b['frac_of_measured_peak']}")
+                         f"frac {b['roofline']['frac']}{of}")
     combined = "\n".join(head + table + kernels + bench) + "\n"
     per = {}
     for r in rows:

@@ -2,8 +2,9 @@
 dslperfgap_amd/viperbench/rocprof_summary.py on small synthetic CSV files in
 rocprofv3's column layout, and the committed summaries that bench.py reads.
 
-* achieved GB/s = algorithmic bytes / AverageNs, of_copy against the 4 GiB copy
-  kernel of the same run;
+* achieved GB/s = algorithmic bytes / AverageNs, of_peak against the kernel's
+  measured yardstick of the same run (the 4 GiB copy, or the 4 GiB streaming
+  read for the kernels that write almost nothing);
 * traffic = (FETCH_SIZE * fetch scale + WRITE_SIZE * write scale) * 1024 with
   the scales set by what the counters read for the copy kernel (4 GiB each way);
 * the headers name the directories and prefixes the inputs came from;
@@ -59,7 +60,8 @@ def test_trace_and_traffic_arithmetic(tmp_path):
     assert set(tr) == {"C2_rms_norm", rs.COPY}
     c2 = tr["C2_rms_norm"]
     assert c2["gbps"] == pytest.approx(134_225_920 / 24000)
-    assert c2["of_copy"] == pytest.approx((134_225_920 / 24000) / (8 * 2**30 / 1_300_000))
+    assert c2["peak"] == "copy"
+    assert c2["of_peak"] == pytest.approx((134_225_920 / 24000) / (8 * 2**30 / 1_300_000))
     rows, fs, ws = rs.traffic_table(rs.read_counter(fetch, rs.CONFIG_KERNELS),
                                     rs.read_counter(write, rs.CONFIG_KERNELS), alg, order)
     assert fs == pytest.approx(2.0) and ws == pytest.approx(1.0)  # copy reads 2 GiB / 4 GiB
@@ -98,6 +100,27 @@ def _full_fixture(tmp_path):
         with open(path, "a", newline="") as f:
             csv.writer(f).writerows(rows)
     return stats, fetch, write
+
+
+READK = "void vbh::(anonymous namespace)::read_kernel<4>(unsigned int __vector(4) const*, unsigned int*, long)"
+
+
+def test_read_dominated_kernels_use_the_read_yardstick(tmp_path):
+    stats = _write(tmp_path / "s.csv",
+                   ["Name", "Calls", "TotalDurationNs", "AverageNs", "Percentage", "MinNs", "MaxNs",
+                    "StdDev"],
+                   [[CONFIG_SYMBOLS["C4_cross_entropy"], 10, 1, 150000, 1, 1, 1, 1],
+                    [C2, 10, 240000, 24000, 1, 23000, 25000, 100],
+                    [COPYK, 2, 2600000, 1300000, 1, 1290000, 1310000, 10],
+                    [READK, 2, 1, 600000, 1, 1, 1, 1]])
+    tr = {r["workload"]: r for r in rs.trace_table(rs.read_stats(stats, rs.CONFIG_KERNELS),
+                                                     rs.config_bytes(),
+                                                     [k for k, _ in rs.CONFIG_KERNELS])}
+    c4 = tr["C4_cross_entropy"]
+    assert c4["peak"] == "read"
+    assert c4["of_peak"] == pytest.approx((1_048_739_840 / 150000) / ((4 << 30) / 600000))
+    assert tr[rs.READ]["of_peak"] == pytest.approx(1.0)
+    assert tr["C2_rms_norm"]["peak"] == "copy"
 
 
 def test_every_config_symbol_is_recognised():
