@@ -96,3 +96,60 @@ def reduce(x: torch.Tensor, dims: list[int], keepdim: bool, op: int, out_dtype, 
         _bridge.launch_fn(fn, name, dev, xc.data_ptr(), _bridge.ptr(vals), _bridge.ptr(idx),
                           outer, n, inner, idt, odt, op)
     return vals, idx
+
+
+class _FastPlans(dict):
+    """Launch plans of single-dim reductions of contiguous inputs, keyed by
+    (shape, dim, keepdim, dtype, op, out_dtype); bounded, and cleared with the
+    geometry caches (``cache_clear``)."""
+
+    LIMIT = 4096
+
+    def cache_clear(self):
+        self.clear()
+
+
+_FAST = _FastPlans()
+_lib.GEOMETRY_CACHES.append(_FAST)
+
+
+def fast_reduce(x: torch.Tensor, dim: int, keepdim: bool, op: int, out_dtype):
+    """reduce() over one int `dim` of a contiguous GPU tensor whose reduced
+    axis is not empty, through a cached plan: (values or None, indices or
+    None), or None where the call needs the general path (which also raises
+    the errors of invalid calls)."""
+    key = (x.shape, dim, keepdim, x.dtype, op, out_dtype)
+    p = _FAST.get(key)
+    if p is None:
+        ndim = x.dim()
+        idt = _bridge.FLOAT_CODES.get(x.dtype)
+        odt = _bridge.FLOAT_CODES.get(out_dtype)
+        if ndim == 0 or idt is None or odt is None or not -ndim <= dim < ndim:
+            return None
+        d = dim % ndim
+        shape = tuple(x.shape)
+        if shape[d] == 0:
+            return None
+        outer, n, inner, _perm, out_shape, out_strides, ws, fn, name = plan(
+            shape, (d,), bool(keepdim), False, idt, op)
+        if ws or outer * inner == 0:
+            return None
+        p = (outer, n, inner, out_shape, out_strides, fn, name, idt, odt)
+        if len(_FAST) >= _FAST.LIMIT:
+            _FAST.clear()
+        _FAST[key] = p
+    dev = x.get_device()
+    if dev < 0 or not x.is_contiguous():
+        return None
+    outer, n, inner, out_shape, out_strides, fn, name, idt, odt = p
+    if op == _lib.REDUCE_ARGMAX:
+        vals = None
+    elif out_dtype is x.dtype:
+        vals = x.new_empty_strided(out_shape, out_strides)
+    else:
+        vals = x.new_empty_strided(out_shape, out_strides, dtype=out_dtype)
+    idx = None if op == _lib.REDUCE_MEAN else x.new_empty_strided(out_shape, out_strides,
+                                                                 dtype=torch.int64)
+    _bridge.launch_fn(fn, name, dev, x.data_ptr(), None if vals is None else vals.data_ptr(),
+                      None if idx is None else idx.data_ptr(), outer, n, inner, idt, odt, op)
+    return vals, idx

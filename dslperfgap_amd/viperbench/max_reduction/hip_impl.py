@@ -21,6 +21,10 @@ def max_reduction(input, dim, keepdim=False):
     """Computes max along a specified dimension, returning (values, indices)."""
     if not isinstance(input, torch.Tensor):
         raise TypeError('The input must be a torch.Tensor.')
+    if type(dim) is int:  # the common call: a cached plan
+        r = _reduce.fast_reduce(input, dim, keepdim, _lib.REDUCE_MAX, input.dtype)
+        if r is not None:
+            return r
     dims = _reduce.norm_dims(int(dim), input.dim(), "max_reduction")
     if input.dim() > 0 and input.shape[dims[0]] == 0:  # other empty axes: empty result
         raise IndexError(f"max(): Expected reduction dim {dims[0]} to have non-zero size.")

@@ -21,6 +21,10 @@ from dslperfgap_amd import _bridge, _lib, _reduce  # noqa: E402
 def mean_reduction(input_tensor, dim, keepdim=False, dtype=None):
     """Computes the mean value along specified dimensions."""
     x = input_tensor
+    if dtype is None and type(dim) is int:  # the common call: a cached plan
+        r = _reduce.fast_reduce(x, dim, keepdim, _lib.REDUCE_MEAN, x.dtype)
+        if r is not None:
+            return r[0]
     out_dtype = x.dtype if dtype is None else dtype
     if out_dtype not in _bridge.FLOAT_CODES:
         raise TypeError(f"mean_reduction: dtype {out_dtype} is not supported by the HIP backend")
