@@ -16,7 +16,7 @@ if _ROOT not in sys.path:  # loadable by file path, as ViperBench's harness load
 
 import torch  # noqa: E402
 
-from dslperfgap_amd import _bridge  # noqa: E402
+from dslperfgap_amd import _bridge, _lib  # noqa: E402
 
 
 def layer_norm(x, weight, bias, eps=1e-5):
@@ -28,6 +28,21 @@ def layer_norm(x, weight, bias, eps=1e-5):
     if eps != 1e-5:
         raise ValueError(f"Only eps=1e-5 is supported (got {eps}). "
                          "The Triton kernel hardcodes eps=1e-5.")
+    # the common call: contiguous x, weight and bias of one dtype on one GPU,
+    # normalized over the last dim -- straight to the row kernel
+    dt = _bridge.FLOAT_CODES.get(x.dtype)
+    if (dt is not None and bias is not None and weight.dim() == 1 and x.dim() > 0 and
+            weight.dtype is x.dtype and bias.dtype is x.dtype and
+            x.shape[-1] == weight.shape[0] and bias.shape == weight.shape):
+        dev = x.get_device()
+        if (dev >= 0 and weight.get_device() == dev and bias.get_device() == dev and
+                x.is_contiguous() and weight.is_contiguous() and bias.is_contiguous()):
+            cols = weight.shape[0]
+            y = torch.empty_like(x)
+            _bridge.launch_fn(_lib.entry("vbh_layer_norm_fwd"), "vbh_layer_norm_fwd", dev,
+                              x.data_ptr(), weight.data_ptr(), bias.data_ptr(), y.data_ptr(),
+                              x.numel() // cols if cols else 0, cols, 1e-5, dt, dt)
+            return y
     dev = _bridge.require_gpu("layer_norm", x, weight, bias)
     norm_shape = tuple(weight.shape)
     k = len(norm_shape)
