@@ -35,6 +35,12 @@ struct CeScalars {
   // as a logsumexp would, not the golden's NaN; the second stage applies the
   // golden's rule to the whole row
   int empty_neg_inf;
+  // logit_scale * log2(e): exp(x * scale - m) = 2^(x * exp_scale - m * log2(e)),
+  // one FMA per logit ahead of v_exp_f32
+  float exp_scale;
+  // logit_scale > 0: the row max of the scaled logits is scale * the max of the
+  // raw ones (rounding is monotone), one multiply per row instead of per logit
+  int scale_pos;
 };
 
 CeScalars make_scalars(float smoothing, float logit_scale, float lse_square_scale,
@@ -54,6 +60,8 @@ CeScalars make_scalars(float smoothing, float logit_scale, float lse_square_scal
   c.has_smoothing = has_smoothing;
   c.split = split;
   c.empty_neg_inf = 0;
+  c.exp_scale = static_cast<float>(static_cast<double>(logit_scale) * 1.4426950408889634);
+  c.scale_pos = logit_scale > 0.f && logit_scale <= 3.4028234663852886e38f;
   return c;
 }
 
@@ -111,7 +119,9 @@ __device__ __forceinline__ MisSeg mis_seg(int64_t start, int len) {
   return MisSeg{head, nvec, len - head - nvec * V};
 }
 
-template <typename T, int V, int IT, bool NT, bool MIS>
+// SL: the segment's sum of logits is needed (smoothing, or the first stage of
+// a split row); without it that accumulation is left out.
+template <typename T, int V, int IT, bool NT, bool MIS, bool SL>
 __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
     const T* __restrict__ logits, const void* __restrict__ labels, int label_i64,
     float* __restrict__ loss, float* __restrict__ lse_out, float* __restrict__ z_out,
@@ -160,11 +170,21 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
   float mx[V];
 #pragma unroll
   for (int k = 0; k < V; ++k) mx[k] = kNegInf;
+  if (c.scale_pos) {  // max of the raw logits, scaled once
 #pragma unroll
-  for (int i = 0; i < IT; ++i)
-    if (i * tpr + g < nvec)
+    for (int i = 0; i < IT; ++i)
+      if (i * tpr + g < nvec)
 #pragma unroll
-      for (int k = 0; k < V; ++k) mx[k] = fmaxf(mx[k], raw_at<T, V>(xr[i], k) * scale);
+        for (int k = 0; k < V; ++k) mx[k] = fmaxf(mx[k], raw_at<T, V>(xr[i], k));
+#pragma unroll
+    for (int k = 0; k < V; ++k) mx[k] *= scale;
+  } else {
+#pragma unroll
+    for (int i = 0; i < IT; ++i)
+      if (i * tpr + g < nvec)
+#pragma unroll
+        for (int k = 0; k < V; ++k) mx[k] = fmaxf(mx[k], raw_at<T, V>(xr[i], k) * scale);
+  }
   float lm = mx[0];
 #pragma unroll
   for (int k = 1; k < V; ++k) lm = fmaxf(lm, mx[k]);
@@ -176,14 +196,15 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
   float se[V], sl[V];
 #pragma unroll
   for (int k = 0; k < V; ++k) se[k] = sl[k] = 0.f;
+  const float mb = m * kLog2e;
 #pragma unroll
   for (int i = 0; i < IT; ++i) {
     if (i * tpr + g < nvec) {
 #pragma unroll
       for (int k = 0; k < V; ++k) {
-        const float v = raw_at<T, V>(xr[i], k) * scale;
-        se[k] += fast_exp(v - m);
-        sl[k] += v;
+        const float x = raw_at<T, V>(xr[i], k);
+        se[k] += __builtin_amdgcn_exp2f(fmaf(x, c.exp_scale, -mb));
+        if constexpr (SL) sl[k] += x * scale;
       }
     }
   }
@@ -204,7 +225,7 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
   }
   const float s = group_allreduce<Sum>(se[0], tpr, lds[1]);
   float sum_logits = 0.f;
-  if (c.has_smoothing || c.empty_neg_inf) sum_logits = group_allreduce<Sum>(sl[0], tpr, lds[2]);
+  if constexpr (SL) sum_logits = group_allreduce<Sum>(sl[0], tpr, lds[2]);
 
   if (live && g == 0) {
     float lse = fast_log(s) + m;
@@ -441,9 +462,14 @@ hipError_t launch_cross_entropy_fwd(const CeArgs& a, const Geometry& g, hipStrea
                                g.tpr, c);
             err = hipGetLastError();
           };
-          if (V > 1 && g.mis) launch(ce_fwd_rows<T, V, M, true, V != 1>);
-          else if (g.nt) launch(ce_fwd_rows<T, V, M, true, false>);
-          else launch(ce_fwd_rows<T, V, M, false, false>);
+          auto pick = [&](auto sl) {
+            constexpr bool SL = decltype(sl)::value;
+            if (V > 1 && g.mis) launch(ce_fwd_rows<T, V, M, true, V != 1, SL>);
+            else if (g.nt) launch(ce_fwd_rows<T, V, M, true, false, SL>);
+            else launch(ce_fwd_rows<T, V, M, false, false, SL>);
+          };
+          if (c.has_smoothing || c.empty_neg_inf) pick(std::true_type{});
+          else pick(std::false_type{});
         }
       });
     };
