@@ -4,6 +4,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 #include <unordered_map>
@@ -1073,9 +1074,14 @@ int vbh_stream_copy(const void* src, void* dst, int64_t bytes, void* stream) {
                     "stream_copy launch");
 }
 
+// The read yardstick's persistent grid: one workgroup per CU, never more than
+// the read has tiles, and at most kReadMaxGrid (the partial buffer's size does
+// not depend on the device).
+constexpr int64_t kReadMaxGrid = 4096;
+
 int64_t vbh_stream_read_partial_bytes(int64_t bytes) {
   if (bytes <= 0 || bytes % 16 != 0 || bytes / 16 > kMaxWorkItems) return 0;
-  return 4 * stream_read_tiles(bytes);
+  return 4 * std::min(stream_read_tiles(bytes), kReadMaxGrid);
 }
 
 int vbh_stream_read(const void* src, int64_t bytes, void* partial, int64_t partial_bytes,
@@ -1092,8 +1098,16 @@ int vbh_stream_read(const void* src, int64_t bytes, void* partial, int64_t parti
   if (partial_bytes < need)
     return fail(VBH_E_INVALID, "stream_read: partial holds %lld bytes, %lld needed",
                 static_cast<long long>(partial_bytes), static_cast<long long>(need));
-  return hip_status(launch_stream_read(src, partial, bytes, static_cast<hipStream_t>(stream)),
-                    "stream_read launch");
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  const int grid = static_cast<int>(std::min<int64_t>(
+      {static_cast<int64_t>(cus), stream_read_tiles(bytes), kReadMaxGrid}));
+  return hip_status(
+      launch_stream_read(src, partial, bytes, grid, static_cast<hipStream_t>(stream)),
+      "stream_read launch");
 }
 
 }  // extern "C"

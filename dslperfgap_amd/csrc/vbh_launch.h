@@ -255,9 +255,12 @@ hipError_t launch_reduce_combine(const void* pvals, const int64_t* pidx, void* v
 hipError_t launch_stream_copy(const void* src, void* dst, int64_t bytes, hipStream_t s);
 
 // streaming-read yardstick: 16-byte vectors per lane per workgroup tile
-constexpr int kReadUnroll = 4;
-// workgroup tiles (= 32-bit partial words written) of a read of `bytes`
+constexpr int kReadUnroll = 8;
+// workgroup tiles of a read of `bytes`
 int64_t stream_read_tiles(int64_t bytes);
-hipError_t launch_stream_read(const void* src, void* partial, int64_t bytes, hipStream_t s);
+// `grid` persistent workgroups (at most the tile count), one 32-bit partial
+// word each
+hipError_t launch_stream_read(const void* src, void* partial, int64_t bytes, int grid,
+                              hipStream_t s);
 
 }  // namespace vbh

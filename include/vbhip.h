@@ -249,9 +249,11 @@ int64_t vbh_reduce_workspace_bytes(int64_t outer, int64_t n, int64_t inner, int 
 int vbh_stream_copy(const void* src, void* dst, int64_t bytes, void* stream);
 
 /* Streaming read of `bytes` (16-byte aligned pointer, multiple of 16): every
- * 16-byte vector is loaded once and folded into one 32-bit word per 16 KiB
- * tile, written to `partial` (4-byte aligned, at least
- * vbh_stream_read_partial_bytes(bytes) bytes).  Its sustained rate is the
+ * 16-byte vector is loaded once, by a persistent grid of one workgroup per CU
+ * walking 32 KiB tiles, and folded by XOR into one 32-bit word per workgroup,
+ * written to `partial` (4-byte aligned, at least
+ * vbh_stream_read_partial_bytes(bytes) bytes; the XOR of the words written is
+ * the XOR of every 32-bit word read).  Its sustained rate is the
  * measured read peak that read-dominated kernels (logsumexp, cross-entropy
  * forward, mean / max / argmax) are quoted against.
  * Replaces: the vendor-spec PEAKS table of experiments/exp_cliff_roofline.py:192-218,

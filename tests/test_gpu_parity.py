@@ -572,28 +572,30 @@ def test_stream_copy_copies(nbytes):
     assert bool((dst[nbytes:] == 7).all())
 
 
-@pytest.mark.parametrize("nbytes", [16, 16368, 16384, 16400, (1 << 20) + 48, 3 << 24])
+@pytest.mark.parametrize("nbytes", [16, 32752, 32768, 32784, (1 << 20) + 48, 3 << 24, 1 << 30])
 def test_stream_read_reads_every_vector(nbytes):
-    """The read yardstick folds every 32-bit word of its 16 KiB tile into the
-    tile's partial word (XOR), so each partial equals numpy's XOR over the same
-    words; the words just past the partials keep their old value."""
+    """The read yardstick folds every 32-bit word it reads into its
+    workgroup's partial word (XOR) and writes one word per workgroup of its
+    persistent grid (one per CU, at most one per 32 KiB tile): the XOR of the
+    words written equals numpy's XOR over the whole buffer, and the words past
+    them keep their old value."""
     import numpy as np
 
     g = _g(121)
     src = torch.randint(0, 256, (nbytes,), generator=g, dtype=torch.uint8)
     pbytes = _lib.lib().vbh_stream_read_partial_bytes(nbytes)
-    tiles = -(-nbytes // 16384)
-    assert pbytes == 4 * tiles
-    part = torch.full((tiles + 16,), 7, dtype=torch.int32, device=DEV)
+    tiles = -(-nbytes // 32768)
+    assert pbytes == 4 * min(tiles, 4096)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    grid = min(tiles, cus, 4096)
+    part = torch.full((pbytes // 4 + 16,), 7, dtype=torch.int32, device=DEV)
     stream = torch.cuda.current_stream().cuda_stream
     _lib.call("vbh_stream_read", src.to(DEV).data_ptr(), nbytes, part.data_ptr(), pbytes, stream)
     torch.cuda.synchronize()
-    words = np.zeros(tiles * 4096, dtype=np.uint32)
-    words[: nbytes // 4] = src.numpy().view(np.uint32)
-    want = np.bitwise_xor.reduce(words.reshape(tiles, 4096), axis=1)
-    got = part.cpu().numpy()
-    assert np.array_equal(got[:tiles].view(np.uint32), want)
-    assert (got[tiles:] == 7).all()
+    want = np.bitwise_xor.reduce(src.numpy().view(np.uint32))
+    got = part.cpu().numpy().view(np.uint32)
+    assert np.bitwise_xor.reduce(got[:grid]) == want
+    assert (got[grid:] == 7).all()
 
 
 # ---------------------------------------------------------------------------
