@@ -175,7 +175,7 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
     for (int i = 0; i < IT; ++i)
       if (i * tpr + g < nvec)
 #pragma unroll
-        for (int k = 0; k < V; ++k) mx[k] = fmaxf(mx[k], raw_at<T, V>(xr[i], k));
+        for (int k = 0; k < V; ++k) mx[k] = max_nan(mx[k], raw_at<T, V>(xr[i], k));
 #pragma unroll
     for (int k = 0; k < V; ++k) mx[k] *= scale;
   } else {
@@ -183,13 +183,13 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
     for (int i = 0; i < IT; ++i)
       if (i * tpr + g < nvec)
 #pragma unroll
-        for (int k = 0; k < V; ++k) mx[k] = fmaxf(mx[k], raw_at<T, V>(xr[i], k) * scale);
+        for (int k = 0; k < V; ++k) mx[k] = max_nan(mx[k], raw_at<T, V>(xr[i], k) * scale);
   }
   float lm = mx[0];
 #pragma unroll
-  for (int k = 1; k < V; ++k) lm = fmaxf(lm, mx[k]);
-  if (hv) lm = fmaxf(lm, hx);
-  if (tv) lm = fmaxf(lm, tx);
+  for (int k = 1; k < V; ++k) lm = max_nan(lm, mx[k]);
+  if (hv) lm = max_nan(lm, hx);
+  if (tv) lm = max_nan(lm, tx);
   const float m = group_allreduce<Max>(lm, tpr, lds[0]);
   reload_barrier<T, V, IT>(xr);
 
@@ -228,7 +228,7 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
   if constexpr (SL) sum_logits = group_allreduce<Sum>(sl[0], tpr, lds[2]);
 
   if (live && g == 0) {
-    float lse = fast_log(s) + m;
+    float lse = (fast_log(s) - shift_residual(m, mb) * kLn2) + m;
     // all -inf (the sum of logits is -inf, not NaN): -inf in a first stage
     if (c.empty_neg_inf && m == kNegInf && sum_logits == sum_logits) lse = kNegInf;
     ce_store(lse, sum_logits, in_block, logit_label, ignored, c, loss, lse_out, z_out,

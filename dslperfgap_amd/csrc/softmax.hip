@@ -36,7 +36,7 @@ __device__ __forceinline__ void load_raw_row(const T* __restrict__ xr, int nvec,
   }
 }
 
-// max over the lane's valid values (-inf when it holds none)
+// max over the lane's valid values (-inf when it holds none; NaN when one is NaN)
 template <typename T, int V, int IT>
 __device__ __forceinline__ float lane_max(const typename Raw<T, V>::type (&xr)[IT], int nvec,
                                           int g, int tpr) {
@@ -47,17 +47,20 @@ __device__ __forceinline__ float lane_max(const typename Raw<T, V>::type (&xr)[I
   for (int i = 0; i < IT; ++i)
     if (i * tpr + g < nvec)
 #pragma unroll
-      for (int k = 0; k < V; ++k) m[k] = fmaxf(m[k], raw_at<T, V>(xr[i], k));
+      for (int k = 0; k < V; ++k) m[k] = max_nan(m[k], raw_at<T, V>(xr[i], k));
   float r = m[0];
 #pragma unroll
-  for (int k = 1; k < V; ++k) r = fmaxf(r, m[k]);
+  for (int k = 1; k < V; ++k) r = max_nan(r, m[k]);
   return r;
 }
 
-// sum over the lane's valid values of exp(v - shift)
-template <typename T, int V, int IT>
-__device__ __forceinline__ float lane_sum_exp(const typename Raw<T, V>::type (&xr)[IT], int nvec,
-                                              int g, int tpr, float shift) {
+// sum over the lane's valid values of exp(v - m), given mb = m * log2 e (see
+// exp_shifted).  KEEP (fp32 rows only) leaves each exp(v - m) in place of v, for
+// a softmax output pass that then only multiplies.
+template <typename T, int V, int IT, bool KEEP = false>
+__device__ __forceinline__ float lane_sum_exp(typename Raw<T, V>::type (&xr)[IT], int nvec,
+                                              int g, int tpr, float mb) {
+  static_assert(!KEEP || sizeof(T) == 4, "exp values are kept in fp32 registers only");
   float a[V];
 #pragma unroll
   for (int k = 0; k < V; ++k) a[k] = 0.f;
@@ -65,7 +68,14 @@ __device__ __forceinline__ float lane_sum_exp(const typename Raw<T, V>::type (&x
   for (int i = 0; i < IT; ++i)
     if (i * tpr + g < nvec)
 #pragma unroll
-      for (int k = 0; k < V; ++k) a[k] += fast_exp(raw_at<T, V>(xr[i], k) - shift);
+      for (int k = 0; k < V; ++k) {
+        const float e = exp_shifted(raw_at<T, V>(xr[i], k), mb);
+        if constexpr (KEEP) {
+          if constexpr (V == 1) xr[i] = e;
+          else xr[i][k] = e;
+        }
+        a[k] += e;
+      }
 #pragma unroll
   for (int w = V / 2; w >= 1; w /= 2)
 #pragma unroll
@@ -116,13 +126,16 @@ __global__ __launch_bounds__(kMaxBlock) void softmax_rows(const Ti* __restrict__
   if (hv) hx = static_cast<float>(x[start + g]);
   if (tv) tx = static_cast<float>(xb[static_cast<int64_t>(nvec) * V + g]);
   float lm = lane_max<Ti, V, IT>(xr, nvec, g, tpr);
-  if (hv) lm = fmaxf(lm, hx);
-  if (tv) lm = fmaxf(lm, tx);
+  if (hv) lm = max_nan(lm, hx);
+  if (tv) lm = max_nan(lm, tx);
   const float m = group_allreduce<Max>(lm, tpr, lds[0]);
   reload_barrier<Ti, V, IT>(xr);
-  float le = lane_sum_exp<Ti, V, IT>(xr, nvec, g, tpr, m);
-  if (hv) le += fast_exp(hx - m);
-  if (tv) le += fast_exp(tx - m);
+  // fp32 softmax keeps each exp(x - m) for the output pass
+  constexpr bool KEEP = !LOG && sizeof(Ti) == 4;
+  const float mb = m * kLog2e;
+  float le = lane_sum_exp<Ti, V, IT, KEEP>(xr, nvec, g, tpr, mb);
+  if (hv) le += exp_shifted(hx, mb);
+  if (tv) le += exp_shifted(tx, mb);
   const float s = group_allreduce<Sum>(le, tpr, lds[1]);
   if (!live) return;
   reload_barrier<Ti, V, IT>(xr);
@@ -130,7 +143,7 @@ __global__ __launch_bounds__(kMaxBlock) void softmax_rows(const Ti* __restrict__
   const OutWindow<To, SP> out(y + first * cols, std::min<int64_t>(rpb, rows - first) * cols);
   To* yr = y + start + mr.head;
   const int yoff = static_cast<int>(row - first) * cols + mr.head;
-  const float ls = LOG ? fast_log(s) : 0.f;
+  const float ls = LOG ? fast_log(s) - shift_residual(m, mb) * kLn2 : 0.f;
   const float r = LOG ? 0.f : 1.0f / s;
 #pragma unroll
   for (int i = 0; i < IT; ++i) {
@@ -139,18 +152,20 @@ __global__ __launch_bounds__(kMaxBlock) void softmax_rows(const Ti* __restrict__
       float o[V];
 #pragma unroll
       for (int k = 0; k < V; ++k) {
-        const float d = raw_at<Ti, V>(xr[i], k) - m;
-        o[k] = LOG ? d - ls : fast_exp(d) * r;
+        const float v = raw_at<Ti, V>(xr[i], k);
+        if constexpr (LOG) o[k] = (v - m) - ls;
+        else if constexpr (KEEP) o[k] = v * r;
+        else o[k] = exp_shifted(v, mb) * r;
       }
       out.template store<V>(yr + static_cast<int64_t>(j) * V, yoff + j * V, o);
     }
   }
   if (hv) {
-    const float o = LOG ? (hx - m) - ls : fast_exp(hx - m) * r;
+    const float o = LOG ? (hx - m) - ls : exp_shifted(hx, mb) * r;
     store_from_f32<To, 1>(y + start + g, &o);
   }
   if (tv) {
-    const float o = LOG ? (tx - m) - ls : fast_exp(tx - m) * r;
+    const float o = LOG ? (tx - m) - ls : exp_shifted(tx, mb) * r;
     store_from_f32<To, 1>(yr + static_cast<int64_t>(nvec) * V + g, &o);
   }
 }
@@ -189,17 +204,18 @@ __global__ __launch_bounds__(kMaxBlock) void logsumexp_rows(const Ti* __restrict
   if (hv) hx = static_cast<float>(x[start + g]);
   if (tv) tx = static_cast<float>(xb[static_cast<int64_t>(nvec) * V + g]);
   float lm = lane_max<Ti, V, IT>(xr, nvec, g, tpr);
-  if (hv) lm = fmaxf(lm, hx);
-  if (tv) lm = fmaxf(lm, tx);
+  if (hv) lm = max_nan(lm, hx);
+  if (tv) lm = max_nan(lm, tx);
   float m = group_allreduce<Max>(lm, tpr, lds[0]);
   reload_barrier<Ti, V, IT>(xr);
   if (__builtin_isinf(m)) m = 0.f;
-  float le = lane_sum_exp<Ti, V, IT>(xr, nvec, g, tpr, m);
-  if (hv) le += fast_exp(hx - m);
-  if (tv) le += fast_exp(tx - m);
+  const float mb = m * kLog2e;
+  float le = lane_sum_exp<Ti, V, IT>(xr, nvec, g, tpr, mb);
+  if (hv) le += exp_shifted(hx, mb);
+  if (tv) le += exp_shifted(tx, mb);
   const float s = group_allreduce<Sum>(le, tpr, lds[1]);
   if (live && g == 0) {
-    const float r = fast_log(s) + m;
+    const float r = (fast_log(s) - shift_residual(m, mb) * kLn2) + m;
     store_from_f32<To, 1>(y + row, &r);
   }
 }

@@ -178,11 +178,20 @@ struct OutWindow {
 struct Sum {
   __device__ static float apply(float a, float b) { return a + b; }
 };
-// fmaxf drops a NaN operand.  The row kernels never expose the max itself:
-// every output that depends on it also depends on exp(x - max) summed over the
-// row, and a NaN element poisons that sum, so NaN rows still come out NaN.
+// Max of two floats for the row maxima of the exp-sum kernels: IEEE maximum,
+// NaN if either operand is NaN.  It compiles to one v_maximum3_f32 per two
+// values.  fmaxf (which drops a NaN operand) costs up to three instructions per
+// value here: in the kernels' IEEE mode the compiler first quiets every operand
+// it cannot prove canonical (v_max_f32 v, x, x), which includes every loaded
+// value.  No output depends on which of the two a NaN row gets: every output
+// that depends on the max also depends on exp(x - max) summed over the row,
+// which a NaN element (or a NaN max) makes NaN.
+__device__ __forceinline__ float max_nan(float a, float b) {
+  return __builtin_elementwise_maximum(a, b);
+}
+
 struct Max {
-  __device__ static float apply(float a, float b) { return fmaxf(a, b); }
+  __device__ static float apply(float a, float b) { return max_nan(a, b); }
 };
 
 template <int Ctrl>
@@ -316,6 +325,24 @@ __device__ __forceinline__ float fast_exp(float x) {
 }
 __device__ __forceinline__ float fast_log(float x) {
   return __builtin_amdgcn_logf(x) * kLn2;
+}
+
+// exp(x - m) for many x against one row shift m, given mb = m * log2 e once per
+// row: 2^(x * log2 e - mb), one FMA ahead of v_exp_f32 where fast_exp(x - m)
+// takes a subtract and a multiply.  The rounding of mb moves every exponent of
+// the row by the same amount, shift_residual(m, mb): it cancels in a softmax
+// normalisation, and a log of the row sum subtracts it (times ln 2) -- at
+// |m| = 3e4 it is 2e-3.  Special values follow x - m: -inf - (-inf) and
+// +inf - (+inf) give NaN (as fma(x, log2 e, -mb) does), -inf against a finite m
+// gives 0.
+__device__ __forceinline__ float exp_shifted(float x, float mb) {
+  return __builtin_amdgcn_exp2f(fmaf(x, kLog2e, -mb));
+}
+
+// m * log2 e - mb, exactly (one FMA): sum of exp_shifted(x, mb) over a row =
+// 2^shift_residual * the sum of exp(x - m).
+__device__ __forceinline__ float shift_residual(float m, float mb) {
+  return fmaf(m, kLog2e, -mb);
 }
 
 }  // namespace vbh
