@@ -357,16 +357,22 @@ __global__ __launch_bounds__(256) void ce_combine(
 // read once per workgroup.
 constexpr int kBwdLanes = kCeBwdLanes;
 
-// dlogits of one element: q = p + 2 * lss * lse * p, p = exp(x * scale - lse),
-// minus the (smoothed) one-hot; times dloss * logit_scale.
-__device__ __forceinline__ float ce_grad(float xv, int64_t col, int64_t adj, float lse_r,
-                                         float zfac, float hit, float smooth_neg, float scale,
+// Per-row factors of the backward: p = exp(x * logit_scale - lse) is computed as
+// 2^(x * exp_scale - lb) * 2^-res with lb = lse * log2 e rounded and res its
+// rounding error (exact, one FMA), so each element costs one FMA ahead of
+// v_exp_f32; 2^-res rides on the factor (1 + 2 * lss * lse) that multiplies p.
+struct CeBwdRow {
+  float lb, pf, hit, smooth_neg, scale;
+};
+
+// dlogits of one element: q = p + 2 * lss * lse * p, minus the (smoothed)
+// one-hot (`is_label`); times dloss * logit_scale.
+__device__ __forceinline__ float ce_grad(float xv, bool is_label, const CeBwdRow& b,
                                          const CeScalars& c) {
-  float p = fast_exp(xv * c.logit_scale - lse_r);
-  p = p + zfac * p;
-  if (col == adj) p = p - hit;
-  if (c.has_smoothing) p = p - smooth_neg;
-  return scale * p;
+  float q = __builtin_amdgcn_exp2f(fmaf(xv, c.exp_scale, -b.lb)) * b.pf;
+  if (is_label) q = q - b.hit;
+  if (c.has_smoothing) q = q - b.smooth_neg;
+  return b.scale * q;
 }
 
 // MIS: rows not a multiple of V long (same offset within a vector for logits
@@ -382,15 +388,6 @@ __global__ __launch_bounds__(kBwdLanes) void ce_bwd_tiles(
   const int tix = static_cast<int>(blockIdx.x - row32 * tiles_per_row);
   const int j0 = tix * kBwdLanes;
   const int64_t row = row32;
-  const int64_t label = read_label(labels, label_i64, row);
-  const float dl = label != c.ignored_index ? dloss[row * dloss_stride] : 0.f;
-  const float lse_r = lse[row];
-  const int64_t adj = label - c.class_start;
-  // (dl * logit_scale) is a Python-double product in the golden
-  const float scale = static_cast<float>(static_cast<double>(dl) * c.logit_scale);
-  const float zfac = c.two_lse_square_scale * lse_r;
-  const float smooth_neg = c.has_smoothing ? c.smooth_negative : 0.f;
-  const float hit = c.has_smoothing ? c.one_minus_smoothing : 1.0f;
   const int64_t in0 = row * ld_in;
   int head = 0, nvec = n_cols / V, tail = 0;
   if constexpr (MIS) {
@@ -401,30 +398,43 @@ __global__ __launch_bounds__(kBwdLanes) void ce_bwd_tiles(
   }
   const T* lr = logits + in0 + head;     // 16-byte aligned body
   T* dr = dlogits + row * ld_out + head;
+  const int j = j0 + static_cast<int>(threadIdx.x);
+  // the tile's logits load goes out first; the row's label, dloss and lse
+  // (independent loads: dloss is read for ignored rows too) while it is in flight
+  typename Raw<T, V>::type r{};
+  if (j < nvec) r = load_raw<T, V, SP != kStoreCached>(lr + static_cast<int64_t>(j) * V);
+  const int64_t label = read_label(labels, label_i64, row);
+  const float dlv = dloss[row * dloss_stride];
+  const float lse_r = lse[row];
+  const float dl = label != c.ignored_index ? dlv : 0.f;
+  const int64_t adj = label - c.class_start;
+  CeBwdRow b;
+  b.lb = lse_r * kLog2e;
+  b.pf = __builtin_amdgcn_exp2f(-shift_residual(lse_r, b.lb)) *
+         (1.0f + c.two_lse_square_scale * lse_r);
+  // (dl * logit_scale) is a Python-double product in the golden
+  b.scale = static_cast<float>(static_cast<double>(dl) * c.logit_scale);
+  b.smooth_neg = c.has_smoothing ? c.smooth_negative : 0.f;
+  b.hit = c.has_smoothing ? c.one_minus_smoothing : 1.0f;
   const int tile = nvec - j0 < kBwdLanes ? nvec - j0 : kBwdLanes;  // <= 0: no body here
   const OutWindow<T, SP> out(dr + static_cast<int64_t>(j0) * V,
                              static_cast<int64_t>(tile > 0 ? tile : 0) * V);
-  const int j = j0 + static_cast<int>(threadIdx.x);
   if (j < nvec) {
-    const auto r = load_raw<T, V, SP != kStoreCached>(lr + static_cast<int64_t>(j) * V);
+    const int64_t rel = adj - head - static_cast<int64_t>(j) * V;  // label's place in r
     float o[V];
 #pragma unroll
-    for (int k = 0; k < V; ++k)
-      o[k] = ce_grad(raw_at<T, V>(r, k), head + static_cast<int64_t>(j) * V + k, adj, lse_r,
-                     zfac, hit, smooth_neg, scale, c);
+    for (int k = 0; k < V; ++k) o[k] = ce_grad(raw_at<T, V>(r, k), rel == k, b, c);
     out.template store<V>(dr + static_cast<int64_t>(j) * V, static_cast<int>(threadIdx.x) * V, o);
   }
   if (MIS && tix == 0) {
     const int t = static_cast<int>(threadIdx.x);
     if (t < head) {
-      const float o = ce_grad(static_cast<float>(logits[in0 + t]), t, adj, lse_r, zfac, hit,
-                              smooth_neg, scale, c);
+      const float o = ce_grad(static_cast<float>(logits[in0 + t]), adj == t, b, c);
       store_from_f32<T, 1>(dr - head + t, &o);
     }
     if (t < tail) {
       const int64_t k = static_cast<int64_t>(nvec) * V + t;
-      const float o = ce_grad(static_cast<float>(lr[k]), head + k, adj, lse_r, zfac, hit,
-                              smooth_neg, scale, c);
+      const float o = ce_grad(static_cast<float>(lr[k]), adj == head + k, b, c);
       store_from_f32<T, 1>(dr + k, &o);
     }
   }

@@ -145,11 +145,15 @@ template <typename T, int SP>
 struct OutWindow {
   __amdgpu_buffer_rsrc_t rsrc;
 
+  // The byte count goes through readfirstlane: a uniform clamp such as
+  // max(min(n, lanes), 0) is selected as v_med3_i32, a VGPR, and a resource
+  // with a field in a VGPR makes the compiler wrap every store in a loop over
+  // the distinct values of the lanes.
   __device__ __forceinline__ OutWindow(T* base, int64_t elems) {
     if constexpr (SP == kStoreThrough)
-      rsrc = __builtin_amdgcn_make_buffer_rsrc(base, static_cast<short>(0),
-                                               static_cast<int>(elems * sizeof(T)),
-                                               kRawBufferWord3);
+      rsrc = __builtin_amdgcn_make_buffer_rsrc(
+          base, static_cast<short>(0),
+          __builtin_amdgcn_readfirstlane(static_cast<int>(elems * sizeof(T))), kRawBufferWord3);
   }
 
   // Round V fp32 values to T and store them at `p`, which is element `off` of
