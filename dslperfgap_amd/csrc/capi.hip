@@ -292,6 +292,14 @@ constexpr int64_t kMaxCols = (int64_t(1) << 31) - 1;
 constexpr int64_t kMaxWorkItems = (int64_t(1) << 32) - 1;
 
 int check_grid(int64_t units, const Geometry& g) {
+  // the row kernels place a lane in its row group with shifts (group_shape),
+  // which holds for these shapes only
+  const bool shape_ok = g.tpr >= 1 && g.block >= g.tpr && g.block <= kMaxBlock &&
+                        g.block % g.tpr == 0 &&
+                        (g.tpr <= kWave ? (g.tpr & (g.tpr - 1)) == 0 : g.tpr % kWave == 0);
+  if (!shape_ok)
+    return fail(VBH_E_INVALID, "internal: launch shape of %d lanes per row, %d per workgroup",
+                g.tpr, g.block);
   // every unit takes at least one lane
   if (units > kMaxWorkItems)
     return fail(VBH_E_RANGE, "launch of %lld rows exceeds 2^32 work-items",
@@ -761,6 +769,7 @@ int vbh_logsumexp_fwd_ws(const void* x, void* y, int64_t rows, int64_t cols, int
     if (vec_ok || use_mis(g1, vn)) {
       if (int rc = check_grid(units, g1)) return rc;
       const Geometry g2 = geometry_for(VBH_OP_LOGSUMEXP, segs, segs % 4 == 0 ? 4 : 1, rows);
+      if (int rc = check_grid(rows, g2)) return rc;
       hipError_t e =
           vec_ok ? launch_logsumexp(x, workspace, units, seg_cols, in_dtype, kF32, g1, s)
                  : launch_logsumexp(x, workspace, units, static_cast<int>(cols), in_dtype, kF32,
@@ -1030,8 +1039,9 @@ int vbh_reduce_fwd_ws(const void* x, void* values, void* indices, int64_t outer,
       if (op == 0) {
         // segment means in fp32 (equal segments: their mean is the row's mean)
         float* means = static_cast<float*>(workspace);
-        e = launch_reduce(x, means, nullptr, units, seg_n, 1, in_dtype, kF32, 0, g1, s);
         const Geometry g2 = reduce_geometry(segs, segs % 4 == 0 ? 4 : 1, outer);
+        if (int rc = check_grid(outer, g2)) return rc;
+        e = launch_reduce(x, means, nullptr, units, seg_n, 1, in_dtype, kF32, 0, g1, s);
         if (e == hipSuccess)
           e = launch_reduce(means, values, nullptr, outer, segs, 1, kF32, out_dtype, 0, g2, s);
       } else {

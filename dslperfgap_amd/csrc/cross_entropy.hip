@@ -128,9 +128,10 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
     int64_t n_rows, int n_cols, int64_t ld, int bs, int ncb, int tpr, CeScalars c) {
   typedef typename Raw<T, V>::type RT;
   __shared__ float lds[3][kMaxWaves];
-  const int g = threadIdx.x % tpr;
+  const GroupShape gs = group_shape(tpr);
+  const int g = gs.g;
   const int64_t nseg = n_rows * ncb;
-  int64_t seg = static_cast<int64_t>(blockIdx.x) * (blockDim.x / tpr) + threadIdx.x / tpr;
+  int64_t seg = static_cast<int64_t>(blockIdx.x) * gs.per_block + gs.sub;
   const bool live = seg < nseg;
   if (!live) seg = nseg - 1;
   const int64_t row = seg / ncb;
@@ -163,9 +164,10 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
   }
   const float scale = c.logit_scale;
   const bool hv = MIS && g < ms.head, tv = MIS && g < ms.tail;
-  float hx = 0.f, tx = 0.f;
-  if (hv) hx = static_cast<float>(logits[sstart + g]) * scale;
-  if (tv) tx = static_cast<float>(lb[static_cast<int64_t>(nvec) * V + g]) * scale;
+  float hr = 0.f, tr = 0.f;  // raw head / tail logits
+  if (hv) hr = static_cast<float>(logits[sstart + g]);
+  if (tv) tr = static_cast<float>(lb[static_cast<int64_t>(nvec) * V + g]);
+  const float hx = hr * scale, tx = tr * scale;
 
   float mx[V];
 #pragma unroll
@@ -216,11 +218,11 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
       sl[k] += sl[k + w];
     }
   if (hv) {
-    se[0] += fast_exp(hx - m);
+    se[0] += __builtin_amdgcn_exp2f(fmaf(hr, c.exp_scale, -mb));
     sl[0] += hx;
   }
   if (tv) {
-    se[0] += fast_exp(tx - m);
+    se[0] += __builtin_amdgcn_exp2f(fmaf(tr, c.exp_scale, -mb));
     sl[0] += tx;
   }
   const float s = group_allreduce<Sum>(se[0], tpr, lds[1]);

@@ -108,8 +108,9 @@ __global__ __launch_bounds__(kMaxBlock) void reduce_rows(const Ti* __restrict__ 
                                                          int64_t* __restrict__ idx,
                                                          int64_t rows, int n, int tpr) {
   __shared__ float lds[2 * kMaxWaves];
-  const int g = threadIdx.x % tpr;
-  int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / tpr) + threadIdx.x / tpr;
+  const GroupShape gs = group_shape(tpr);
+  const int g = gs.g;
+  int64_t row = static_cast<int64_t>(blockIdx.x) * gs.per_block + gs.sub;
   const bool live = row < rows;
   if (!live) row = rows - 1;
   const int64_t start = row * n;

@@ -110,6 +110,25 @@ __device__ __forceinline__ float lane_sumsq(const typename Raw<T, V>::type (&xr)
   return tree_sum<V>(acc);
 }
 
+// Row statistics on the hardware units: 1 / cols by v_rcp_f32 and 1 / sqrt(v)
+// by v_rsq_f32 (1 ulp each; torch's rsqrt is the latter), where IEEE division
+// and square root take about ten instructions each, paid per lane and row.
+__device__ __forceinline__ float inv_count(int cols) {
+  return __builtin_amdgcn_rcpf(static_cast<float>(cols));
+}
+__device__ __forceinline__ float rsqrt_hw(float v) { return __builtin_amdgcn_rsqf(v); }
+
+// sum / cols for the row mean: the v_rcp_f32 quotient refined by one residual
+// step (the residual sum - q * cols is exact in the FMA), which rounds
+// correctly in practice -- a row of equal values then gets its value back
+// exactly and centres to 0, as under IEEE division.
+__device__ __forceinline__ float mean_of(float sum, int cols) {
+  const float n = static_cast<float>(cols);
+  const float inv = __builtin_amdgcn_rcpf(n);
+  const float q = sum * inv;
+  return fmaf(fmaf(-q, n, sum), inv, q);
+}
+
 // Weight / bias slices ride along with the row when they take at most 32
 // VGPRs in raw storage; otherwise they are read after the reduction.
 template <typename TW, int V, int IT> constexpr bool kEarlyLN = 2 * raw_vgprs<TW>(V, IT) <= 32;
@@ -138,10 +157,11 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_rows(
   typedef typename Raw<TW, V>::type RW;
   __shared__ float lds[2][kMaxWaves];
   const int nvec = cols / V;
-  const int g = threadIdx.x % tpr;
-  const int rpb = blockDim.x / tpr;
+  const GroupShape gs = group_shape(tpr);
+  const int g = gs.g;
+  const int rpb = gs.per_block;
   const int64_t first = static_cast<int64_t>(blockIdx.x) * rpb;
-  int64_t row = first + threadIdx.x / tpr;
+  int64_t row = first + gs.sub;
   const bool live = row < rows;
   if (!live) row = rows - 1;
 
@@ -155,11 +175,11 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_rows(
   }
 
   const float mean =
-      group_allreduce<Sum>(lane_sum<T, V, IT>(xr), tpr, lds[0]) / static_cast<float>(cols);
+      mean_of(group_allreduce<Sum>(lane_sum<T, V, IT>(xr), tpr, lds[0]), cols);
   reload_barrier<T, V, IT>(xr);
   const float m2 = group_allreduce<Sum>(lane_centered_sumsq<T, V, IT>(xr, mean, nvec, g, tpr),
                                         tpr, lds[1]);
-  const float rstd = 1.0f / sqrtf(m2 / static_cast<float>(cols) + eps);
+  const float rstd = rsqrt_hw(m2 * inv_count(cols) + eps);
   if (!live) return;
   reload_barrier<T, V, IT>(xr);
 
@@ -196,10 +216,11 @@ __global__ __launch_bounds__(kMaxBlock) void rms_norm_rows(
   typedef typename Raw<TW, V>::type RW;
   __shared__ float lds[kMaxWaves];
   const int nvec = cols / V;
-  const int g = threadIdx.x % tpr;
-  const int rpb = blockDim.x / tpr;
+  const GroupShape gs = group_shape(tpr);
+  const int g = gs.g;
+  const int rpb = gs.per_block;
   const int64_t first = static_cast<int64_t>(blockIdx.x) * rpb;
-  int64_t row = first + threadIdx.x / tpr;
+  int64_t row = first + gs.sub;
   const bool live = row < rows;
   if (!live) row = rows - 1;
 
@@ -210,7 +231,7 @@ __global__ __launch_bounds__(kMaxBlock) void rms_norm_rows(
   if constexpr (kEarly) load_raw_row<TW, V, IT, false>(w, nvec, g, tpr, wr);
 
   const float ss = group_allreduce<Sum>(lane_sumsq<T, V, IT>(xr), tpr, lds);
-  const float rinv = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+  const float rinv = rsqrt_hw(ss * inv_count(cols) + eps);
   if (!live) return;
   reload_barrier<T, V, IT>(xr);
 
@@ -290,10 +311,11 @@ __global__ __launch_bounds__(kMaxBlock) void norm_rows_mis(
     T* __restrict__ y, int64_t rows, int cols, int tpr, float eps) {
   typedef typename Raw<T, V>::type RT;
   __shared__ float lds[2][kMaxWaves];
-  const int g = threadIdx.x % tpr;
-  const int rpb = blockDim.x / tpr;
+  const GroupShape gs = group_shape(tpr);
+  const int g = gs.g;
+  const int rpb = gs.per_block;
   const int64_t first = static_cast<int64_t>(blockIdx.x) * rpb;
-  int64_t row = first + threadIdx.x / tpr;
+  int64_t row = first + gs.sub;
   const bool live = row < rows;
   if (!live) row = rows - 1;
   const int64_t start = row * cols;
@@ -311,16 +333,15 @@ __global__ __launch_bounds__(kMaxBlock) void norm_rows_mis(
   if constexpr (RMS) {
     const float ss = group_allreduce<Sum>(lane_sumsq<T, V, IT>(xr) + hx * hx + tx * tx, tpr,
                                           lds[0]);
-    scale = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+    scale = rsqrt_hw(ss * inv_count(cols) + eps);
   } else {
-    mean = group_allreduce<Sum>(lane_sum<T, V, IT>(xr) + hx + tx, tpr, lds[0]) /
-           static_cast<float>(cols);
+    mean = mean_of(group_allreduce<Sum>(lane_sum<T, V, IT>(xr) + hx + tx, tpr, lds[0]), cols);
     reload_barrier<T, V, IT>(xr);
     float c2 = lane_centered_sumsq<T, V, IT>(xr, mean, nvec, g, tpr);
     if (hv) c2 = fmaf(hx - mean, hx - mean, c2);
     if (tv) c2 = fmaf(tx - mean, tx - mean, c2);
     const float m2 = group_allreduce<Sum>(c2, tpr, lds[1]);
-    scale = 1.0f / sqrtf(m2 / static_cast<float>(cols) + eps);
+    scale = rsqrt_hw(m2 * inv_count(cols) + eps);
   }
   if (!live) return;
   reload_barrier<T, V, IT>(xr);
@@ -387,9 +408,10 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_pipe(
   typedef typename Raw<TW, V>::type RW;
   __shared__ float lds[2][2][kMaxWaves];
   const int nvec = cols / V;
-  const int g = threadIdx.x % tpr;
-  const int rpb = blockDim.x / tpr;
-  const int grp = threadIdx.x / tpr;
+  const GroupShape gs = group_shape(tpr);
+  const int g = gs.g;
+  const int rpb = gs.per_block;
+  const int grp = gs.sub;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * rpb;
   constexpr bool kNT = SP != kStoreCached;
 
@@ -422,12 +444,12 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_pipe(
       else load_raw_row<T, V, IT, kNT>(x, 0, g, tpr, nxt);
     }
 
-    const float mean = group_allreduce<Sum>(lane_sum<T, V, IT>(cur), tpr, lds[par][0]) /
-                       static_cast<float>(cols);
+    const float mean =
+        mean_of(group_allreduce<Sum>(lane_sum<T, V, IT>(cur), tpr, lds[par][0]), cols);
     reload_barrier<T, V, IT>(cur);
     const float m2 = group_allreduce<Sum>(
         lane_centered_sumsq<T, V, IT, FULL>(cur, mean, nvec, g, tpr), tpr, lds[par][1]);
-    const float rstd = 1.0f / sqrtf(m2 / static_cast<float>(cols) + eps);
+    const float rstd = rsqrt_hw(m2 * inv_count(cols) + eps);
     reload_barrier<T, V, IT>(cur);
     if (FULL || row < rows) {
       const OutWindow<T, SP> out(y + base * cols, std::min<int64_t>(rpb, rows - base) * cols);
@@ -460,9 +482,10 @@ __global__ __launch_bounds__(kMaxBlock) void rms_norm_pipe(
   typedef typename Raw<TW, V>::type RW;
   __shared__ float lds[2][kMaxWaves];
   const int nvec = cols / V;
-  const int g = threadIdx.x % tpr;
-  const int rpb = blockDim.x / tpr;
-  const int grp = threadIdx.x / tpr;
+  const GroupShape gs = group_shape(tpr);
+  const int g = gs.g;
+  const int rpb = gs.per_block;
+  const int grp = gs.sub;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * rpb;
   constexpr bool kNT = SP != kStoreCached;
 
@@ -491,7 +514,7 @@ __global__ __launch_bounds__(kMaxBlock) void rms_norm_pipe(
     }
 
     const float ss = group_allreduce<Sum>(lane_sumsq<T, V, IT>(cur), tpr, lds[par]);
-    const float rinv = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+    const float rinv = rsqrt_hw(ss * inv_count(cols) + eps);
     reload_barrier<T, V, IT>(cur);
     if (FULL || row < rows) {
       const OutWindow<T, SP> out(y + base * cols, std::min<int64_t>(rpb, rows - base) * cols);
@@ -543,7 +566,7 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_stream(
   }
   m = group_allreduce_moments(m, tpr, lds);
   const float mean = m.mean;
-  const float rstd = 1.0f / sqrtf(m.m2 / static_cast<float>(cols) + eps);
+  const float rstd = rsqrt_hw(m.m2 * inv_count(cols) + eps);
   T* yr = y + row * cols;
   for (int j = threadIdx.x; j < nvec; j += tpr) {
     float v[V], wv[V], bv[V], o[V];
@@ -578,7 +601,7 @@ __global__ __launch_bounds__(kMaxBlock) void rms_norm_stream(
     for (int k = 0; k < V; ++k) acc = fmaf(v[k], v[k], acc);
   }
   const float ss = group_allreduce<Sum>(acc, tpr, lds);
-  const float rinv = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+  const float rinv = rsqrt_hw(ss * inv_count(cols) + eps);
   T* yr = y + row * cols;
   for (int j = threadIdx.x; j < nvec; j += tpr) {
     float v[V], wv[V], o[V];

@@ -25,57 +25,60 @@ namespace {
 
 constexpr float kNegInf = -__builtin_huge_valf();
 
+// The lane's vectors of the row; those past the row's end hold -inf, which
+// the row max ignores and exp maps to 0, so lane_max and lane_sum_exp need no
+// mask.  (With a mask there, and 0 as the filler, the compiler kept a second,
+// -inf filled copy of each loaded vector, and filling it waited for each load
+// on the spot, one row load at a time.)
 template <typename T, int V, int IT, bool NT>
 __device__ __forceinline__ void load_raw_row(const T* __restrict__ xr, int nvec, int g, int tpr,
                                              typename Raw<T, V>::type (&dst)[IT]) {
+  typedef typename Raw<T, V>::type RT;
+  const RT fill = RT(static_cast<T>(kNegInf));
 #pragma unroll
   for (int i = 0; i < IT; ++i) {
     const int j = i * tpr + g;
     if (j < nvec) dst[i] = load_raw<T, V, NT>(xr + static_cast<int64_t>(j) * V);
-    else dst[i] = typename Raw<T, V>::type{};
+    else dst[i] = fill;
   }
 }
 
-// max over the lane's valid values (-inf when it holds none; NaN when one is NaN)
+// max over the lane's values (-inf when it holds none; NaN when one is NaN)
 template <typename T, int V, int IT>
-__device__ __forceinline__ float lane_max(const typename Raw<T, V>::type (&xr)[IT], int nvec,
-                                          int g, int tpr) {
+__device__ __forceinline__ float lane_max(const typename Raw<T, V>::type (&xr)[IT]) {
   float m[V];
 #pragma unroll
   for (int k = 0; k < V; ++k) m[k] = kNegInf;
 #pragma unroll
   for (int i = 0; i < IT; ++i)
-    if (i * tpr + g < nvec)
 #pragma unroll
-      for (int k = 0; k < V; ++k) m[k] = max_nan(m[k], raw_at<T, V>(xr[i], k));
+    for (int k = 0; k < V; ++k) m[k] = max_nan(m[k], raw_at<T, V>(xr[i], k));
   float r = m[0];
 #pragma unroll
   for (int k = 1; k < V; ++k) r = max_nan(r, m[k]);
   return r;
 }
 
-// sum over the lane's valid values of exp(v - m), given mb = m * log2 e (see
-// exp_shifted).  KEEP (fp32 rows only) leaves each exp(v - m) in place of v, for
-// a softmax output pass that then only multiplies.
+// sum over the lane's values of exp(v - m), given mb = m * log2 e (see
+// exp_shifted; the -inf filler adds 0).  KEEP (fp32 rows only) leaves each
+// exp(v - m) in place of v, for a softmax output pass that then only multiplies.
 template <typename T, int V, int IT, bool KEEP = false>
-__device__ __forceinline__ float lane_sum_exp(typename Raw<T, V>::type (&xr)[IT], int nvec,
-                                              int g, int tpr, float mb) {
+__device__ __forceinline__ float lane_sum_exp(typename Raw<T, V>::type (&xr)[IT], float mb) {
   static_assert(!KEEP || sizeof(T) == 4, "exp values are kept in fp32 registers only");
   float a[V];
 #pragma unroll
   for (int k = 0; k < V; ++k) a[k] = 0.f;
 #pragma unroll
   for (int i = 0; i < IT; ++i)
-    if (i * tpr + g < nvec)
 #pragma unroll
-      for (int k = 0; k < V; ++k) {
-        const float e = exp_shifted(raw_at<T, V>(xr[i], k), mb);
-        if constexpr (KEEP) {
-          if constexpr (V == 1) xr[i] = e;
-          else xr[i][k] = e;
-        }
-        a[k] += e;
+    for (int k = 0; k < V; ++k) {
+      const float e = exp_shifted(raw_at<T, V>(xr[i], k), mb);
+      if constexpr (KEEP) {
+        if constexpr (V == 1) xr[i] = e;
+        else xr[i][k] = e;
       }
+      a[k] += e;
+    }
 #pragma unroll
   for (int w = V / 2; w >= 1; w /= 2)
 #pragma unroll
@@ -108,10 +111,11 @@ __global__ __launch_bounds__(kMaxBlock) void softmax_rows(const Ti* __restrict__
                                                           int cols, int tpr) {
   typedef typename Raw<Ti, V>::type RT;
   __shared__ float lds[2][kMaxWaves];
-  const int g = threadIdx.x % tpr;
-  const int rpb = blockDim.x / tpr;
+  const GroupShape gs = group_shape(tpr);
+  const int g = gs.g;
+  const int rpb = gs.per_block;
   const int64_t first = static_cast<int64_t>(blockIdx.x) * rpb;
-  int64_t row = first + threadIdx.x / tpr;
+  int64_t row = first + gs.sub;
   const bool live = row < rows;
   if (!live) row = rows - 1;
   const int64_t start = row * cols;
@@ -125,7 +129,7 @@ __global__ __launch_bounds__(kMaxBlock) void softmax_rows(const Ti* __restrict__
   float hx = 0.f, tx = 0.f;
   if (hv) hx = static_cast<float>(x[start + g]);
   if (tv) tx = static_cast<float>(xb[static_cast<int64_t>(nvec) * V + g]);
-  float lm = lane_max<Ti, V, IT>(xr, nvec, g, tpr);
+  float lm = lane_max<Ti, V, IT>(xr);
   if (hv) lm = max_nan(lm, hx);
   if (tv) lm = max_nan(lm, tx);
   const float m = group_allreduce<Max>(lm, tpr, lds[0]);
@@ -133,7 +137,7 @@ __global__ __launch_bounds__(kMaxBlock) void softmax_rows(const Ti* __restrict__
   // fp32 softmax keeps each exp(x - m) for the output pass
   constexpr bool KEEP = !LOG && sizeof(Ti) == 4;
   const float mb = m * kLog2e;
-  float le = lane_sum_exp<Ti, V, IT, KEEP>(xr, nvec, g, tpr, mb);
+  float le = lane_sum_exp<Ti, V, IT, KEEP>(xr, mb);
   if (hv) le += exp_shifted(hx, mb);
   if (tv) le += exp_shifted(tx, mb);
   const float s = group_allreduce<Sum>(le, tpr, lds[1]);
@@ -144,7 +148,7 @@ __global__ __launch_bounds__(kMaxBlock) void softmax_rows(const Ti* __restrict__
   To* yr = y + start + mr.head;
   const int yoff = static_cast<int>(row - first) * cols + mr.head;
   const float ls = LOG ? fast_log(s) - shift_residual(m, mb) * kLn2 : 0.f;
-  const float r = LOG ? 0.f : 1.0f / s;
+  const float r = LOG ? 0.f : __builtin_amdgcn_rcpf(s);  // v_rcp_f32, 1 ulp
 #pragma unroll
   for (int i = 0; i < IT; ++i) {
     const int j = i * tpr + g;
@@ -181,8 +185,9 @@ __global__ __launch_bounds__(kMaxBlock) void logsumexp_rows(const Ti* __restrict
                                                             int seg_cols) {
   typedef typename Raw<Ti, V>::type RT;
   __shared__ float lds[2][kMaxWaves];
-  const int g = threadIdx.x % tpr;
-  int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / tpr) + threadIdx.x / tpr;
+  const GroupShape gs = group_shape(tpr);
+  const int g = gs.g;
+  int64_t row = static_cast<int64_t>(blockIdx.x) * gs.per_block + gs.sub;
   const bool live = row < rows;
   if (!live) row = rows - 1;
   int64_t start = row * cols;
@@ -203,14 +208,14 @@ __global__ __launch_bounds__(kMaxBlock) void logsumexp_rows(const Ti* __restrict
   float hx = 0.f, tx = 0.f;
   if (hv) hx = static_cast<float>(x[start + g]);
   if (tv) tx = static_cast<float>(xb[static_cast<int64_t>(nvec) * V + g]);
-  float lm = lane_max<Ti, V, IT>(xr, nvec, g, tpr);
+  float lm = lane_max<Ti, V, IT>(xr);
   if (hv) lm = max_nan(lm, hx);
   if (tv) lm = max_nan(lm, tx);
   float m = group_allreduce<Max>(lm, tpr, lds[0]);
   reload_barrier<Ti, V, IT>(xr);
   if (__builtin_isinf(m)) m = 0.f;
   const float mb = m * kLog2e;
-  float le = lane_sum_exp<Ti, V, IT>(xr, nvec, g, tpr, mb);
+  float le = lane_sum_exp<Ti, V, IT>(xr, mb);
   if (hv) le += exp_shifted(hx, mb);
   if (tv) le += exp_shifted(tx, mb);
   const float s = group_allreduce<Sum>(le, tpr, lds[1]);

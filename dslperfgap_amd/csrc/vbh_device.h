@@ -226,6 +226,52 @@ __device__ __forceinline__ float wave_allreduce(float v, int width) {
   return v;
 }
 
+// ---------------------------------------------------------------------------
+// row groups without integer division
+//
+// The launchers make the lanes per row group, tpr, a power of two up to 64 or
+// a multiple of 64 up to 1024 that divides the workgroup size.  Integer
+// division by a run-time value costs about a dozen VALU instructions per lane
+// here; for these shapes shifts do the work, and several multi-wave groups in
+// one workgroup take one float multiply.
+// ---------------------------------------------------------------------------
+
+// a / b for 0 <= a <= 64 and 1 <= b <= 64, exact: (a + 1/2) / b lies at least
+// 1 / (2b) >= 1/128 from an integer, far beyond the error of v_rcp_f32 (1 ulp).
+__device__ __forceinline__ int small_quotient(int a, int b) {
+  return static_cast<int>((static_cast<float>(a) + 0.5f) *
+                          __builtin_amdgcn_rcpf(static_cast<float>(b)));
+}
+
+// A lane's place in the workgroup's row groups: lane `g` of its group, group
+// `sub` of the workgroup, `per_block` groups per workgroup.
+struct GroupShape {
+  int g, sub, per_block;
+};
+
+__device__ __forceinline__ GroupShape group_shape(int tpr) {
+  const int t = static_cast<int>(threadIdx.x);
+  const int block = static_cast<int>(blockDim.x);
+  if (tpr == block) return GroupShape{t, 0, 1};
+  if ((tpr & (tpr - 1)) == 0) {  // every tpr <= 64 is one
+    const int sh = __builtin_ctz(static_cast<unsigned>(tpr));
+    return GroupShape{t & (tpr - 1), t >> sh, block >> sh};
+  }
+  const int k = tpr >> 6;  // waves per group
+  const int sub = small_quotient(t >> 6, k);
+  return GroupShape{t - sub * tpr, sub, small_quotient(block >> 6, k)};
+}
+
+// First wave of the row group that wave `wave` belongs to, for groups of
+// nwaves = tpr / 64 > 1 waves: 0 when the group is the workgroup, a mask when
+// nwaves is a power of two (the float quotient costs a transcendental-rate
+// v_rcp_f32 on the reduction's path, measurably slower there).
+__device__ __forceinline__ int first_wave_of_group(int wave, int nwaves, int tpr) {
+  if (tpr == static_cast<int>(blockDim.x)) return 0;
+  if ((nwaves & (nwaves - 1)) == 0) return wave & -nwaves;
+  return small_quotient(wave, nwaves) * nwaves;
+}
+
 // All-reduce across the `tpr` threads that own one row.  For tpr <= 64 (a
 // power of two) the group lives inside one wave; for tpr > 64 (any multiple of
 // 64) a row spans tpr / 64 consecutive waves of the workgroup and wave partials
@@ -237,9 +283,9 @@ template <class Op>
 __device__ __forceinline__ float group_allreduce(float v, int tpr, float* lds) {
   if (tpr <= kWave) return wave_allreduce<Op>(v, tpr);
   v = wave_allreduce<Op>(v, kWave);
-  const int wave = threadIdx.x / kWave;
-  const int nwaves = tpr / kWave;
-  const int first = (wave / nwaves) * nwaves;
+  const int wave = static_cast<int>(threadIdx.x) >> 6;
+  const int nwaves = tpr >> 6;
+  const int first = first_wave_of_group(wave, nwaves, tpr);
   if ((threadIdx.x & (kWave - 1)) == 0) lds[wave] = v;
   __syncthreads();
   float r = lds[first];
@@ -307,9 +353,9 @@ __device__ __forceinline__ Moments group_allreduce_moments(Moments m, int tpr, f
     m = merge_moments(m, Moments{swap32_partner(m.n), swap32_partner(m.mean),
                                  swap32_partner(m.m2)});
   if (tpr <= kWave) return m;
-  const int wave = threadIdx.x / kWave;
-  const int nwaves = tpr / kWave;
-  const int first = (wave / nwaves) * nwaves;
+  const int wave = static_cast<int>(threadIdx.x) >> 6;
+  const int nwaves = tpr >> 6;
+  const int first = first_wave_of_group(wave, nwaves, tpr);
   if ((threadIdx.x & (kWave - 1)) == 0) {
     lds[wave] = m.n;
     lds[kMaxWaves + wave] = m.mean;
