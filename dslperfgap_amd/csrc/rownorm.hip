@@ -61,9 +61,50 @@ __device__ __forceinline__ float tree_sum(const float (&a)[V]) {
   return t[0];
 }
 
+// Products of 16-bit pairs on the packed dot-product unit: a.lo * b.lo +
+// a.hi * b.hi + c (v_dot2c_f32_bf16 / v_dot2c_f32_f16; the products of 16-bit
+// values are exact in fp32), two values per instruction and no widening.
+template <typename T> struct Pair;
+template <> struct Pair<__bf16> {
+  typedef __bf16 type __attribute__((ext_vector_type(2)));
+  __device__ static float dot(type a, type b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false);
+  }
+};
+template <> struct Pair<_Float16> {
+  typedef _Float16 type __attribute__((ext_vector_type(2)));
+  __device__ static float dot(type a, type b, float c) {
+    return __builtin_amdgcn_fdot2(a, b, c, false);
+  }
+};
+
+// sum over the lane's 16-bit values of x * (SQ ? x : 1), V / 2 accumulators
+template <typename T, int V, int IT, bool SQ>
+__device__ __forceinline__ float lane_dot2_sum(const typename Raw<T, V>::type (&xr)[IT]) {
+  typedef typename Pair<T>::type P;
+  float acc[V / 2];
+#pragma unroll
+  for (int k = 0; k < V / 2; ++k) acc[k] = 0.f;
+  P one;
+  one[0] = static_cast<T>(1.0f);
+  one[1] = static_cast<T>(1.0f);
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+#pragma unroll
+    for (int k = 0; k < V / 2; ++k) {
+      P x;
+      x[0] = xr[i][2 * k];
+      x[1] = xr[i][2 * k + 1];
+      acc[k] = Pair<T>::dot(x, SQ ? x : one, acc[k]);
+    }
+  }
+  return tree_sum<V / 2>(acc);
+}
+
 // Sum of the lane's values (padding vectors are zero).
 template <typename T, int V, int IT>
 __device__ __forceinline__ float lane_sum(const typename Raw<T, V>::type (&xr)[IT]) {
+  if constexpr (sizeof(T) == 2 && V >= 2) return lane_dot2_sum<T, V, IT, false>(xr);
   float acc[V];
 #pragma unroll
   for (int k = 0; k < V; ++k) acc[k] = 0.f;
@@ -97,6 +138,7 @@ __device__ __forceinline__ float lane_centered_sumsq(const typename Raw<T, V>::t
 
 template <typename T, int V, int IT>
 __device__ __forceinline__ float lane_sumsq(const typename Raw<T, V>::type (&xr)[IT]) {
+  if constexpr (sizeof(T) == 2 && V >= 2) return lane_dot2_sum<T, V, IT, true>(xr);
   float acc[V];
 #pragma unroll
   for (int k = 0; k < V; ++k) acc[k] = 0.f;
