@@ -63,7 +63,8 @@ CONFIG_KERNELS = [
     ("C3_log_softmax", r"softmax_rows<float, float, 4, 2, true, \d(, false)?>"),
     ("C3_softmax", r"softmax_rows<float, float, 4, 2, false, \d(, false)?>"),
     ("C3_logsumexp", r"logsumexp_rows<float, float, 4, 8, true(, false)?>"),
-    ("C4_cross_entropy", r"ce_fwd_rows<float, 4, 8, true(, false)?>"),
+    ("C4_cross_entropy", r"ce_fwd_rows<float, 4, 8, true(, false){0,2}>|"
+                         r"ce_fwd_rowsIfLi4ELi8ELb1E(Lb0E){0,2}E"),
     ("C4_cross_entropy_bwd", r"ce_bwd_tiles<float, 4, \d(, false)?>|ce_bwd_tilesIfLi4ELi\dE"),
     ("C5_layer_norm", r"layer_norm_pipeIDF16bDF16bLi8ELi4ELi\dELb1E"),
     (COPY, r"copy_kernel\("),
@@ -75,7 +76,8 @@ REFERENCE_KERNELS = [
     ("softmax", r"softmax_rowsIDF16_DF16_Li8ELi4ELb0ELi\dE"),
     ("log_softmax", r"softmax_rowsIDF16_DF16_Li8ELi4ELb1ELi\dE"),
     ("logsumexp", r"logsumexp_rows<float, float, 4, 8, true(, false)?>"),
-    ("cross_entropy", r"ce_fwd_rows<float, 4, \d, true(, false)?>"),
+    ("cross_entropy", r"ce_fwd_rows<float, 4, \d, true(, false){0,2}>|"
+                      r"ce_fwd_rowsIfLi4ELi\dELb1E(Lb0E){0,2}E"),
     ("argmax", r"reduce_rowsIDF16_DF16_Li8ELi2E"),
     ("max_reduction", r"reduce_rowsIDF16_DF16_Li8ELi1E"),
     ("mean_reduction", r"reduce_rows<float, float, 4, 0(, false)?>"),
