@@ -232,7 +232,7 @@ def copy_peak(device, nbytes: int = 4 << 30, reps: int = 20) -> float:
 
 def read_peak(device, nbytes: int = 4 << 30, reps: int = 20) -> float:
     """Sustained streaming-read rate in bytes/s (bytes read; the one 32-bit
-    word written per 16 KiB tile is not counted)."""
+    word written per workgroup is not counted)."""
     src = torch.empty(nbytes, dtype=torch.uint8, device=device)
     src.fill_(1)
     pbytes = _lib.lib().vbh_stream_read_partial_bytes(nbytes)
