@@ -177,12 +177,19 @@ def run_workload(key, steps, warmup, peaks, with_cpu, cpu_budget):
     return line
 
 
-def run_copy_at(nbytes, steps, warmup, peaks):
-    """The stream copy moving `nbytes` per launch (half read, half written),
-    rotated through >= 2 GiB and timed like a workload: the yardstick of what a
-    kernel of that size can reach."""
-    launch, moved, copies = harness.copy_rotation("cuda:0", nbytes)
-    key = f"copy@{moved}"
+def run_copy_at(nbytes, steps, warmup, peaks, kind="copy"):
+    """The stream copy moving `nbytes` per launch (half read, half written), or
+    with kind "read" the streaming read of `nbytes`, rotated through >= 2 GiB
+    and timed like a workload: the yardstick of what a kernel of that size can
+    reach."""
+    if kind == "read":
+        launch, moved, copies = harness.read_rotation("cuda:0", nbytes)
+        desc = f"vbh_stream_read of {moved} B per launch, {copies} buffers"
+    else:
+        launch, moved, copies = harness.copy_rotation("cuda:0", nbytes)
+        desc = (f"vbh_stream_copy of {moved // 2} B per launch "
+                f"(read + write {moved} B), {copies} buffer pairs")
+    key = f"{kind}@{moved}"
     harness.warm_gpu(launch, DEVICE_WARM_S)
     r = harness.time_back_to_back(launch, steps, warmup,
                                   fence=_roctx.range_(f"vbh-timed:{key}:{steps}"))
@@ -192,13 +199,12 @@ def run_copy_at(nbytes, steps, warmup, peaks):
         "warmup": warmup, "device_warm_s": DEVICE_WARM_S,
         "ms_per_step": round(r["wall_ms"] / steps, 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "u8", "data": "synthetic (constant bytes)",
-        "config": {"workload": key, "desc": f"vbh_stream_copy of {moved // 2} B per launch "
-                                            f"(read + write {moved} B), {copies} buffer pairs"},
+        "config": {"workload": key, "desc": desc},
         "latency_us": round(r["event_ms"] / steps * 1e3, 3),
         "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": VENDOR_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(value / VENDOR_PEAK_GBPS, 4), "traffic": None,
                      "algorithmic_bytes": moved},
-        # a yardstick line: the copy rate at this size, next to the 4 GiB one
+        # a yardstick line: the copy (or read) rate at this size, next to the 4 GiB ones
         "measured_copy_peak_GBps": round(peaks["copy"] / 1e9, 2),
         "measured_read_peak_GBps": round(peaks["read"] / 1e9, 2),
         "timed_range": f"vbh-timed:{key}:{steps}" if _roctx.available() else None,
@@ -219,6 +225,9 @@ def main():
     ap.add_argument("--copy-at", type=int, nargs="+", metavar="BYTES",
                     help="instead of workloads: the stream copy moving BYTES per launch "
                          "(read + write), one line per size")
+    ap.add_argument("--read-at", type=int, nargs="+", metavar="BYTES",
+                    help="instead of workloads: the streaming read of BYTES per launch, "
+                         "one line per size")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -234,9 +243,12 @@ def main():
     peaks = {"copy": harness.copy_peak("cuda:0"), "read": harness.read_peak("cuda:0")}
     log(f"[bench] measured stream-copy peak: {peaks['copy'] / 1e9:.1f} GB/s (read + write), "
         f"stream-read peak: {peaks['read'] / 1e9:.1f} GB/s")
-    if args.copy_at:
-        for nbytes in args.copy_at:
+    if args.copy_at or args.read_at:
+        for nbytes in args.copy_at or []:
             print(json.dumps(run_copy_at(nbytes, args.steps, args.warmup, peaks)), flush=True)
+        for nbytes in args.read_at or []:
+            print(json.dumps(run_copy_at(nbytes, args.steps, args.warmup, peaks, "read")),
+                  flush=True)
         return
     keys = sorted(WORKLOADS) if args.all else [args.workload]
     for key in keys:

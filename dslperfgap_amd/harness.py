@@ -268,6 +268,28 @@ def copy_rotation(device, traffic_bytes: int, min_footprint: int = 2 << 30):
     return launch, 2 * half, copies
 
 
+def read_rotation(device, nbytes: int, min_footprint: int = 2 << 30):
+    """(launch, bytes read per launch, copies): streaming reads of `nbytes`
+    (rounded down to 16-byte vectors) cycling through enough buffers that no
+    launch hits the Infinity Cache -- the read-only counterpart of
+    copy_rotation, the yardstick at a read-only kernel's own size."""
+    size = max(16, nbytes // 16 * 16)
+    copies = max(2, math.ceil(min_footprint / size))
+    bufs = [torch.empty(size, dtype=torch.uint8, device=device) for _ in range(copies)]
+    for a in bufs:
+        a.fill_(1)
+    pbytes = _lib.lib().vbh_stream_read_partial_bytes(size)
+    partial = torch.empty(pbytes, dtype=torch.uint8, device=device)
+    stream = _bridge.stream(torch.device(device))
+
+    def launch(k):
+        _lib.call("vbh_stream_read", bufs[k % copies].data_ptr(), size, partial.data_ptr(),
+                  pbytes, stream)
+
+    launch.buffers = (bufs, partial)  # kept alive as long as the launcher
+    return launch, size, copies
+
+
 def copy_rate_at(device, traffic_bytes: int, reps: int = 200,
                  min_footprint: int = 2 << 30) -> float:
     """Copy rate (bytes/s, read + write) when one launch moves `traffic_bytes`

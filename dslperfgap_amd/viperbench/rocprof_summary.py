@@ -338,8 +338,9 @@ def read_ranges(path) -> list[dict]:
 
 def alg_bytes_of(key: str) -> int:
     """Algorithmic bytes per launch of a workload key, or of ``copy@N`` (the
-    stream copy moving N bytes per launch, read + write)."""
-    if key.startswith("copy@"):
+    stream copy moving N bytes per launch, read + write) or ``read@N`` (the
+    streaming read of N bytes per launch)."""
+    if key.startswith(("copy@", "read@")):
         return int(key.split("@", 1)[1])
     return WORKLOADS[key].bytes_per_launch
 
@@ -407,8 +408,10 @@ def render_timed(kernel_trace, markers, bench_lines) -> tuple[str, dict]:
     tdir, tpre = _dir_prefix(kernel_trace, "_kernel_trace.csv")
     rows = [timed_row(dispatches, r, alg_bytes_of(r["workload"])) for r in ranges]
     keys = [r["workload"] for r in rows]
-    if all(k.startswith("copy@") for k in keys):
-        args = "--copy-at " + " ".join(k.split("@", 1)[1] for k in keys)
+    if all(k.startswith(("copy@", "read@")) for k in keys):
+        sizes = {kind: [k.split("@", 1)[1] for k in keys if k.startswith(kind + "@")]
+                 for kind in ("copy", "read")}
+        args = " ".join(f"--{kind}-at " + " ".join(v) for kind, v in sizes.items() if v)
     else:
         args = "--all" if len(rows) > 1 else (
             "" if keys == ["C4_cross_entropy"] else f"--workload {keys[0]}")

@@ -255,4 +255,5 @@ def test_kernel_base_names():
     assert rs.kernel_base(CONFIG_SYMBOLS["C5_layer_norm"]) == "layer_norm_pipe"
     assert rs.timed_file("copy@33562624", COPYK) == "copy_kernel_copy_33562624_timed_trace.txt"
     assert rs.alg_bytes_of("copy@33562624") == 33562624
+    assert rs.alg_bytes_of("read@268500992") == 268500992
     assert rs.alg_bytes_of("C1_layer_norm") == WORKLOADS["C1_layer_norm"].bytes_per_launch
