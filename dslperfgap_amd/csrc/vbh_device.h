@@ -264,8 +264,8 @@ __device__ __forceinline__ GroupShape group_shape(int tpr) {
 
 // First wave of the row group that wave `wave` belongs to, for groups of
 // nwaves = tpr / 64 > 1 waves: 0 when the group is the workgroup, a mask when
-// nwaves is a power of two (the float quotient costs a transcendental-rate
-// v_rcp_f32 on the reduction's path, measurably slower there).
+// nwaves is a power of two, else the float quotient (whose v_rcp_f32 runs at
+// the transcendental rate, on the reduction's path).
 __device__ __forceinline__ int first_wave_of_group(int wave, int nwaves, int tpr) {
   if (tpr == static_cast<int>(blockDim.x)) return 0;
   if ((nwaves & (nwaves - 1)) == 0) return wave & -nwaves;
