@@ -20,6 +20,8 @@ adds logsumexp and cross-entropy byte models), evaluated on meta tensors.
 Presets:
   configs    the five measured configs of ``bench.py --all`` (C1-C5)
   reference  the family at the reference's large shapes (cliff_roofline.py)
+  pipes      instruction counters of the configs (SQ_INSTS_*, SQ_WAVES,
+             VALUBusy; one or more ``--pmc`` runs of ``bench.py --all``)
 
     python -m dslperfgap_amd.viperbench.rocprof_summary configs \\
         --trace D/trace/all_kernel_stats.csv --fetch D/fetch/all_counter_collection.csv \\
@@ -309,6 +311,132 @@ def render(preset: str, trace, fetch, write, tail: int = 0) -> tuple[str, str]:
     return trace_txt, head + format_traffic(rows, fs, ws, p["machine"])
 
 
+# Instruction counters of the "pipes" summary, in table order.  SQ_INSTS_* and
+# SQ_WAVES are totals per dispatch over every shader engine of the 8 XCDs.
+PIPE_COUNTERS = ("SQ_WAVES", "SQ_INSTS_VALU", "SQ_INSTS_VALU_TRANS_F32", "SQ_INSTS_SALU",
+                 "SQ_INSTS_VMEM_RD", "SQ_INSTS_VMEM_WR", "VALUBusy")
+PIPES_FILE = "row_kernels_all_configs_instruction_counters.txt"
+SIMDS = 256 * 4                     # MI355X: 256 CUs x 4 SIMDs
+PEAK_CLOCK_HZ = 2.4e9               # MI355X peak engine clock
+VALU_CYCLES = 4                     # a wave64 VALU instruction on a 16-lane SIMD
+
+
+def config_elements() -> dict:
+    """Input elements per launch of each config (rows x columns of the row
+    input; 4-byte words for the 4 GiB yardsticks)."""
+    shapes = {"C1_layer_norm": (4096, 1024), "C2_rms_norm": (8192, 4096),
+              "C3_softmax": (16384, 4096), "C3_log_softmax": (16384, 4096),
+              "C3_logsumexp": (16384, 4096), "C4_cross_entropy": (8192, 32000),
+              "C4_cross_entropy_bwd": (8192, 32000), "C5_layer_norm": (2048, 20480)}
+    out = {k: r * c for k, (r, c) in shapes.items()}
+    out[COPY] = out[READ] = (4 << 30) // 4
+    return out
+
+
+def read_counters(paths, kernels, tail: int = 0) -> dict:
+    """{workload: {counter: mean value per dispatch}} from one or more
+    counter_collection.csv files (a counter found in several files is taken
+    from the first); `tail` as in read_counter."""
+    out: dict = collections.defaultdict(dict)
+    for path in paths:
+        acc = collections.defaultdict(lambda: collections.defaultdict(float))
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                key = classify(r["Kernel_Name"], kernels)
+                if key:
+                    acc[(key, r["Counter_Name"])][int(r["Dispatch_Id"])] += float(r["Counter_Value"])
+        for (key, counter), per in acc.items():
+            if counter in out[key]:
+                continue
+            ids = sorted(per)
+            if tail and key != COPY:
+                ids = ids[-tail:]
+            out[key][counter] = sum(per[i] for i in ids) / len(ids)
+    return dict(out)
+
+
+def pipes_table(counters: dict, stats: dict, elements: dict, order) -> list[dict]:
+    rows = []
+    for key in order:
+        c = counters.get(key)
+        if not c or "SQ_WAVES" not in c or key not in stats:
+            continue
+        waves = c["SQ_WAVES"]
+        per_wave = {n: c[n] / waves for n in PIPE_COUNTERS[1:6] if n in c}
+        valu = c.get("SQ_INSTS_VALU", float("nan"))
+        floor_ns = valu * VALU_CYCLES / SIMDS / PEAK_CLOCK_HZ * 1e9
+        avg = stats[key][2]
+        rows.append(dict(workload=key, waves=waves, per_wave=per_wave,
+                         valu_per_64=valu / (elements[key] / 64), avg_ns=avg,
+                         valu_floor_ns=floor_ns, floor_share=floor_ns / avg,
+                         valu_busy=c.get("VALUBusy", float("nan"))))
+    return rows
+
+
+def render_pipes(trace, pmcs, tail: int = 0, bench_lines=None) -> str:
+    kernels = CONFIG_KERNELS
+    order = [k for k, _ in kernels]
+    stats = read_stats(trace, kernels)
+    counters = read_counters(pmcs, kernels, tail)
+    missing = [k for k in order if k != READ and (k not in stats or k not in counters)]
+    if missing:
+        raise ValueError(f"pipes: no kernel in the rocprofv3 files matched {missing}; "
+                         "update the symbol patterns")
+    rows = pipes_table(counters, stats, config_elements(), order)
+    tdir, tpre = _dir_prefix(trace, "_kernel_stats.csv")
+    cmd = PRESETS["configs"]["pmc_cmd"]
+    runs = []
+    for path in pmcs:
+        d, pre = _dir_prefix(path, "_counter_collection.csv")
+        with open(path, newline="") as f:
+            names = sorted({r["Counter_Name"] for r in csv.DictReader(f)})
+        runs.append(f"  timeout -s KILL 400 rocprofv3 --pmc {' '.join(names)} \\\n"
+                    f"      --output-format csv -d {d} -o {pre} -- {cmd}")
+    head = [
+        "rocprofv3 instruction counters -- every measured workload (C1-C5, bench.py --all) "
+        "(MI355X, gfx950)", "",
+        "Commands (from the repository root, after `cd /tmp && export TMPDIR=/tmp`), one run",
+        "per counter group, and the kernel trace the durations come from:", *runs,
+        f"  rocprofv3 --kernel-trace --stats --output-format csv -d {tdir} -o {tpre} -- {cmd}",
+        "Summary: python -m dslperfgap_amd.viperbench.rocprof_summary pipes \\",
+        "      --trace <stats csv> --pmc <counter csv> ... --tail 50 --bench-lines <bench.py lines>",
+        "",
+        "Counters are totals per dispatch (every shader engine of the 8 XCDs), averaged over",
+        "the last 50 dispatches of each workload's kernel (bench.py's timed launches; the",
+        "yardsticks over all of theirs); per-wave figures divide by SQ_WAVES.",
+        "VALU/64el = VALU instructions per 64 input elements (one wave64 instruction per",
+        "element would be 1.0).  VALU floor = SQ_INSTS_VALU x 4 cycles / 1024 SIMDs at the",
+        "2.4 GHz peak clock: the time the SIMDs need just to issue the VALU instructions",
+        "(transcendentals and dependency stalls take longer), against the traced average",
+        "duration avg_ns.  VALUBusy = rocprofv3's derived counter (100 x SQ_ACTIVE_INST_VALU",
+        "/ CU count / GRBM_GUI_ACTIVE), the share of the dispatch's cycles the SIMDs spent",
+        "on VALU work.", ""]
+    if bench_lines:
+        import json
+
+        hashes = sorted({json.loads(ln).get("lib_srchash", "") for ln in
+                         Path(bench_lines).read_text().splitlines() if ln.strip().startswith("{")}
+                        - {""})
+        if hashes:
+            head.insert(1, f"Library source hash (libvbhip.srchash, csrc/ + include/): "
+                           f"{', '.join(hashes)}")
+    hdr = (f"{'workload':<21}{'waves':>9}{'VALU/wave':>10}{'trans/wave':>11}{'SALU/wave':>10}"
+           f"{'VMEMrd/w':>9}{'VMEMwr/w':>9}{'VALU/64el':>10}{'avg_ns':>10}{'VALUfloor':>10}"
+           f"{'floor%':>7}{'VALUBusy%':>10}")
+    lines = [hdr]
+    for r in rows:
+        pw = r["per_wave"]
+        lines.append(
+            f"{r['workload']:<21}{r['waves']:>9.0f}{pw.get('SQ_INSTS_VALU', float('nan')):>10.1f}"
+            f"{pw.get('SQ_INSTS_VALU_TRANS_F32', float('nan')):>11.1f}"
+            f"{pw.get('SQ_INSTS_SALU', float('nan')):>10.1f}"
+            f"{pw.get('SQ_INSTS_VMEM_RD', float('nan')):>9.1f}"
+            f"{pw.get('SQ_INSTS_VMEM_WR', float('nan')):>9.1f}{r['valu_per_64']:>10.2f}"
+            f"{r['avg_ns']:>10.0f}{r['valu_floor_ns']:>10.0f}{100 * r['floor_share']:>7.1f}"
+            f"{r['valu_busy']:>10.1f}")
+    return "\n".join(head + lines) + "\n"
+
+
 TIMED_PREFIX = "vbh-timed:"
 
 
@@ -471,7 +599,7 @@ def render_timed(kernel_trace, markers, bench_lines) -> tuple[str, dict]:
 
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
-    ap.add_argument("preset", choices=sorted(PRESETS) + ["timed"])
+    ap.add_argument("preset", choices=sorted(PRESETS) + ["timed", "pipes"])
     ap.add_argument("--trace", help="<prefix>_kernel_stats.csv")
     ap.add_argument("--kernel-trace", help="timed: <prefix>_kernel_trace.csv")
     ap.add_argument("--markers", help="timed: <prefix>_marker_api_trace.csv")
@@ -479,7 +607,11 @@ def main(argv=None) -> int:
                     help="timed: also write the table of every range under this file name")
     ap.add_argument("--fetch", help="FETCH_SIZE <prefix>_counter_collection.csv")
     ap.add_argument("--write", help="WRITE_SIZE <prefix>_counter_collection.csv")
-    ap.add_argument("--bench-lines", help="timed: the JSON lines bench.py printed in the run")
+    ap.add_argument("--pmc", action="append", default=[],
+                    help="pipes: a <prefix>_counter_collection.csv of instruction counters "
+                         "(repeatable)")
+    ap.add_argument("--bench-lines", help="timed, pipes: the JSON lines bench.py printed in the "
+                                          "run")
     ap.add_argument("--tail", type=int, default=0,
                     help="counters: only the last TAIL dispatches of each workload's kernel "
                          "(bench.py's timed launches are each workload's last ones)")
@@ -499,6 +631,15 @@ def main(argv=None) -> int:
                 Path(args.out_dir, args.combined_name).write_text(combined)
         else:
             sys.stdout.write(combined)
+        return 0
+    if args.preset == "pipes":
+        if not (args.trace and args.pmc):
+            ap.error("pipes needs --trace and at least one --pmc")
+        txt = render_pipes(args.trace, args.pmc, tail=args.tail, bench_lines=args.bench_lines)
+        if args.out_dir:
+            Path(args.out_dir, PIPES_FILE).write_text(txt)
+        else:
+            sys.stdout.write(txt)
         return 0
     if not (args.trace and args.fetch and args.write):
         ap.error(f"{args.preset} needs --trace, --fetch and --write")

@@ -257,3 +257,39 @@ def test_kernel_base_names():
     assert rs.alg_bytes_of("copy@33562624") == 33562624
     assert rs.alg_bytes_of("read@268500992") == 268500992
     assert rs.alg_bytes_of("C1_layer_norm") == WORKLOADS["C1_layer_norm"].bytes_per_launch
+
+
+def test_instruction_counters_per_wave_and_floor(tmp_path):
+    """pipes: per-wave figures divide by SQ_WAVES, VALU/64el by the input's
+    elements / 64, the VALU floor is SQ_INSTS_VALU x 4 cycles over 1024 SIMDs at
+    2.4 GHz; a counter in two files comes from the first, and --tail keeps the
+    last dispatches."""
+    hdr = ["Correlation_Id", "Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"]
+    a = _write(tmp_path / "a" / "all_counter_collection.csv", hdr,
+               [[1, 1, C2, "SQ_WAVES", 999.0], [1, 1, C2, "SQ_INSTS_VALU", 1.0],
+                [2, 2, C2, "SQ_WAVES", 8192.0], [2, 2, C2, "SQ_INSTS_VALU", 8192 * 300.0],
+                [2, 2, C2, "VALUBusy", 41.5]])
+    b = _write(tmp_path / "b" / "all_counter_collection.csv", hdr,
+               [[2, 2, C2, "SQ_WAVES", 1.0], [2, 2, C2, "SQ_INSTS_SALU", 8192 * 20.0],
+                [2, 2, C2, "SQ_INSTS_VMEM_RD", 8192 * 16.0]])
+    c = rs.read_counters([a, b], rs.CONFIG_KERNELS, tail=1)
+    assert c["C2_rms_norm"]["SQ_WAVES"] == 8192.0          # from the first file, last dispatch
+    stats = {"C2_rms_norm": (C2, 10, 24000.0, 23000.0, 25000.0)}
+    (row,) = rs.pipes_table(c, stats, rs.config_elements(), ["C2_rms_norm"])
+    assert row["per_wave"]["SQ_INSTS_VALU"] == pytest.approx(300.0)
+    assert row["per_wave"]["SQ_INSTS_SALU"] == pytest.approx(20.0)
+    assert row["per_wave"]["SQ_INSTS_VMEM_RD"] == pytest.approx(16.0)
+    assert row["valu_per_64"] == pytest.approx(8192 * 300.0 / (8192 * 4096 / 64))
+    floor = 8192 * 300.0 * 4 / 1024 / 2.4e9 * 1e9
+    assert row["valu_floor_ns"] == pytest.approx(floor)
+    assert row["floor_share"] == pytest.approx(floor / 24000.0)
+    assert row["valu_busy"] == pytest.approx(41.5)
+
+
+def test_instruction_counters_need_every_config(tmp_path):
+    stats, _, _ = _fixture(tmp_path)
+    hdr = ["Correlation_Id", "Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"]
+    a = _write(tmp_path / "a" / "all_counter_collection.csv", hdr,
+               [[2, 2, C2, "SQ_WAVES", 8192.0], [3, 3, COPYK, "SQ_WAVES", 1.0]])
+    with pytest.raises(ValueError, match="C1_layer_norm"):
+        rs.render_pipes(stats, [a], tail=50)
