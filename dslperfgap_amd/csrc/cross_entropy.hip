@@ -5,9 +5,11 @@
 // into registers in the storage type (scaled by logit_scale where used),
 // all-reduce max, sum of exp(x - max) and, with smoothing, the plain sum of the
 // logits, and one lane writes loss / lse / z_loss at flat index
-// cb * n_rows + row.  The label logit is fetched by that lane at kernel start,
-// so its latency overlaps the segment loads.  Segments wider than the register
-// budget use a streaming online (max, rescaled sum) pass.
+// cb * n_rows + row.  The label logit is fetched by that lane at kernel start;
+// only the storing lane's wave waits for it before issuing its segment loads,
+// the segment's other waves load at once (a version without the fetch ran
+// 0.1% faster on MI355X).  Segments wider than the register budget use a
+// streaming online (max, rescaled sum) pass.
 //
 // Semantics: ViperBench/cross_entropy/pytorch_impl.py:22-90 (golden) and
 // ViperBench/cross_entropy/triton_impl.py:33-75 (per-(row, block) program).
