@@ -89,6 +89,28 @@ def stream(dev) -> int:
 _raw_device = getattr(torch._C, "_cuda_getDevice", None) or torch.cuda.current_device
 
 
+class PlanCache(dict):
+    """Launch plans of the wrappers' common calls, keyed by what decides them
+    (shape, dtype, ...): bounded, and registered with the library's geometry
+    caches, so that ``_lib.tune_override`` (which changes launch shapes and
+    row splits) clears it."""
+
+    LIMIT = 4096
+
+    def __init__(self):
+        super().__init__()
+        _lib.GEOMETRY_CACHES.append(self)
+
+    def cache_clear(self):
+        self.clear()
+
+    def put(self, key, plan):
+        if len(self) >= self.LIMIT:
+            self.clear()
+        self[key] = plan
+        return plan
+
+
 def launch(name: str, idx: int, *args) -> None:
     """Call entry point `name` with `args` followed by the handle of torch's
     current stream on device `idx` (every launching entry point takes the
@@ -114,3 +136,42 @@ def numel_prod(shape) -> int:
     for s in shape:
         n *= int(s)
     return n
+
+
+# (shape, dtype) -> (rows, cols, dtype code, entry point) of a last-axis
+# softmax / log_softmax on the unsplit row kernel, or False
+_SOFTMAX_PLANS = PlanCache()
+
+
+def softmax_rows_fast(x: torch.Tensor, log_mode: int):
+    """Softmax (log_mode 0) or log_softmax (1) over the last axis of a
+    contiguous tensor on the current GPU, in its own dtype, through a cached
+    plan; None where the call needs the wrapper's general path (other devices
+    or layouts, split rows, empty or 0-d tensors, unsupported dtypes, which
+    that path also rejects with the proper error)."""
+    dt = x.dtype
+    p = _SOFTMAX_PLANS.get((x.shape, dt))
+    if p is None:
+        p = _SOFTMAX_PLANS.put((x.shape, dt), _softmax_plan(x, dt))
+    if not p:
+        return None
+    dev = x.get_device()
+    if dev < 0 or dev != _raw_device() or not x.is_contiguous():
+        return None
+    rows, cols, code, fn = p
+    y = torch.empty_like(x)
+    rc = fn(x.data_ptr(), y.data_ptr(), rows, cols, code, code, log_mode, _raw_stream(dev))
+    if rc != 0:
+        raise _lib.VbhError("vbh_softmax_fwd", rc, _lib.last_error())
+    return y
+
+
+def _softmax_plan(x: torch.Tensor, dt):
+    code = FLOAT_CODES.get(dt)
+    if code is None or x.dim() == 0:
+        return False
+    cols = x.shape[-1]
+    rows = x.numel() // cols if cols else 0
+    if not rows or _lib.softmax_workspace_bytes(rows, cols, code):
+        return False
+    return (rows, cols, code, _lib.entry("vbh_softmax_fwd"))

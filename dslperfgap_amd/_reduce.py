@@ -98,58 +98,61 @@ def reduce(x: torch.Tensor, dims: list[int], keepdim: bool, op: int, out_dtype, 
     return vals, idx
 
 
-class _FastPlans(dict):
-    """Launch plans of single-dim reductions of contiguous inputs, keyed by
-    (shape, dim, keepdim, dtype, op, out_dtype); bounded, and cleared with the
-    geometry caches (``cache_clear``)."""
-
-    LIMIT = 4096
-
-    def cache_clear(self):
-        self.clear()
+# launch plans of single-dim reductions of contiguous inputs, keyed by
+# (shape, dim, keepdim, dtype, op)
+_FAST = _bridge.PlanCache()
 
 
-_FAST = _FastPlans()
-_lib.GEOMETRY_CACHES.append(_FAST)
-
-
-def fast_reduce(x: torch.Tensor, dim: int, keepdim: bool, op: int, out_dtype):
-    """reduce() over one int `dim` of a contiguous GPU tensor whose reduced
-    axis is not empty, through a cached plan: (values or None, indices or
-    None), or None where the call needs the general path (which also raises
-    the errors of invalid calls)."""
-    key = (x.shape, dim, keepdim, x.dtype, op, out_dtype)
-    p = _FAST.get(key)
+def fast_reduce(x: torch.Tensor, dim: int, keepdim: bool, op: int):
+    """reduce() over one int `dim` of a contiguous tensor on the current GPU
+    whose reduced axis is not empty, into outputs of the input's dtype, through
+    a cached plan: (values or None, indices or None), or None where the call
+    needs the general path (which also raises the errors of invalid calls).
+    At the reference's small shapes this host path is most of a call's
+    latency, so it makes one pass over the tensor's attributes and calls the
+    entry point directly."""
+    dt = x.dtype
+    p = _FAST.get((x.shape, dim, keepdim, dt, op))
     if p is None:
-        ndim = x.dim()
-        idt = _bridge.FLOAT_CODES.get(x.dtype)
-        odt = _bridge.FLOAT_CODES.get(out_dtype)
-        if ndim == 0 or idt is None or odt is None or not -ndim <= dim < ndim:
+        p = _fast_plan(x, dim, keepdim, dt, op)
+        if p is None:
             return None
-        d = dim % ndim
-        shape = tuple(x.shape)
-        if shape[d] == 0:
-            return None
-        outer, n, inner, _perm, out_shape, out_strides, ws, fn, name = plan(
-            shape, (d,), bool(keepdim), False, idt, op)
-        if ws or outer * inner == 0:
-            return None
-        p = (outer, n, inner, out_shape, out_strides, fn, name, idt, odt)
-        if len(_FAST) >= _FAST.LIMIT:
-            _FAST.clear()
-        _FAST[key] = p
     dev = x.get_device()
-    if dev < 0 or not x.is_contiguous():
+    if dev < 0 or dev != _raw_device() or not x.is_contiguous():
         return None
-    outer, n, inner, out_shape, out_strides, fn, name, idt, odt = p
-    if op == _lib.REDUCE_ARGMAX:
-        vals = None
-    elif out_dtype is x.dtype:
+    outer, n, inner, out_shape, out_strides, fn, name, idt = p
+    if op == REDUCE_MEAN:
         vals = x.new_empty_strided(out_shape, out_strides)
+        rc = fn(x.data_ptr(), vals.data_ptr(), None, outer, n, inner, idt, idt, op,
+                _raw_stream(dev))
+        idx = None
     else:
-        vals = x.new_empty_strided(out_shape, out_strides, dtype=out_dtype)
-    idx = None if op == _lib.REDUCE_MEAN else x.new_empty_strided(out_shape, out_strides,
-                                                                 dtype=torch.int64)
-    _bridge.launch_fn(fn, name, dev, x.data_ptr(), None if vals is None else vals.data_ptr(),
-                      None if idx is None else idx.data_ptr(), outer, n, inner, idt, odt, op)
+        vals = None if op == REDUCE_ARGMAX else x.new_empty_strided(out_shape, out_strides)
+        idx = x.new_empty_strided(out_shape, out_strides, dtype=torch.int64)
+        rc = fn(x.data_ptr(), None if vals is None else vals.data_ptr(), idx.data_ptr(), outer,
+                n, inner, idt, idt, op, _raw_stream(dev))
+    if rc != 0:
+        raise _lib.VbhError(name, rc, _lib.last_error())
     return vals, idx
+
+
+REDUCE_MEAN, REDUCE_ARGMAX = _lib.REDUCE_MEAN, _lib.REDUCE_ARGMAX
+_raw_device, _raw_stream = _bridge._raw_device, _bridge._raw_stream
+
+
+def _fast_plan(x: torch.Tensor, dim: int, keepdim: bool, dt, op: int):
+    """The cached plan of fast_reduce (None: the call takes the general path)."""
+    ndim = x.dim()
+    idt = _bridge.FLOAT_CODES.get(dt)
+    if ndim == 0 or idt is None or not -ndim <= dim < ndim:
+        return None
+    d = dim % ndim
+    shape = tuple(x.shape)
+    if shape[d] == 0:
+        return None
+    outer, n, inner, _perm, out_shape, out_strides, ws, fn, name = plan(
+        shape, (d,), bool(keepdim), False, idt, op)
+    if ws or outer * inner == 0:
+        return None
+    return _FAST.put((x.shape, dim, keepdim, dt, op),
+                     (outer, n, inner, out_shape, out_strides, fn, name, idt))

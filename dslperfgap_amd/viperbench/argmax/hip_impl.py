@@ -20,7 +20,7 @@ def argmax(input_tensor, dim, keepdim=False):
     """Returns the indices of the maximum values across a specified dimension."""
     x = input_tensor
     if type(dim) is int:  # the common call: a cached plan
-        r = _reduce.fast_reduce(x, dim, keepdim, _lib.REDUCE_ARGMAX, x.dtype)
+        r = _reduce.fast_reduce(x, dim, keepdim, _lib.REDUCE_ARGMAX)
         if r is not None:
             return r[1]
     if dim is None:

@@ -27,16 +27,9 @@ from dslperfgap_amd import _bridge, _lib  # noqa: E402
 def log_softmax(x, dim=-1, dtype=None):
     """Log-softmax: y = log(softmax(x, dim))."""
     if dtype is None and dim == -1:  # the common call, straight to the row kernel
-        dev = x.get_device()
-        idt = _bridge.FLOAT_CODES.get(x.dtype)
-        if dev >= 0 and idt is not None and x.dim() > 0 and x.is_contiguous():
-            cols = x.shape[-1]
-            rows = x.numel() // cols if cols else 0
-            if rows and not _lib.softmax_workspace_bytes(rows, cols, idt):
-                y = torch.empty_like(x)
-                _bridge.launch_fn(_lib.entry("vbh_softmax_fwd"), "vbh_softmax_fwd", dev,
-                                  x.data_ptr(), y.data_ptr(), rows, cols, idt, idt, 1)
-                return y
+        y = _bridge.softmax_rows_fast(x, 1)
+        if y is not None:
+            return y
     dev = _bridge.require_gpu("log_softmax", x)
     out_dtype = x.dtype if dtype is None else dtype
     if out_dtype != x.dtype:

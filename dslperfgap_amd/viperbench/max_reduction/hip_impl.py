@@ -22,7 +22,7 @@ def max_reduction(input, dim, keepdim=False):
     if not isinstance(input, torch.Tensor):
         raise TypeError('The input must be a torch.Tensor.')
     if type(dim) is int:  # the common call: a cached plan
-        r = _reduce.fast_reduce(input, dim, keepdim, _lib.REDUCE_MAX, input.dtype)
+        r = _reduce.fast_reduce(input, dim, keepdim, _lib.REDUCE_MAX)
         if r is not None:
             return r
     dims = _reduce.norm_dims(int(dim), input.dim(), "max_reduction")

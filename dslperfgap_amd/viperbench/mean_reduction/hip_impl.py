@@ -22,7 +22,7 @@ def mean_reduction(input_tensor, dim, keepdim=False, dtype=None):
     """Computes the mean value along specified dimensions."""
     x = input_tensor
     if dtype is None and type(dim) is int:  # the common call: a cached plan
-        r = _reduce.fast_reduce(x, dim, keepdim, _lib.REDUCE_MEAN, x.dtype)
+        r = _reduce.fast_reduce(x, dim, keepdim, _lib.REDUCE_MEAN)
         if r is not None:
             return r[0]
     out_dtype = x.dtype if dtype is None else dtype

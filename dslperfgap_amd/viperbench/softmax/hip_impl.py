@@ -21,6 +21,9 @@ from dslperfgap_amd import _bridge, _lib  # noqa: E402
 
 def softmax(x):
     """Softmax along the last dimension for any shape tensor."""
+    y = _bridge.softmax_rows_fast(x, 0)  # the common call, straight to the row kernel
+    if y is not None:
+        return y
     dev = _bridge.require_gpu("softmax", x)
     dt = _bridge.float_code(x, "softmax")
     x = x.contiguous()

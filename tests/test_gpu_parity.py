@@ -298,6 +298,45 @@ def test_empty_and_degenerate():
     check(logsumexp(*cuda(s.reshape(1))), ref.logsumexp(s.reshape(1)), torch.float32)
 
 
+def test_cached_plans_follow_overrides_layouts_and_dtypes():
+    """The wrappers' per-shape launch plans: a shape planned before a geometry
+    override and called under it (and the reverse), contiguous tensors whose
+    size-1 dims carry odd strides, and one shape in several dtypes."""
+    from dslperfgap_amd.viperbench.max_reduction.hip_impl import max_reduction
+    from dslperfgap_amd.viperbench.mean_reduction.hip_impl import mean_reduction
+
+    x = 3 * torch.randn(7, 131072, generator=_g(112))  # a split softmax / reduction shape
+    xd = x.to(DEV)
+    for _ in range(2):  # plans made without, then used with an override; then the reverse
+        check(softmax(xd), ref.softmax(x), torch.float32, what="softmax, split shape")
+        check(log_softmax(xd), ref.log_softmax(x), torch.float32, what="log_softmax, split shape")
+        check(mean_reduction(xd, 1), ref.mean_reduction(x, 1), torch.float32, what="mean")
+        try:
+            _lib.tune_override(_lib.OP_SOFTMAX, 256, 256, 0)
+            _lib.tune_override(_lib.OP_REDUCE, 64, 256, 0)
+            check(softmax(xd), ref.softmax(x), torch.float32, what="softmax, overridden")
+            check(log_softmax(xd), ref.log_softmax(x), torch.float32, what="log_softmax, overridden")
+            check(mean_reduction(xd, 1), ref.mean_reduction(x, 1), torch.float32, what="mean, ov")
+            assert torch.equal(argmax(xd, 1).cpu(), ref.argmax(x, 1))
+        finally:
+            _lib.tune_override(_lib.OP_SOFTMAX, 0, 0, 0)
+            _lib.tune_override(_lib.OP_REDUCE, 0, 0, 0)
+    base = torch.randn(4 * 1000, generator=_g(113))
+    odd = base.to(DEV).as_strided((4, 1, 1000), (1000, 7, 1))  # contiguous: size-1 dim ignored
+    assert odd.is_contiguous()
+    want = base.view(4, 1, 1000)
+    for got, exp in ((softmax(odd), ref.softmax(want)), (log_softmax(odd), ref.log_softmax(want)),
+                     (mean_reduction(odd, 2), ref.mean_reduction(want, 2))):
+        check(got.reshape(exp.shape), exp, torch.float32, what="odd size-1 stride")
+    v, i = max_reduction(odd, -1, True)
+    rv, ri = ref.max_reduction(want, -1, True)
+    assert torch.equal(v.cpu(), rv) and torch.equal(i.cpu(), ri)
+    for dt in (torch.float32, torch.float16, torch.bfloat16):  # one shape, three plans
+        y = torch.randn(33, 500, generator=_g(114)).to(dt)
+        check(softmax(*cuda(y)), ref.softmax(y), dt, what=f"softmax {dt}")
+        check(mean_reduction(*cuda(y), 1), ref.mean_reduction(y, 1), dt, what=f"mean {dt}")
+
+
 # ---------------------------------------------------------------------------
 # launch-geometry overrides: every group size must give the same answer
 # ---------------------------------------------------------------------------
