@@ -28,21 +28,26 @@ def layer_norm(x, weight, bias, eps=1e-5):
     if eps != 1e-5:
         raise ValueError(f"Only eps=1e-5 is supported (got {eps}). "
                          "The Triton kernel hardcodes eps=1e-5.")
-    # the common call: contiguous x, weight and bias of one dtype on one GPU,
-    # normalized over the last dim -- straight to the row kernel
-    dt = _bridge.FLOAT_CODES.get(x.dtype)
-    if (dt is not None and bias is not None and weight.dim() == 1 and x.dim() > 0 and
-            weight.dtype is x.dtype and bias.dtype is x.dtype and
-            x.shape[-1] == weight.shape[0] and bias.shape == weight.shape):
-        dev = x.get_device()
-        if (dev >= 0 and weight.get_device() == dev and bias.get_device() == dev and
-                x.is_contiguous() and weight.is_contiguous() and bias.is_contiguous()):
-            cols = weight.shape[0]
-            y = torch.empty_like(x)
-            _bridge.launch_fn(_lib.entry("vbh_layer_norm_fwd"), "vbh_layer_norm_fwd", dev,
-                              x.data_ptr(), weight.data_ptr(), bias.data_ptr(), y.data_ptr(),
-                              x.numel() // cols if cols else 0, cols, 1e-5, dt, dt)
-            return y
+    # the common call: contiguous x, weight and bias of one dtype on the current
+    # GPU, normalized over the last dim -- straight to the row kernel
+    dt = x.dtype
+    if bias is not None and weight.dtype is dt and bias.dtype is dt:
+        key = (x.shape, weight.shape, bias.shape, dt)
+        p = _PLANS.get(key)
+        if p is None:
+            p = _PLANS.put(key, _plan(x, weight, bias))
+        if p:
+            dev = x.get_device()
+            if (dev >= 0 and dev == _raw_device() and weight.get_device() == dev and
+                    bias.get_device() == dev and x.is_contiguous() and
+                    weight.is_contiguous() and bias.is_contiguous()):
+                rows, cols, code, fn = p
+                y = torch.empty_like(x)
+                rc = fn(x.data_ptr(), weight.data_ptr(), bias.data_ptr(), y.data_ptr(), rows,
+                        cols, 1e-5, code, code, _raw_stream(dev))
+                if rc != 0:
+                    raise _lib.VbhError("vbh_layer_norm_fwd", rc, _lib.last_error())
+                return y
     dev = _bridge.require_gpu("layer_norm", x, weight, bias)
     norm_shape = tuple(weight.shape)
     k = len(norm_shape)
@@ -66,3 +71,18 @@ def layer_norm(x, weight, bias, eps=1e-5):
     _bridge.launch("vbh_layer_norm_fwd", dev, _bridge.ptr(x), _bridge.ptr(w), _bridge.ptr(b),
                    _bridge.ptr(y), rows, cols, float(eps), dt, wdt)
     return y
+
+
+# (x shape, weight shape, bias shape, dtype) -> (rows, cols, dtype code, entry
+# point) of a last-dim LayerNorm with weight and bias of x's dtype, or False
+_PLANS = _bridge.PlanCache()
+_raw_device, _raw_stream = _bridge._raw_device, _bridge._raw_stream
+
+
+def _plan(x, weight, bias):
+    code = _bridge.FLOAT_CODES.get(x.dtype)
+    if (code is None or x.dim() == 0 or weight.dim() != 1 or
+            x.shape[-1] != weight.shape[0] or bias.shape != weight.shape):
+        return False
+    cols = weight.shape[0]
+    return (x.numel() // cols if cols else 0, cols, code, _lib.entry("vbh_layer_norm_fwd"))

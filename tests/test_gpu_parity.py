@@ -335,6 +335,15 @@ def test_cached_plans_follow_overrides_layouts_and_dtypes():
         y = torch.randn(33, 500, generator=_g(114)).to(dt)
         check(softmax(*cuda(y)), ref.softmax(y), dt, what=f"softmax {dt}")
         check(mean_reduction(*cuda(y), 1), ref.mean_reduction(y, 1), dt, what=f"mean {dt}")
+        w, b = (1 + 0.1 * torch.randn(500, generator=_g(115))), 0.1 * torch.randn(500, generator=_g(116))
+        for wdt in (dt, torch.float32):  # one x shape with weights of x's dtype, then fp32
+            args = (y, w.to(wdt), b.to(wdt))
+            check(layer_norm(*cuda(*args)), ref.layer_norm(*args), dt, what=f"LN {dt} w {wdt}")
+    y = torch.randn(12, 500, generator=_g(117))
+    yd = y.to(DEV)
+    check(layer_norm(yd[:6], w.to(DEV), b.to(DEV)), ref.layer_norm(y[:6], w, b), torch.float32)
+    check(layer_norm(yd[::2], w.to(DEV), b.to(DEV)), ref.layer_norm(y[::2], w, b), torch.float32,
+          what="LN strided rows, shape of a planned call")
 
 
 # ---------------------------------------------------------------------------
