@@ -37,7 +37,7 @@ ABI_VERSION = 1
 # element type codes (VBH_DTYPE_*)
 F32, F16, BF16, I32, I64 = 0, 1, 2, 3, 4
 # argument-error codes (VBH_E_*)
-E_INVALID, E_DTYPE, E_RANGE = -1, -2, -3
+E_INVALID, E_DTYPE, E_RANGE, E_UNSUPPORTED = -1, -2, -3, -4
 # op codes for vbh_tune_override (VBH_OP_*)
 OP_LAYER_NORM, OP_RMS_NORM, OP_SOFTMAX, OP_LOGSUMEXP, OP_CROSS_ENTROPY, OP_REDUCE = 0, 1, 2, 3, 4, 5
 # reduction codes (VBH_REDUCE_*)
@@ -90,6 +90,8 @@ SIGNATURES = {
     "vbh_stream_read": (_i32, [_vp, _i64, _vp, _i64, _vp]),
     "vbh_stream_read_partial_bytes": (_i64, [_i64]),
     "vbh_tune_override": (_i32, [_i32, _i32, _i32, _i32]),
+    "vbh_debug_bounds": (_i32, [ctypes.POINTER(ctypes.c_int64), ctypes.c_char_p, _i64, _i32]),
+    "vbh_debug_bounds_slack": (_i32, [_i64]),
 }
 
 
@@ -213,6 +215,23 @@ def tune_override(op: int, tpr: int = 0, block: int = 0, flags: int = 0) -> None
     cross_entropy_workspace_bytes.cache_clear()
     for cache in GEOMETRY_CACHES:
         cache.cache_clear()
+
+
+def debug_bounds(clear: bool = True) -> tuple:
+    """(failed checks, "<file>:<line>" of the first failing buffer or "") of the
+    bounds-checked debug library (libvbhip_debug.so, selected with VBHIP_LIB);
+    waits for the device.  The release library raises VbhError
+    (VBH_E_UNSUPPORTED)."""
+    n = ctypes.c_int64(0)
+    where = ctypes.create_string_buffer(256)
+    call("vbh_debug_bounds", ctypes.byref(n), where, len(where), int(clear))
+    return n.value, where.value.decode()
+
+
+def debug_bounds_slack(nbytes: int) -> None:
+    """Take `nbytes` off the end of every buffer's allowed extent in the
+    bounds-checked library (0 restores)."""
+    call("vbh_debug_bounds_slack", int(nbytes))
 
 
 @functools.lru_cache(maxsize=4096)

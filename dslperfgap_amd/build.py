@@ -6,12 +6,21 @@ binding of its launching entry points (``csrc/vbhfast.c``) is then compiled
 with the host C compiler into ``dslperfgap_amd/_vbhfast*.so``, linked against
 that library.  Both are rebuilt on every call (the caller asked for a build).
 
-Provenance: the build writes ``libvbhip.srchash`` next to the library, the
-SHA-256 of every file under ``csrc/`` and ``include/`` (names and contents) it
-was built from.  ``_lib.lib()`` refuses a library whose hash differs from the
-sources on disk, so a stale binary cannot run in place of the code in the tree.
+The same sources are also compiled with ``-DVBH_DEBUG_BOUNDS`` into
+``_build/debug/`` and linked into ``libvbhip_debug.so``: the bounds-checked
+debug build, in which every kernel checks each global-memory access against
+the extent of its buffer before making it (``vbh_debug_bounds`` reads the
+count of failed checks; ``VBHIP_LIB`` selects that library for a run).  Its
+release counterpart is the same code with every check compiled away.
 
-Usage: ``python -m dslperfgap_amd.build`` or ``build()`` from Python.
+Provenance: the build writes ``libvbhip.srchash`` (and
+``libvbhip_debug.srchash``) next to the libraries, the SHA-256 of every file
+under ``csrc/`` and ``include/`` (names and contents) they were built from.
+``_lib.lib()`` refuses a library whose hash differs from the sources on disk,
+so a stale binary cannot run in place of the code in the tree.
+
+Usage: ``python -m dslperfgap_amd.build [--no-debug]`` or ``build()`` from
+Python.
 """
 from __future__ import annotations
 
@@ -29,6 +38,8 @@ CSRC = PKG_DIR / "csrc"
 BUILD_DIR = PKG_DIR / "_build"
 LIB_PATH = PKG_DIR / "libvbhip.so"
 HASH_PATH = PKG_DIR / "libvbhip.srchash"
+DEBUG_LIB_PATH = PKG_DIR / "libvbhip_debug.so"
+DEBUG_HASH_PATH = PKG_DIR / "libvbhip_debug.srchash"
 FAST_PATH = PKG_DIR / ("_vbhfast" + sysconfig.get_config_var("EXT_SUFFIX"))
 REPO_ROOT = PKG_DIR.parent
 
@@ -67,9 +78,11 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found: install ROCm or set HIPCC")
 
 
-def _compile(hipcc: str, src: Path) -> Path:
-    obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [hipcc, *DEVICE_FLAGS, "-c", str(src), "-o", str(obj)]
+def _compile(hipcc: str, src: Path, debug: bool = False) -> Path:
+    out_dir = BUILD_DIR / "debug" if debug else BUILD_DIR
+    obj = out_dir / (src.stem + ".o")
+    cmd = [hipcc, *DEVICE_FLAGS, *(["-DVBH_DEBUG_BOUNDS"] if debug else []), "-c", str(src),
+           "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")
@@ -81,28 +94,41 @@ def _compile(hipcc: str, src: Path) -> Path:
     return obj
 
 
-def build(verbose: bool = True) -> Path:
-    """Compile every HIP source for gfx950 and link libvbhip.so; return its path."""
-    hipcc = _hipcc()
-    digest = source_hash()
-    HASH_PATH.unlink(missing_ok=True)  # no hash while the library is being replaced
-    BUILD_DIR.mkdir(exist_ok=True)
-    sources = sorted(CSRC.glob("*.hip"))
-    if not sources:
-        raise RuntimeError(f"no HIP sources under {CSRC}")
-    jobs = min(len(sources), max(1, min(16, os.cpu_count() or 1)))
-    with ThreadPoolExecutor(max_workers=jobs) as pool:
-        objs = list(pool.map(lambda s: _compile(hipcc, s), sources))
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+def _link(hipcc: str, objs: list, lib_path: Path) -> None:
+    tmp = lib_path.with_suffix(".so.tmp")
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, LIB_PATH)
+        raise RuntimeError(f"link of {lib_path.name} failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, lib_path)
+
+
+def build(verbose: bool = True, debug: bool = True) -> Path:
+    """Compile every HIP source for gfx950 and link libvbhip.so (and, with
+    `debug`, the bounds-checked libvbhip_debug.so); return the release path."""
+    hipcc = _hipcc()
+    digest = source_hash()
+    flavors = [(False, LIB_PATH, HASH_PATH)] + ([(True, DEBUG_LIB_PATH, DEBUG_HASH_PATH)]
+                                                if debug else [])
+    for _, _, hash_path in flavors:  # no hash while a library is being replaced
+        hash_path.unlink(missing_ok=True)
+    BUILD_DIR.mkdir(exist_ok=True)
+    (BUILD_DIR / "debug").mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    if not sources:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    units = [(src, dbg) for dbg, _, _ in flavors for src in sources]
+    jobs = min(len(units), max(1, min(16, os.cpu_count() or 1)))
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        objs = list(pool.map(lambda u: _compile(hipcc, *u), units))
+    for i, (_, lib_path, _) in enumerate(flavors):
+        _link(hipcc, objs[i * len(sources):(i + 1) * len(sources)], lib_path)
     build_fast()
-    HASH_PATH.write_text(digest + "\n")
+    for _, _, hash_path in flavors:
+        hash_path.write_text(digest + "\n")
     if verbose:
-        print(f"built {LIB_PATH} from {len(sources)} sources, and {FAST_PATH.name}",
+        names = ", ".join(lib.name for _, lib, _ in flavors)
+        print(f"built {names} from {len(sources)} sources each, and {FAST_PATH.name}",
               file=sys.stderr)
     return LIB_PATH
 
@@ -125,4 +151,4 @@ def build_fast() -> Path:
 
 
 if __name__ == "__main__":
-    build()
+    build(debug="--no-debug" not in sys.argv[1:])

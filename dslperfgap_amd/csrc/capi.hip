@@ -3,11 +3,13 @@
 // interface each entry point stands in for are in include/vbhip.h.
 #include <stdarg.h>
 #include <stdio.h>
+#include <string.h>
 
 #include <algorithm>
 #include <atomic>
 #include <mutex>
 #include <unordered_map>
+#include <vector>
 
 #include "../../include/vbhip.h"
 #include "vbh_device.h"
@@ -523,6 +525,28 @@ static int noalloc_scratch(void** out) {
   *out = g_scratch_ptr[dev];
   return 0;
 }
+
+#ifdef VBH_DEBUG_BOUNDS
+// The debug bounds records of the library's translation units (each registers
+// its reader at load time, from its static initialisation; vbh_device.h).
+struct BoundsTu {
+  const char* file;
+  BoundsRecordFn fn;
+};
+static std::mutex& bounds_mu() {
+  static std::mutex mu;
+  return mu;
+}
+static std::vector<BoundsTu>& bounds_tus() {
+  static std::vector<BoundsTu> tus;
+  return tus;
+}
+int register_bounds_record(const char* file, BoundsRecordFn fn) {
+  std::lock_guard<std::mutex> lock(bounds_mu());
+  bounds_tus().push_back(BoundsTu{file, fn});
+  return 1;
+}
+#endif
 
 }  // namespace vbh
 
@@ -1118,6 +1142,55 @@ int vbh_stream_read(const void* src, int64_t bytes, void* partial, int64_t parti
   return hip_status(
       launch_stream_read(src, partial, bytes, grid, static_cast<hipStream_t>(stream)),
       "stream_read launch");
+}
+
+int vbh_debug_bounds(int64_t* failed, char* where, int64_t where_len, int clear) {
+#ifndef VBH_DEBUG_BOUNDS
+  (void)failed, (void)where, (void)where_len, (void)clear;
+  return fail(VBH_E_UNSUPPORTED,
+              "debug_bounds: this library was built without VBH_DEBUG_BOUNDS "
+              "(libvbhip_debug.so is the bounds-checked build)");
+#else
+  if (failed == nullptr) return fail(VBH_E_INVALID, "debug_bounds: null count pointer");
+  if (where != nullptr && where_len > 0) where[0] = '\0';
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_status(e, "debug_bounds: hipDeviceSynchronize");
+  std::lock_guard<std::mutex> lock(bounds_mu());
+  int64_t total = 0;
+  for (const BoundsTu& tu : bounds_tus()) {
+    unsigned n = 0, line = 0;
+    e = tu.fn(&n, &line, nullptr, clear != 0);
+    if (e != hipSuccess) return hip_status(e, "debug_bounds: reading a record");
+    if (n != 0 && total == 0 && where != nullptr && where_len > 0) {
+      const char* base = strrchr(tu.file, '/');
+      snprintf(where, static_cast<size_t>(std::min<int64_t>(where_len, 1 << 20)), "%s:%u",
+               base != nullptr ? base + 1 : tu.file, line);
+    }
+    total += n;
+  }
+  *failed = total;
+  return hip_status(hipSuccess, "");
+#endif
+}
+
+int vbh_debug_bounds_slack(int64_t bytes) {
+#ifndef VBH_DEBUG_BOUNDS
+  (void)bytes;
+  return fail(VBH_E_UNSUPPORTED,
+              "debug_bounds_slack: this library was built without VBH_DEBUG_BOUNDS");
+#else
+  if (bytes < 0) return fail(VBH_E_INVALID, "debug_bounds_slack: negative byte count");
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_status(e, "debug_bounds_slack: hipDeviceSynchronize");
+  std::lock_guard<std::mutex> lock(bounds_mu());
+  const long long slack = static_cast<long long>(bytes);
+  for (const BoundsTu& tu : bounds_tus()) {
+    unsigned n = 0, line = 0;
+    e = tu.fn(&n, &line, &slack, false);
+    if (e != hipSuccess) return hip_status(e, "debug_bounds_slack: setting a slack");
+  }
+  return hip_status(hipSuccess, "");
+#endif
 }
 
 }  // extern "C"

@@ -67,17 +67,30 @@ CeScalars make_scalars(float smoothing, float logit_scale, float lse_square_scal
   return c;
 }
 
-__device__ __forceinline__ int64_t read_label(const void* labels, int label_i64, int64_t row) {
+__device__ __forceinline__ int64_t read_label(const void* labels, int label_i64, int64_t row,
+                                              const Span& s) {
+  if (!VBH_IN_SPAN(s, static_cast<const char*>(labels) + row * (label_i64 ? 8 : 4),
+                   label_i64 ? 8 : 4))
+    return 0;
   return label_i64 ? static_cast<const int64_t*>(labels)[row]
                    : static_cast<int64_t>(static_cast<const int32_t*>(labels)[row]);
 }
+
+// The labels buffer: n_rows int32 or int64 values.
+#define VBH_LABEL_SPAN(labels, label_i64, n_rows) \
+  VBH_SPAN(static_cast<const char*>(labels), (n_rows) * ((label_i64) ? 8 : 4))
+
+// The three per-segment outputs (loss, lse, z_loss) have one extent.
+struct CeOutSpans {
+  Span loss, lse, z;
+};
 
 // Per-segment epilogue (pytorch_impl.py:37-76), executed by one lane.
 __device__ __forceinline__ void ce_store(float lse, float sum_logits, bool in_block,
                                          float logit_label, bool ignored,
                                          const CeScalars& c, float* loss, float* lse_out,
-                                         float* z_out, int64_t idx) {
-  lse_out[idx] = lse;
+                                         float* z_out, int64_t idx, const CeOutSpans& so) {
+  if (VBH_IN_SPAN(so.lse, lse_out + idx, sizeof(float))) lse_out[idx] = lse;
   float l, z;
   if (ignored) {
     l = 0.f;
@@ -100,8 +113,8 @@ __device__ __forceinline__ void ce_store(float lse, float sum_logits, bool in_bl
       z = 0.f;
     }
   }
-  loss[idx] = l;
-  z_out[idx] = z;
+  if (VBH_IN_SPAN(so.loss, loss + idx, sizeof(float))) loss[idx] = l;
+  if (VBH_IN_SPAN(so.z, z_out + idx, sizeof(float))) z_out[idx] = z;
 }
 
 // Segments whose start is not on a 16-byte boundary (rows not a multiple of
@@ -140,6 +153,9 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
   const int cb = static_cast<int>(seg - row * ncb);
   const int col0 = cb * bs;
   const int col_end = min(n_cols, col0 + bs);
+  const Span sx = VBH_SPAN(logits, strided_extent(n_rows, ld, n_cols));
+  const Span sb = VBH_LABEL_SPAN(labels, label_i64, n_rows);
+  const CeOutSpans so{VBH_SPAN(loss, nseg), VBH_SPAN(lse_out, nseg), VBH_SPAN(z_out, nseg)};
   const T* lr = logits + row * ld;
   const int64_t sstart = row * ld + col0;
   const MisSeg ms = MIS ? mis_seg<V>(sstart, col_end - col0) : MisSeg{0, (col_end - col0) / V, 0};
@@ -150,25 +166,26 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
   bool ignored = false, in_block = false;
   float logit_label = 0.f;
   if (live && g == 0) {
-    const int64_t label = read_label(labels, label_i64, row);
+    const int64_t label = read_label(labels, label_i64, row, sb);
     ignored = label == c.ignored_index;
     const int64_t adj = label - c.class_start;
     in_block = adj >= col0 && adj < col_end;
-    if (!ignored && in_block) logit_label = static_cast<float>(lr[adj]) * c.logit_scale;
+    if (!ignored && in_block && VBH_IN_SPAN(sx, lr + adj, sizeof(T)))
+      logit_label = static_cast<float>(lr[adj]) * c.logit_scale;
   }
 
   RT xr[IT];
 #pragma unroll
   for (int i = 0; i < IT; ++i) {
     const int j = i * tpr + g;
-    if (j < nvec) xr[i] = load_raw<T, V, NT>(lb + static_cast<int64_t>(j) * V);
+    if (j < nvec) xr[i] = load_raw<T, V, NT>(lb + static_cast<int64_t>(j) * V, sx);
     else xr[i] = RT{};
   }
   const float scale = c.logit_scale;
   const bool hv = MIS && g < ms.head, tv = MIS && g < ms.tail;
   float hr = 0.f, tr = 0.f;  // raw head / tail logits
-  if (hv) hr = static_cast<float>(logits[sstart + g]);
-  if (tv) tr = static_cast<float>(lb[static_cast<int64_t>(nvec) * V + g]);
+  if (hv) load_f32<T, 1>(logits + sstart + g, &hr, sx);
+  if (tv) load_f32<T, 1>(lb + static_cast<int64_t>(nvec) * V + g, &tr, sx);
   const float hx = hr * scale, tx = tr * scale;
 
   float mx[V];
@@ -236,7 +253,7 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
     // all -inf (the sum of logits is -inf, not NaN): -inf in a first stage
     if (c.empty_neg_inf && m == kNegInf && sum_logits == sum_logits) lse = kNegInf;
     ce_store(lse, sum_logits, in_block, logit_label, ignored, c, loss, lse_out, z_out,
-             static_cast<int64_t>(cb) * n_rows + row);
+             static_cast<int64_t>(cb) * n_rows + row, so);
   }
 }
 
@@ -256,12 +273,16 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_stream(
   const int col_end = min(n_cols, col0 + bs);
   const int nvec = (col_end - col0) / V;
   const T* lr = logits + row * ld + col0;
+  const Span sx = VBH_SPAN(logits, strided_extent(n_rows, ld, n_cols));
+  const Span sb = VBH_LABEL_SPAN(labels, label_i64, n_rows);
+  const CeOutSpans so{VBH_SPAN(loss, n_rows * ncb), VBH_SPAN(lse_out, n_rows * ncb),
+                      VBH_SPAN(z_out, n_rows * ncb)};
 
   // per-thread running max (NaN ignored), rescaled sum, NaN-propagating sum of logits
   float m = kNegInf, s = 0.f, sl = 0.f, nan = 0.f;
   for (int j = threadIdx.x; j < nvec; j += tpr) {
     float v[V];
-    load_f32<T, V>(lr + static_cast<int64_t>(j) * V, v);
+    load_f32<T, V>(lr + static_cast<int64_t>(j) * V, v, sx);
     float cm = kNegInf;
 #pragma unroll
     for (int k = 0; k < V; ++k) {
@@ -292,15 +313,15 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_stream(
   const bool has_nan = nan != 0.f || (gl != gl);
   float lse = (has_nan || !finite) ? __builtin_nanf("") : fast_log(gs) + gm;
   if (c.empty_neg_inf && !has_nan && gm == kNegInf) lse = kNegInf;  // as in ce_fwd_rows
-  const int64_t label = read_label(labels, label_i64, row);
+  const int64_t label = read_label(labels, label_i64, row, sb);
   const bool ignored = label == c.ignored_index;
   const int64_t adj = label - c.class_start;
   const bool in_block = adj >= col0 && adj < col_end;
   float logit_label = 0.f;
-  if (!ignored && in_block)
+  if (!ignored && in_block && VBH_IN_SPAN(sx, logits + row * ld + adj, sizeof(T)))
     logit_label = static_cast<float>(logits[row * ld + adj]) * c.logit_scale;
   ce_store(lse, gl, in_block, logit_label, ignored, c, loss, lse_out, z_out,
-           static_cast<int64_t>(cb) * n_rows + row);
+           static_cast<int64_t>(cb) * n_rows + row, so);
 }
 
 // Second stage of a split row (one column block per row, cut into `segs`
@@ -320,25 +341,33 @@ __global__ __launch_bounds__(256) void ce_combine(
     int segs, CeScalars c) {
   const int64_t row = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (row >= n_rows) return;
+  const Span ssl = VBH_SPAN(seg_loss, segs * n_rows), sse = VBH_SPAN(seg_lse, segs * n_rows);
+  const Span sb = VBH_LABEL_SPAN(labels, label_i64, n_rows);
+  const CeOutSpans so{VBH_SPAN(loss, n_rows), VBH_SPAN(lse_out, n_rows), VBH_SPAN(z_out, n_rows)};
   float mx = kNegInf, rest = 0.f;
   bool nan = false;
   for (int k = 0; k < segs; ++k) {
-    const float v = seg_lse[static_cast<int64_t>(k) * n_rows + row];
+    float v, sl;
+    load_f32<float, 1>(seg_lse + static_cast<int64_t>(k) * n_rows + row, &v, sse);
     nan |= v != v;
     mx = fmaxf(mx, v);
-    rest += seg_loss[static_cast<int64_t>(k) * n_rows + row];
+    load_f32<float, 1>(seg_loss + static_cast<int64_t>(k) * n_rows + row, &sl, ssl);
+    rest += sl;
   }
   float lse;
   if (nan || mx == kNegInf) {
     lse = __builtin_nanf("");
   } else {
     float s = 0.f;
-    for (int k = 0; k < segs; ++k)
-      s += fast_exp(seg_lse[static_cast<int64_t>(k) * n_rows + row] - mx);
+    for (int k = 0; k < segs; ++k) {
+      float v;
+      load_f32<float, 1>(seg_lse + static_cast<int64_t>(k) * n_rows + row, &v, sse);
+      s += fast_exp(v - mx);
+    }
     lse = fast_log(s) + mx;
   }
-  lse_out[row] = lse;
-  const int64_t label = read_label(labels, label_i64, row);
+  if (VBH_IN_SPAN(so.lse, lse_out + row, sizeof(float))) lse_out[row] = lse;
+  const int64_t label = read_label(labels, label_i64, row, sb);
   float l = 0.f, z = 0.f;
   if (label != c.ignored_index) {
     const int64_t adj = label - c.class_start;
@@ -351,8 +380,8 @@ __global__ __launch_bounds__(256) void ce_combine(
       l = rest;
     }
   }
-  loss[row] = l;
-  z_out[row] = z;
+  if (VBH_IN_SPAN(so.loss, loss + row, sizeof(float))) loss[row] = l;
+  if (VBH_IN_SPAN(so.z, z_out + row, sizeof(float))) z_out[row] = z;
 }
 
 // Backward: elementwise over the rows.  One 256-lane workgroup per tile of
@@ -402,14 +431,21 @@ __global__ __launch_bounds__(kBwdLanes) void ce_bwd_tiles(
   }
   const T* lr = logits + in0 + head;     // 16-byte aligned body
   T* dr = dlogits + row * ld_out + head;
+  // the grid is the row count times tiles_per_row
+  [[maybe_unused]] const int64_t n_rows = gridDim.x / tiles_per_row;
+  const Span sx = VBH_SPAN(logits, strided_extent(n_rows, ld_in, n_cols));
+  const Span sd = VBH_SPAN(dlogits, strided_extent(n_rows, ld_out, n_cols));
+  const Span sdl = VBH_SPAN(dloss, strided_extent(n_rows, dloss_stride, 1));
+  const Span sl = VBH_SPAN(lse, n_rows), sb = VBH_LABEL_SPAN(labels, label_i64, n_rows);
   const int j = j0 + static_cast<int>(threadIdx.x);
   // the tile's logits load goes out first; the row's label, dloss and lse
   // (independent loads: dloss is read for ignored rows too) while it is in flight
   typename Raw<T, V>::type r{};
-  if (j < nvec) r = load_raw<T, V, SP != kStoreCached>(lr + static_cast<int64_t>(j) * V);
-  const int64_t label = read_label(labels, label_i64, row);
-  const float dlv = dloss[row * dloss_stride];
-  const float lse_r = lse[row];
+  if (j < nvec) r = load_raw<T, V, SP != kStoreCached>(lr + static_cast<int64_t>(j) * V, sx);
+  const int64_t label = read_label(labels, label_i64, row, sb);
+  float dlv, lse_r;
+  load_f32<float, 1>(dloss + row * dloss_stride, &dlv, sdl);
+  load_f32<float, 1>(lse + row, &lse_r, sl);
   const float dl = label != c.ignored_index ? dlv : 0.f;
   const int64_t adj = label - c.class_start;
   CeBwdRow b;
@@ -428,18 +464,23 @@ __global__ __launch_bounds__(kBwdLanes) void ce_bwd_tiles(
     float o[V];
 #pragma unroll
     for (int k = 0; k < V; ++k) o[k] = ce_grad(raw_at<T, V>(r, k), rel == k, b, c);
-    out.template store<V>(dr + static_cast<int64_t>(j) * V, static_cast<int>(threadIdx.x) * V, o);
+    out.template store<V>(dr + static_cast<int64_t>(j) * V, static_cast<int>(threadIdx.x) * V, o,
+                          sd);
   }
   if (MIS && tix == 0) {
     const int t = static_cast<int>(threadIdx.x);
     if (t < head) {
-      const float o = ce_grad(static_cast<float>(logits[in0 + t]), adj == t, b, c);
-      store_from_f32<T, 1>(dr - head + t, &o);
+      float v;
+      load_f32<T, 1>(logits + in0 + t, &v, sx);
+      const float o = ce_grad(v, adj == t, b, c);
+      store_from_f32<T, 1>(dr - head + t, &o, sd);
     }
     if (t < tail) {
       const int64_t k = static_cast<int64_t>(nvec) * V + t;
-      const float o = ce_grad(static_cast<float>(lr[k]), adj == head + k, b, c);
-      store_from_f32<T, 1>(dr + k, &o);
+      float v;
+      load_f32<T, 1>(lr + k, &v, sx);
+      const float o = ce_grad(v, adj == head + k, b, c);
+      store_from_f32<T, 1>(dr + k, &o, sd);
     }
   }
 }

@@ -86,13 +86,13 @@ __device__ __forceinline__ ValIdx group_allreduce_vi(ValIdx a, int tpr, float* l
 
 template <typename T, int V, int OP>
 __device__ __forceinline__ void write_result(void* vals, int64_t* idx, int64_t o, float sum_or_v,
-                                             int i, int n) {
+                                             int i, int n, const Span& sv, const Span& si) {
   if constexpr (OP == 0) {
     const float m = sum_or_v / static_cast<float>(n);
-    store_from_f32<T, 1>(static_cast<T*>(vals) + o, &m);
+    store_from_f32<T, 1>(static_cast<T*>(vals) + o, &m, sv);
   } else {
-    if constexpr (OP == 1) store_from_f32<T, 1>(static_cast<T*>(vals) + o, &sum_or_v);
-    idx[o] = i;
+    if constexpr (OP == 1) store_from_f32<T, 1>(static_cast<T*>(vals) + o, &sum_or_v, sv);
+    if (VBH_IN_SPAN(si, idx + o, sizeof(int64_t))) idx[o] = i;
   }
 }
 
@@ -113,6 +113,8 @@ __global__ __launch_bounds__(kMaxBlock) void reduce_rows(const Ti* __restrict__ 
   int64_t row = static_cast<int64_t>(blockIdx.x) * gs.per_block + gs.sub;
   const bool live = row < rows;
   if (!live) row = rows - 1;
+  const Span sx = VBH_SPAN(x, rows * n);
+  const Span sv = VBH_SPAN(static_cast<To*>(vals), rows), si = VBH_SPAN(idx, rows);
   const int64_t start = row * n;
   int head = 0, nvec = n / V, tail = 0;
   if constexpr (MIS) {
@@ -138,7 +140,7 @@ __global__ __launch_bounds__(kMaxBlock) void reduce_rows(const Ti* __restrict__ 
 #pragma unroll
       for (int c = 0; c < kChunk; ++c) {
         const int j = base + c * tpr;
-        r[c] = j < nvec ? load_raw<Ti, V, true>(xr + static_cast<int64_t>(j) * V) : RT{};
+        r[c] = j < nvec ? load_raw<Ti, V, true>(xr + static_cast<int64_t>(j) * V, sx) : RT{};
       }
 #pragma unroll
       for (int c = 0; c < kChunk; ++c)
@@ -148,10 +150,18 @@ __global__ __launch_bounds__(kMaxBlock) void reduce_rows(const Ti* __restrict__ 
     float s = 0.f;
 #pragma unroll
     for (int k = 0; k < V; ++k) s += acc[k];
-    if (hv) s += static_cast<float>(x[start + g]);
-    if (tv) s += static_cast<float>(x[start + tail0 + g]);
+    if (hv) {
+      float v;
+      load_f32<Ti, 1>(x + start + g, &v, sx);
+      s += v;
+    }
+    if (tv) {
+      float v;
+      load_f32<Ti, 1>(x + start + tail0 + g, &v, sx);
+      s += v;
+    }
     s = group_allreduce<Sum>(s, tpr, lds);
-    if (live && g == 0) write_result<To, V, OP>(vals, idx, row, s, 0, n);
+    if (live && g == 0) write_result<To, V, OP>(vals, idx, row, s, 0, n, sv, si);
   } else {
     // A lane visits its positions in increasing order, so a later value only
     // wins when it is strictly larger (or the first NaN).  Per 16-byte vector:
@@ -160,7 +170,8 @@ __global__ __launch_bounds__(kMaxBlock) void reduce_rows(const Ti* __restrict__ 
     ValIdx best{kNegInf, n};  // an empty lane loses to any element
     bool done = false;        // a NaN was found: nothing later can win
     if (hv) {
-      const float v = static_cast<float>(x[start + g]);
+      float v;
+      load_f32<Ti, 1>(x + start + g, &v, sx);
       if (v != v) {
         best = ValIdx{__builtin_nanf(""), g};
         done = true;
@@ -173,7 +184,7 @@ __global__ __launch_bounds__(kMaxBlock) void reduce_rows(const Ti* __restrict__ 
 #pragma unroll
       for (int c = 0; c < kChunk; ++c) {
         const int j = base + c * tpr;
-        r[c] = j < nvec ? load_raw<Ti, V, true>(xr + static_cast<int64_t>(j) * V) : RT{};
+        r[c] = j < nvec ? load_raw<Ti, V, true>(xr + static_cast<int64_t>(j) * V, sx) : RT{};
       }
 #pragma unroll
       for (int c = 0; c < kChunk; ++c) {
@@ -206,12 +217,13 @@ __global__ __launch_bounds__(kMaxBlock) void reduce_rows(const Ti* __restrict__ 
       }
     }
     if (tv && !done) {
-      const float v = static_cast<float>(x[start + tail0 + g]);
+      float v;
+      load_f32<Ti, 1>(x + start + tail0 + g, &v, sx);
       if (v != v) best = ValIdx{__builtin_nanf(""), tail0 + g};
       else if (v > best.v || best.i == n) best = ValIdx{v, tail0 + g};
     }
     best = group_allreduce_vi(best, tpr, lds);
-    if (live && g == 0) write_result<To, V, OP>(vals, idx, row, best.v, best.i, n);
+    if (live && g == 0) write_result<To, V, OP>(vals, idx, row, best.v, best.i, n, sv, si);
   }
 }
 
@@ -229,14 +241,20 @@ __global__ __launch_bounds__(256) void reduce_combine_vi(const T* __restrict__ p
   const int64_t row = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (row >= rows) return;
   const int64_t base = row * segs;
-  ValIdx best{static_cast<float>(pvals[base]), static_cast<int>(pidx[base])};
+  const Span spv = VBH_SPAN(pvals, rows * segs), spi = VBH_SPAN(pidx, rows * segs);
+  const Span sv = VBH_SPAN(static_cast<T*>(vals), rows), si = VBH_SPAN(idx, rows);
+  ValIdx best{VBH_IN_SPAN(spv, pvals + base, sizeof(T)) ? static_cast<float>(pvals[base]) : 0.f,
+              VBH_IN_SPAN(spi, pidx + base, sizeof(int64_t)) ? static_cast<int>(pidx[base]) : 0};
   for (int s = 1; s < segs; ++s) {
-    const ValIdx c{static_cast<float>(pvals[base + s]),
-                   s * segn + static_cast<int>(pidx[base + s])};
+    const ValIdx c{
+        VBH_IN_SPAN(spv, pvals + base + s, sizeof(T)) ? static_cast<float>(pvals[base + s]) : 0.f,
+        s * segn + (VBH_IN_SPAN(spi, pidx + base + s, sizeof(int64_t))
+                        ? static_cast<int>(pidx[base + s])
+                        : 0)};
     best = pick(best, c);
   }
-  if constexpr (OP == 1) store_from_f32<T, 1>(static_cast<T*>(vals) + row, &best.v);
-  idx[row] = best.i;
+  if constexpr (OP == 1) store_from_f32<T, 1>(static_cast<T*>(vals) + row, &best.v, sv);
+  if (VBH_IN_SPAN(si, idx + row, sizeof(int64_t))) idx[row] = best.i;
 }
 
 template <typename Ti, typename To, int OP>
@@ -249,17 +267,24 @@ __global__ __launch_bounds__(256) void reduce_cols(const Ti* __restrict__ x,
   const int64_t o = col / inner;
   const int64_t c = col - o * inner;
   const Ti* xc = x + o * n * inner + c;
+  const Span sx = VBH_SPAN(x, outer * n * inner);
+  const Span sv = VBH_SPAN(static_cast<To*>(vals), outer * inner), si = VBH_SPAN(idx, outer * inner);
+  auto xat = [&](int r) {
+    float v;
+    load_f32<Ti, 1>(xc + r * inner, &v, sx);
+    return v;
+  };
   if constexpr (OP == 0) {
     float s = 0.f;
-    for (int r = 0; r < n; ++r) s += static_cast<float>(xc[r * inner]);
-    write_result<To, 1, OP>(vals, idx, col, s, 0, n);
+    for (int r = 0; r < n; ++r) s += xat(r);
+    write_result<To, 1, OP>(vals, idx, col, s, 0, n, sv, si);
   } else {
     ValIdx best{kNegInf, n};
     for (int r = 0; r < n; ++r) {
-      const float v = static_cast<float>(xc[r * inner]);
+      const float v = xat(r);
       if (better(v, r, best.v, best.i)) best = ValIdx{v, r};
     }
-    write_result<To, 1, OP>(vals, idx, col, best.v, best.i, n);
+    write_result<To, 1, OP>(vals, idx, col, best.v, best.i, n, sv, si);
   }
 }
 

@@ -34,11 +34,12 @@ namespace {
 
 template <typename T, int V, int IT, bool NT, bool FULL = false>
 __device__ __forceinline__ void load_raw_row(const T* __restrict__ xr, int nvec, int g, int tpr,
-                                             typename Raw<T, V>::type (&dst)[IT]) {
+                                             typename Raw<T, V>::type (&dst)[IT],
+                                             const Span& s) {
 #pragma unroll
   for (int i = 0; i < IT; ++i) {
     const int j = i * tpr + g;
-    if (FULL || j < nvec) dst[i] = load_raw<T, V, NT>(xr + static_cast<int64_t>(j) * V);
+    if (FULL || j < nvec) dst[i] = load_raw<T, V, NT>(xr + static_cast<int64_t>(j) * V, s);
     else dst[i] = typename Raw<T, V>::type{};
   }
 }
@@ -207,14 +208,16 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_rows(
   int64_t row = first + gs.sub;
   const bool live = row < rows;
   if (!live) row = rows - 1;
+  const Span sx = VBH_SPAN(x, rows * cols), sy = VBH_SPAN(y, rows * cols);
+  const Span sw = VBH_SPAN(w, cols), sb = VBH_SPAN(b, cols);
 
   RT xr[IT];
-  load_raw_row<T, V, IT, SP != kStoreCached>(x + row * cols, nvec, g, tpr, xr);
+  load_raw_row<T, V, IT, SP != kStoreCached>(x + row * cols, nvec, g, tpr, xr, sx);
   constexpr bool kEarly = kEarlyLN<TW, V, IT>;
   RW wr[kEarly ? IT : 1], br[kEarly ? IT : 1];
   if constexpr (kEarly) {
-    load_raw_row<TW, V, IT, false>(w, nvec, g, tpr, wr);
-    if (b != nullptr) load_raw_row<TW, V, IT, false>(b, nvec, g, tpr, br);
+    load_raw_row<TW, V, IT, false>(w, nvec, g, tpr, wr, sw);
+    if (b != nullptr) load_raw_row<TW, V, IT, false>(b, nvec, g, tpr, br, sb);
   }
 
   const float mean =
@@ -238,15 +241,15 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_rows(
         wv = wr[i];
         if (b != nullptr) bv = br[i];
       } else {
-        wv = load_raw<TW, V, false>(w + static_cast<int64_t>(j) * V);
-        if (b != nullptr) bv = load_raw<TW, V, false>(b + static_cast<int64_t>(j) * V);
+        wv = load_raw<TW, V, false>(w + static_cast<int64_t>(j) * V, sw);
+        if (b != nullptr) bv = load_raw<TW, V, false>(b + static_cast<int64_t>(j) * V, sb);
       }
       float o[V];
 #pragma unroll
       for (int k = 0; k < V; ++k)
         o[k] = (raw_at<T, V>(xr[i], k) - mean) * rstd * raw_at<TW, V>(wv, k) +
                raw_at<TW, V>(bv, k);
-      out.template store<V>(yr + static_cast<int64_t>(j) * V, yoff + j * V, o);
+      out.template store<V>(yr + static_cast<int64_t>(j) * V, yoff + j * V, o, sy);
     }
   }
 }
@@ -266,12 +269,14 @@ __global__ __launch_bounds__(kMaxBlock) void rms_norm_rows(
   int64_t row = first + gs.sub;
   const bool live = row < rows;
   if (!live) row = rows - 1;
+  const Span sx = VBH_SPAN(x, rows * cols), sy = VBH_SPAN(y, rows * cols);
+  const Span sw = VBH_SPAN(w, cols);
 
   RT xr[IT];
-  load_raw_row<T, V, IT, SP != kStoreCached>(x + row * cols, nvec, g, tpr, xr);
+  load_raw_row<T, V, IT, SP != kStoreCached>(x + row * cols, nvec, g, tpr, xr, sx);
   constexpr bool kEarly = kEarlyRMS<TW, V, IT>;
   RW wr[kEarly ? IT : 1];
-  if constexpr (kEarly) load_raw_row<TW, V, IT, false>(w, nvec, g, tpr, wr);
+  if constexpr (kEarly) load_raw_row<TW, V, IT, false>(w, nvec, g, tpr, wr, sw);
 
   const float ss = group_allreduce<Sum>(lane_sumsq<T, V, IT>(xr), tpr, lds);
   const float rinv = rsqrt_hw(ss * inv_count(cols) + eps);
@@ -287,11 +292,11 @@ __global__ __launch_bounds__(kMaxBlock) void rms_norm_rows(
     if (j < nvec) {
       RW wv;
       if constexpr (kEarly) wv = wr[i];
-      else wv = load_raw<TW, V, false>(w + static_cast<int64_t>(j) * V);
+      else wv = load_raw<TW, V, false>(w + static_cast<int64_t>(j) * V, sw);
       float o[V];
 #pragma unroll
       for (int k = 0; k < V; ++k) o[k] = (raw_at<T, V>(xr[i], k) * rinv) * raw_at<TW, V>(wv, k);
-      out.template store<V>(yr + static_cast<int64_t>(j) * V, yoff + j * V, o);
+      out.template store<V>(yr + static_cast<int64_t>(j) * V, yoff + j * V, o, sy);
     }
   }
 }
@@ -327,19 +332,22 @@ __device__ __forceinline__ NormMisRow norm_mis_row(int64_t start, int cols) {
 // `head`, so a wave holding rows of different heads does not diverge.
 template <typename TW, int V>
 __device__ __forceinline__ void row_weights(const TW* __restrict__ w, int j, int head,
-                                            float (&out)[V]) {
+                                            float (&out)[V], const Span& s) {
   typedef typename Raw<TW, V>::type RW;
   const TW* p = w + head + static_cast<int64_t>(j) * V;
   RW a;
   if constexpr (sizeof(TW) == 4) {
-    __builtin_memcpy(&a, __builtin_assume_aligned(p, 4), sizeof(a));
+    if (!VBH_IN_SPAN(s, p, sizeof(a))) a = RW{};
+    else __builtin_memcpy(&a, __builtin_assume_aligned(p, 4), sizeof(a));
 #pragma unroll
     for (int k = 0; k < V; ++k) out[k] = raw_at<TW, V>(a, k);
   } else {
     static_assert(sizeof(TW) == 2, "16-bit or 4-byte weights");
     const int odd = head & 1;
-    __builtin_memcpy(&a, __builtin_assume_aligned(p - odd, 4), sizeof(a));
-    const float last = odd ? static_cast<float>(p[V - 1]) : 0.f;
+    if (!VBH_IN_SPAN(s, p - odd, sizeof(a))) a = RW{};
+    else __builtin_memcpy(&a, __builtin_assume_aligned(p - odd, 4), sizeof(a));
+    const float last = odd && VBH_IN_SPAN(s, p + V - 1, sizeof(TW)) ? static_cast<float>(p[V - 1])
+                                                                 : 0.f;
 #pragma unroll
     for (int k = 0; k < V; ++k) {
       const float up = k + 1 < V ? raw_at<TW, V>(a, k + 1) : last;
@@ -361,17 +369,21 @@ __global__ __launch_bounds__(kMaxBlock) void norm_rows_mis(
   int64_t row = first + gs.sub;
   const bool live = row < rows;
   if (!live) row = rows - 1;
+  const Span sx = VBH_SPAN(x, rows * cols), sy = VBH_SPAN(y, rows * cols);
+  const Span sw = VBH_SPAN(w, cols), sb = VBH_SPAN(b, cols);
   const int64_t start = row * cols;
   const NormMisRow mr = norm_mis_row<V>(start, cols);
   const int nvec = mr.nvec;
   const T* xb = x + start + mr.head;
 
   RT xr[IT];
-  load_raw_row<T, V, IT, SP != kStoreCached>(xb, nvec, g, tpr, xr);
+  load_raw_row<T, V, IT, SP != kStoreCached>(xb, nvec, g, tpr, xr, sx);
   const bool hv = g < mr.head, tv = g < mr.tail;
   const int tcol = mr.head + nvec * V + g;  // this lane's tail column
-  const float hx = hv ? static_cast<float>(x[start + g]) : 0.f;
-  const float tx = tv ? static_cast<float>(x[start + tcol]) : 0.f;
+  const float hx = hv && VBH_IN_SPAN(sx, x + start + g, sizeof(T)) ? static_cast<float>(x[start + g])
+                                                              : 0.f;
+  const float tx =
+      tv && VBH_IN_SPAN(sx, x + start + tcol, sizeof(T)) ? static_cast<float>(x[start + tcol]) : 0.f;
   float mean = 0.f, scale;
   if constexpr (RMS) {
     const float ss = group_allreduce<Sum>(lane_sumsq<T, V, IT>(xr) + hx * hx + tx * tx, tpr,
@@ -391,9 +403,10 @@ __global__ __launch_bounds__(kMaxBlock) void norm_rows_mis(
 
   // element c of this row's output, from its value v
   auto out_at = [&](float v, int c) {
-    const float wv = static_cast<float>(w[c]);
+    const float wv = VBH_IN_SPAN(sw, w + c, sizeof(TW)) ? static_cast<float>(w[c]) : 0.f;
     if constexpr (RMS) return (v * scale) * wv;
-    const float bv = b != nullptr ? static_cast<float>(b[c]) : 0.f;
+    const float bv =
+        b != nullptr && VBH_IN_SPAN(sb, b + c, sizeof(TW)) ? static_cast<float>(b[c]) : 0.f;
     return (v - mean) * scale * wv + bv;
   };
   const OutWindow<T, SP> out(y + first * cols, std::min<int64_t>(rpb, rows - first) * cols);
@@ -404,24 +417,24 @@ __global__ __launch_bounds__(kMaxBlock) void norm_rows_mis(
     const int j = i * tpr + g;
     if (j < nvec) {
       float wv[V], bv[V], o[V];
-      row_weights<TW, V>(w, j, mr.head, wv);
-      if (!RMS && b != nullptr) row_weights<TW, V>(b, j, mr.head, bv);
+      row_weights<TW, V>(w, j, mr.head, wv, sw);
+      if (!RMS && b != nullptr) row_weights<TW, V>(b, j, mr.head, bv, sb);
 #pragma unroll
       for (int k = 0; k < V; ++k) {
         const float v = raw_at<T, V>(xr[i], k);
         if constexpr (RMS) o[k] = (v * scale) * wv[k];
         else o[k] = (v - mean) * scale * wv[k] + (b != nullptr ? bv[k] : 0.f);
       }
-      out.template store<V>(yb + static_cast<int64_t>(j) * V, yoff + j * V, o);
+      out.template store<V>(yb + static_cast<int64_t>(j) * V, yoff + j * V, o, sy);
     }
   }
   if (hv) {
     const float o = out_at(hx, g);
-    store_from_f32<T, 1>(y + start + g, &o);
+    store_from_f32<T, 1>(y + start + g, &o, sy);
   }
   if (tv) {
     const float o = out_at(tx, tcol);
-    store_from_f32<T, 1>(y + start + tcol, &o);
+    store_from_f32<T, 1>(y + start + tcol, &o, sy);
   }
 }
 
@@ -457,10 +470,12 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_pipe(
   const int grp = gs.sub;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * rpb;
   constexpr bool kNT = SP != kStoreCached;
+  const Span sx = VBH_SPAN(x, rows * cols), sy = VBH_SPAN(y, rows * cols);
+  const Span sw = VBH_SPAN(w, cols), sb = VBH_SPAN(b, cols);
 
   RW wr[IT], br[IT];
-  load_raw_row<TW, V, IT, false, FULL>(w, nvec, g, tpr, wr);
-  if (b != nullptr) load_raw_row<TW, V, IT, false, FULL>(b, nvec, g, tpr, br);
+  load_raw_row<TW, V, IT, false, FULL>(w, nvec, g, tpr, wr, sw);
+  if (b != nullptr) load_raw_row<TW, V, IT, false, FULL>(b, nvec, g, tpr, br, sb);
   else
 #pragma unroll
     for (int i = 0; i < IT; ++i) br[i] = RW{};
@@ -471,20 +486,20 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_pipe(
   // load helper whose guards are all false (which schedules better for fp32
   // rows than plain register zeroing); FULL never reaches the first branch.
   if (base + grp < rows) {
-    load_raw_row<T, V, IT, kNT, FULL>(x + (base + grp) * cols, nvec, g, tpr, cur);
+    load_raw_row<T, V, IT, kNT, FULL>(x + (base + grp) * cols, nvec, g, tpr, cur, sx);
   } else {
     if constexpr (FULL) zero_row<T, V, IT>(cur);
-    else load_raw_row<T, V, IT, kNT>(x, 0, g, tpr, cur);
+    else load_raw_row<T, V, IT, kNT>(x, 0, g, tpr, cur, sx);
   }
   int par = 0;
   for (; base < rows; base += stride) {
     const int64_t row = base + grp;
     const int64_t next = row + stride;
     if (next < rows) {
-      load_raw_row<T, V, IT, kNT, FULL>(x + next * cols, nvec, g, tpr, nxt);
+      load_raw_row<T, V, IT, kNT, FULL>(x + next * cols, nvec, g, tpr, nxt, sx);
     } else {
       if constexpr (FULL) zero_row<T, V, IT>(nxt);
-      else load_raw_row<T, V, IT, kNT>(x, 0, g, tpr, nxt);
+      else load_raw_row<T, V, IT, kNT>(x, 0, g, tpr, nxt, sx);
     }
 
     const float mean =
@@ -507,7 +522,7 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_pipe(
           for (int k = 0; k < V; ++k)
             o[k] = (raw_at<T, V>(cur[i], k) - mean) * rstd * raw_at<TW, V>(wr[i], k) +
                    raw_at<TW, V>(br[i], k);
-          out.template store<V>(yr + static_cast<int64_t>(j) * V, yoff + j * V, o);
+          out.template store<V>(yr + static_cast<int64_t>(j) * V, yoff + j * V, o, sy);
         }
       }
     }
@@ -531,29 +546,31 @@ __global__ __launch_bounds__(kMaxBlock) void rms_norm_pipe(
   const int grp = gs.sub;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * rpb;
   constexpr bool kNT = SP != kStoreCached;
+  const Span sx = VBH_SPAN(x, rows * cols), sy = VBH_SPAN(y, rows * cols);
+  const Span sw = VBH_SPAN(w, cols);
 
   RW wr[IT];
-  load_raw_row<TW, V, IT, false, FULL>(w, nvec, g, tpr, wr);
+  load_raw_row<TW, V, IT, false, FULL>(w, nvec, g, tpr, wr, sw);
   RT cur[IT], nxt[IT];
   int64_t base = static_cast<int64_t>(blockIdx.x) * rpb;
   // Rows past the end: zero registers.  The guarded kernels get them from a
   // load helper whose guards are all false (which schedules better for fp32
   // rows than plain register zeroing); FULL never reaches the first branch.
   if (base + grp < rows) {
-    load_raw_row<T, V, IT, kNT, FULL>(x + (base + grp) * cols, nvec, g, tpr, cur);
+    load_raw_row<T, V, IT, kNT, FULL>(x + (base + grp) * cols, nvec, g, tpr, cur, sx);
   } else {
     if constexpr (FULL) zero_row<T, V, IT>(cur);
-    else load_raw_row<T, V, IT, kNT>(x, 0, g, tpr, cur);
+    else load_raw_row<T, V, IT, kNT>(x, 0, g, tpr, cur, sx);
   }
   int par = 0;
   for (; base < rows; base += stride) {
     const int64_t row = base + grp;
     const int64_t next = row + stride;
     if (next < rows) {
-      load_raw_row<T, V, IT, kNT, FULL>(x + next * cols, nvec, g, tpr, nxt);
+      load_raw_row<T, V, IT, kNT, FULL>(x + next * cols, nvec, g, tpr, nxt, sx);
     } else {
       if constexpr (FULL) zero_row<T, V, IT>(nxt);
-      else load_raw_row<T, V, IT, kNT>(x, 0, g, tpr, nxt);
+      else load_raw_row<T, V, IT, kNT>(x, 0, g, tpr, nxt, sx);
     }
 
     const float ss = group_allreduce<Sum>(lane_sumsq<T, V, IT>(cur), tpr, lds[par]);
@@ -571,7 +588,7 @@ __global__ __launch_bounds__(kMaxBlock) void rms_norm_pipe(
 #pragma unroll
           for (int k = 0; k < V; ++k)
             o[k] = (raw_at<T, V>(cur[i], k) * rinv) * raw_at<TW, V>(wr[i], k);
-          out.template store<V>(yr + static_cast<int64_t>(j) * V, yoff + j * V, o);
+          out.template store<V>(yr + static_cast<int64_t>(j) * V, yoff + j * V, o, sy);
         }
       }
     }
@@ -594,10 +611,14 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_stream(
   const int nvec = cols / V;
   const int64_t row = blockIdx.x;
   const T* xr = x + row * cols;
+  // one workgroup per row: the grid is the row count
+  const Span sx = VBH_SPAN(x, static_cast<int64_t>(gridDim.x) * cols);
+  const Span sy = VBH_SPAN(y, static_cast<int64_t>(gridDim.x) * cols);
+  const Span sw = VBH_SPAN(w, cols), sb = VBH_SPAN(b, cols);
   Moments m{0.f, 0.f, 0.f};
   for (int j = threadIdx.x; j < nvec; j += tpr) {
     float v[V];
-    load_f32<T, V>(xr + static_cast<int64_t>(j) * V, v);
+    load_f32<T, V>(xr + static_cast<int64_t>(j) * V, v, sx);
     float s = 0.f;
 #pragma unroll
     for (int k = 0; k < V; ++k) s += v[k];
@@ -613,17 +634,17 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_stream(
   T* yr = y + row * cols;
   for (int j = threadIdx.x; j < nvec; j += tpr) {
     float v[V], wv[V], bv[V], o[V];
-    load_f32<T, V>(xr + static_cast<int64_t>(j) * V, v);
-    load_f32<TW, V>(w + static_cast<int64_t>(j) * V, wv);
+    load_f32<T, V>(xr + static_cast<int64_t>(j) * V, v, sx);
+    load_f32<TW, V>(w + static_cast<int64_t>(j) * V, wv, sw);
     if (b != nullptr) {
-      load_f32<TW, V>(b + static_cast<int64_t>(j) * V, bv);
+      load_f32<TW, V>(b + static_cast<int64_t>(j) * V, bv, sb);
     } else {
 #pragma unroll
       for (int k = 0; k < V; ++k) bv[k] = 0.f;
     }
 #pragma unroll
     for (int k = 0; k < V; ++k) o[k] = (v[k] - mean) * rstd * wv[k] + bv[k];
-    store_from_f32<T, V>(yr + static_cast<int64_t>(j) * V, o);
+    store_from_f32<T, V>(yr + static_cast<int64_t>(j) * V, o, sy);
   }
 }
 
@@ -636,10 +657,14 @@ __global__ __launch_bounds__(kMaxBlock) void rms_norm_stream(
   const int nvec = cols / V;
   const int64_t row = blockIdx.x;
   const T* xr = x + row * cols;
+  // one workgroup per row: the grid is the row count
+  const Span sx = VBH_SPAN(x, static_cast<int64_t>(gridDim.x) * cols);
+  const Span sy = VBH_SPAN(y, static_cast<int64_t>(gridDim.x) * cols);
+  const Span sw = VBH_SPAN(w, cols);
   float acc = 0.f;
   for (int j = threadIdx.x; j < nvec; j += tpr) {
     float v[V];
-    load_f32<T, V>(xr + static_cast<int64_t>(j) * V, v);
+    load_f32<T, V>(xr + static_cast<int64_t>(j) * V, v, sx);
 #pragma unroll
     for (int k = 0; k < V; ++k) acc = fmaf(v[k], v[k], acc);
   }
@@ -648,11 +673,11 @@ __global__ __launch_bounds__(kMaxBlock) void rms_norm_stream(
   T* yr = y + row * cols;
   for (int j = threadIdx.x; j < nvec; j += tpr) {
     float v[V], wv[V], o[V];
-    load_f32<T, V>(xr + static_cast<int64_t>(j) * V, v);
-    load_f32<TW, V>(w + static_cast<int64_t>(j) * V, wv);
+    load_f32<T, V>(xr + static_cast<int64_t>(j) * V, v, sx);
+    load_f32<TW, V>(w + static_cast<int64_t>(j) * V, wv, sw);
 #pragma unroll
     for (int k = 0; k < V; ++k) o[k] = (v[k] * rinv) * wv[k];
-    store_from_f32<T, V>(yr + static_cast<int64_t>(j) * V, o);
+    store_from_f32<T, V>(yr + static_cast<int64_t>(j) * V, o, sy);
   }
 }
 

@@ -32,13 +32,14 @@ constexpr float kNegInf = -__builtin_huge_valf();
 // on the spot, one row load at a time.)
 template <typename T, int V, int IT, bool NT>
 __device__ __forceinline__ void load_raw_row(const T* __restrict__ xr, int nvec, int g, int tpr,
-                                             typename Raw<T, V>::type (&dst)[IT]) {
+                                             typename Raw<T, V>::type (&dst)[IT],
+                                             const Span& s) {
   typedef typename Raw<T, V>::type RT;
   const RT fill = RT(static_cast<T>(kNegInf));
 #pragma unroll
   for (int i = 0; i < IT; ++i) {
     const int j = i * tpr + g;
-    if (j < nvec) dst[i] = load_raw<T, V, NT>(xr + static_cast<int64_t>(j) * V);
+    if (j < nvec) dst[i] = load_raw<T, V, NT>(xr + static_cast<int64_t>(j) * V, s);
     else dst[i] = fill;
   }
 }
@@ -118,17 +119,18 @@ __global__ __launch_bounds__(kMaxBlock) void softmax_rows(const Ti* __restrict__
   int64_t row = first + gs.sub;
   const bool live = row < rows;
   if (!live) row = rows - 1;
+  const Span sx = VBH_SPAN(x, rows * cols), sy = VBH_SPAN(y, rows * cols);
   const int64_t start = row * cols;
   const MisRow mr = MIS ? mis_row<V>(start, cols) : MisRow{0, cols / V, 0};
   const int nvec = mr.nvec;
   const Ti* xb = x + start + mr.head;  // 16-byte aligned body
 
   RT xr[IT];
-  load_raw_row<Ti, V, IT, SP != kStoreCached>(xb, nvec, g, tpr, xr);
+  load_raw_row<Ti, V, IT, SP != kStoreCached>(xb, nvec, g, tpr, xr, sx);
   const bool hv = MIS && g < mr.head, tv = MIS && g < mr.tail;
   float hx = 0.f, tx = 0.f;
-  if (hv) hx = static_cast<float>(x[start + g]);
-  if (tv) tx = static_cast<float>(xb[static_cast<int64_t>(nvec) * V + g]);
+  if (hv) load_f32<Ti, 1>(x + start + g, &hx, sx);
+  if (tv) load_f32<Ti, 1>(xb + static_cast<int64_t>(nvec) * V + g, &tx, sx);
   float lm = lane_max<Ti, V, IT>(xr);
   if (hv) lm = max_nan(lm, hx);
   if (tv) lm = max_nan(lm, tx);
@@ -161,16 +163,16 @@ __global__ __launch_bounds__(kMaxBlock) void softmax_rows(const Ti* __restrict__
         else if constexpr (KEEP) o[k] = v * r;
         else o[k] = exp_shifted(v, mb) * r;
       }
-      out.template store<V>(yr + static_cast<int64_t>(j) * V, yoff + j * V, o);
+      out.template store<V>(yr + static_cast<int64_t>(j) * V, yoff + j * V, o, sy);
     }
   }
   if (hv) {
     const float o = LOG ? (hx - m) - ls : exp_shifted(hx, mb) * r;
-    store_from_f32<To, 1>(y + start + g, &o);
+    store_from_f32<To, 1>(y + start + g, &o, sy);
   }
   if (tv) {
     const float o = LOG ? (tx - m) - ls : exp_shifted(tx, mb) * r;
-    store_from_f32<To, 1>(yr + static_cast<int64_t>(nvec) * V + g, &o);
+    store_from_f32<To, 1>(yr + static_cast<int64_t>(nvec) * V + g, &o, sy);
   }
 }
 
@@ -190,6 +192,9 @@ __global__ __launch_bounds__(kMaxBlock) void logsumexp_rows(const Ti* __restrict
   int64_t row = static_cast<int64_t>(blockIdx.x) * gs.per_block + gs.sub;
   const bool live = row < rows;
   if (!live) row = rows - 1;
+  // x holds rows / segs rows of `cols` in the MIS segment mode
+  const Span sx = VBH_SPAN(x, (MIS && segs > 1 ? rows / segs : rows) * cols);
+  const Span sy = VBH_SPAN(y, rows);
   int64_t start = row * cols;
   int len = cols;
   if (MIS && segs > 1) {
@@ -203,11 +208,11 @@ __global__ __launch_bounds__(kMaxBlock) void logsumexp_rows(const Ti* __restrict
   const Ti* xb = x + start + mr.head;
 
   RT xr[IT];
-  load_raw_row<Ti, V, IT, NT>(xb, nvec, g, tpr, xr);
+  load_raw_row<Ti, V, IT, NT>(xb, nvec, g, tpr, xr, sx);
   const bool hv = MIS && g < mr.head, tv = MIS && g < mr.tail;
   float hx = 0.f, tx = 0.f;
-  if (hv) hx = static_cast<float>(x[start + g]);
-  if (tv) tx = static_cast<float>(xb[static_cast<int64_t>(nvec) * V + g]);
+  if (hv) load_f32<Ti, 1>(x + start + g, &hx, sx);
+  if (tv) load_f32<Ti, 1>(xb + static_cast<int64_t>(nvec) * V + g, &tx, sx);
   float lm = lane_max<Ti, V, IT>(xr);
   if (hv) lm = max_nan(lm, hx);
   if (tv) lm = max_nan(lm, tx);
@@ -221,7 +226,7 @@ __global__ __launch_bounds__(kMaxBlock) void logsumexp_rows(const Ti* __restrict
   const float s = group_allreduce<Sum>(le, tpr, lds[1]);
   if (live && g == 0) {
     const float r = (fast_log(s) - shift_residual(m, mb) * kLn2) + m;
-    store_from_f32<To, 1>(y + row, &r);
+    store_from_f32<To, 1>(y + row, &r, sy);
   }
 }
 
@@ -248,6 +253,10 @@ __global__ __launch_bounds__(kApplyLanes) void softmax_apply_tiles(
   const uint32_t row32 = blockIdx.x / tiles_per_row;
   const int tix = static_cast<int>(blockIdx.x - row32 * tiles_per_row);
   const int64_t row = row32;
+  // the grid is the row count times tiles_per_row
+  const Span sx = VBH_SPAN(x, static_cast<int64_t>(gridDim.x / tiles_per_row) * cols);
+  const Span sy = VBH_SPAN(y, static_cast<int64_t>(gridDim.x / tiles_per_row) * cols);
+  const Span sl = VBH_SPAN(seg_lse, static_cast<int64_t>(gridDim.x / tiles_per_row) * segs);
   const int64_t start = row * cols;
   const MisRow mr = MIS ? mis_row<V>(start, cols) : MisRow{0, cols / V, 0};
   const int nvec = mr.nvec;
@@ -255,11 +264,12 @@ __global__ __launch_bounds__(kApplyLanes) void softmax_apply_tiles(
   const int j0 = tix * kApplyLanes;
   const int j = j0 + static_cast<int>(threadIdx.x);
   typename Raw<Ti, V>::type r{};
-  if (j < nvec) r = load_raw<Ti, V, SP != kStoreCached>(xb + static_cast<int64_t>(j) * V);
+  if (j < nvec) r = load_raw<Ti, V, SP != kStoreCached>(xb + static_cast<int64_t>(j) * V, sx);
 
   const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
   const bool has = lane < segs;
-  const float l = has ? seg_lse[row * segs + lane] : kNegInf;
+  float l = kNegInf;
+  if (has) load_f32<float, 1>(seg_lse + row * segs + lane, &l, sl);
   const float m = wave_allreduce<Max>(l, kWave);
   const float nan = wave_allreduce<Max>(l != l ? 1.f : 0.f, kWave);
   const bool bad = nan > 0.f || __builtin_isinf(m);
@@ -278,18 +288,23 @@ __global__ __launch_bounds__(kApplyLanes) void softmax_apply_tiles(
     float o[V];
 #pragma unroll
     for (int k = 0; k < V; ++k) o[k] = value(raw_at<Ti, V>(r, k));
-    out.template store<V>(yb + static_cast<int64_t>(j) * V, static_cast<int>(threadIdx.x) * V, o);
+    out.template store<V>(yb + static_cast<int64_t>(j) * V, static_cast<int>(threadIdx.x) * V, o,
+                          sy);
   }
   if (MIS && tix == 0) {
     const int t = static_cast<int>(threadIdx.x);
     if (t < mr.head) {
-      const float o = value(static_cast<float>(x[start + t]));
-      store_from_f32<To, 1>(y + start + t, &o);
+      float v;
+      load_f32<Ti, 1>(x + start + t, &v, sx);
+      const float o = value(v);
+      store_from_f32<To, 1>(y + start + t, &o, sy);
     }
     if (t < mr.tail) {
       const int64_t k = static_cast<int64_t>(nvec) * V + t;
-      const float o = value(static_cast<float>(xb[k]));
-      store_from_f32<To, 1>(yb + k, &o);
+      float v;
+      load_f32<Ti, 1>(xb + k, &v, sx);
+      const float o = value(v);
+      store_from_f32<To, 1>(yb + k, &o, sy);
     }
   }
 }
@@ -309,11 +324,11 @@ struct RowStats {
 
 template <typename T, int V>
 __device__ __forceinline__ RowStats stream_stats(const T* __restrict__ xr, int nvec,
-                                                 float* lds) {
+                                                 float* lds, const Span& sx) {
   float m = kNegInf, s = 0.f, nan = 0.f;
   for (int j = threadIdx.x; j < nvec; j += blockDim.x) {
     float v[V];
-    load_f32<T, V>(xr + static_cast<int64_t>(j) * V, v);
+    load_f32<T, V>(xr + static_cast<int64_t>(j) * V, v, sx);
     float cm = kNegInf;
 #pragma unroll
     for (int k = 0; k < V; ++k) {
@@ -345,7 +360,10 @@ __global__ __launch_bounds__(kMaxBlock) void softmax_stream(const Ti* __restrict
   const int nvec = cols / V;
   const int64_t row = blockIdx.x;
   const Ti* xr = x + row * cols;
-  const RowStats st = stream_stats<Ti, V>(xr, nvec, lds);
+  // one workgroup per row: the grid is the row count
+  const Span sx = VBH_SPAN(x, static_cast<int64_t>(gridDim.x) * cols);
+  const Span sy = VBH_SPAN(y, static_cast<int64_t>(gridDim.x) * cols);
+  const RowStats st = stream_stats<Ti, V>(xr, nvec, lds, sx);
   const bool special = st.nan != 0.f || st.m == kNegInf || st.m == -kNegInf;
   const float qnan = __builtin_nanf("");
   const float m = st.m;
@@ -354,19 +372,19 @@ __global__ __launch_bounds__(kMaxBlock) void softmax_stream(const Ti* __restrict
     const float ls = special ? qnan : fast_log(st.s);
     for (int j = threadIdx.x; j < nvec; j += blockDim.x) {
       float v[V], o[V];
-      load_f32<Ti, V>(xr + static_cast<int64_t>(j) * V, v);
+      load_f32<Ti, V>(xr + static_cast<int64_t>(j) * V, v, sx);
 #pragma unroll
       for (int k = 0; k < V; ++k) o[k] = (v[k] - m) - ls;
-      store_from_f32<To, V>(yr + static_cast<int64_t>(j) * V, o);
+      store_from_f32<To, V>(yr + static_cast<int64_t>(j) * V, o, sy);
     }
   } else {
     const float r = special ? qnan : 1.0f / st.s;
     for (int j = threadIdx.x; j < nvec; j += blockDim.x) {
       float v[V], o[V];
-      load_f32<Ti, V>(xr + static_cast<int64_t>(j) * V, v);
+      load_f32<Ti, V>(xr + static_cast<int64_t>(j) * V, v, sx);
 #pragma unroll
       for (int k = 0; k < V; ++k) o[k] = fast_exp(v[k] - m) * r;
-      store_from_f32<To, V>(yr + static_cast<int64_t>(j) * V, o);
+      store_from_f32<To, V>(yr + static_cast<int64_t>(j) * V, o, sy);
     }
   }
 }
@@ -377,13 +395,16 @@ __global__ __launch_bounds__(kMaxBlock) void logsumexp_stream(const Ti* __restri
   __shared__ float lds[3 * kMaxWaves];
   const int nvec = cols / V;
   const int64_t row = blockIdx.x;
-  const RowStats st = stream_stats<Ti, V>(x + row * cols, nvec, lds);
+  // one workgroup per row: the grid is the row count
+  const Span sx = VBH_SPAN(x, static_cast<int64_t>(gridDim.x) * cols);
+  const Span sy = VBH_SPAN(y, static_cast<int64_t>(gridDim.x));
+  const RowStats st = stream_stats<Ti, V>(x + row * cols, nvec, lds, sx);
   if (threadIdx.x == 0) {
     float r;
     if (st.nan != 0.f) r = __builtin_nanf("");
     else if (st.m == kNegInf || st.m == -kNegInf) r = st.m;
     else r = fast_log(st.s) + st.m;
-    store_from_f32<To, 1>(y + row, &r);
+    store_from_f32<To, 1>(y + row, &r, sy);
   }
 }
 
@@ -400,21 +421,26 @@ __global__ __launch_bounds__(256) void softmax_mid(const Ti* __restrict__ x,
   const int64_t i = col - o * inner;
   const Ti* xc = x + o * n * inner + i;
   To* yc = y + o * n * inner + i;
+  const Span sx = VBH_SPAN(x, outer * n * inner), sy = VBH_SPAN(y, outer * n * inner);
+  auto xat = [&](int r) {
+    const Ti* p = xc + r * inner;
+    return VBH_IN_SPAN(sx, p, sizeof(Ti)) ? static_cast<float>(*p) : 0.f;
+  };
   float m = kNegInf;
-  for (int r = 0; r < n; ++r) m = fmaxf(m, static_cast<float>(xc[r * inner]));
+  for (int r = 0; r < n; ++r) m = fmaxf(m, xat(r));
   float s = 0.f;
-  for (int r = 0; r < n; ++r) s += fast_exp(static_cast<float>(xc[r * inner]) - m);
+  for (int r = 0; r < n; ++r) s += fast_exp(xat(r) - m);
   if constexpr (LOG) {
     const float ls = fast_log(s);
     for (int r = 0; r < n; ++r) {
-      const float out = (static_cast<float>(xc[r * inner]) - m) - ls;
-      store_from_f32<To, 1>(yc + r * inner, &out);
+      const float out = (xat(r) - m) - ls;
+      store_from_f32<To, 1>(yc + r * inner, &out, sy);
     }
   } else {
     const float rs = 1.0f / s;
     for (int r = 0; r < n; ++r) {
-      const float out = fast_exp(static_cast<float>(xc[r * inner]) - m) * rs;
-      store_from_f32<To, 1>(yc + r * inner, &out);
+      const float out = fast_exp(xat(r) - m) * rs;
+      store_from_f32<To, 1>(yc + r * inner, &out, sy);
     }
   }
 }

@@ -37,7 +37,8 @@ __global__ __launch_bounds__(256) void copy_kernel(const u32x4* __restrict__ src
   const int64_t tile = n - first < blockDim.x ? n - first : blockDim.x;
   const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(
       dst + first, static_cast<short>(0), static_cast<int>(tile * sizeof(u32x4)), kRawBufferWord3);
-  if (i < n)
+  const Span ss = VBH_SPAN(src, n), sd = VBH_SPAN(dst, n);
+  if (i < n && VBH_IN_SPAN(ss, src + i, sizeof(u32x4)) && VBH_IN_SPAN(sd, dst + i, sizeof(u32x4)))
     __builtin_amdgcn_raw_buffer_store_b128(
         __builtin_bit_cast(i32x4, __builtin_nontemporal_load(src + i)), out,
         static_cast<int>(threadIdx.x * sizeof(u32x4)), 0, kCacheNtSc1);
@@ -51,13 +52,15 @@ __global__ __launch_bounds__(kReadBlock) void read_kernel(const u32x4* __restric
                                                           int64_t n) {
   constexpr int64_t kTile = int64_t(kReadBlock) * U;
   const int64_t step = static_cast<int64_t>(gridDim.x) * kTile;
+  const Span ss = VBH_SPAN(src, n), sp = VBH_SPAN(partial, gridDim.x);
   u32x4 acc = {0u, 0u, 0u, 0u};
   for (int64_t first = static_cast<int64_t>(blockIdx.x) * kTile; first < n; first += step) {
     u32x4 v[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t i = first + u * kReadBlock + threadIdx.x;
-      v[u] = i < n ? __builtin_nontemporal_load(src + i) : u32x4{0u, 0u, 0u, 0u};
+      v[u] = i < n && VBH_IN_SPAN(ss, src + i, sizeof(u32x4)) ? __builtin_nontemporal_load(src + i)
+                                                           : u32x4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) acc ^= v[u];
@@ -72,7 +75,7 @@ __global__ __launch_bounds__(kReadBlock) void read_kernel(const u32x4* __restric
     uint32_t r = 0;
 #pragma unroll
     for (int w = 0; w < kReadBlock / kWave; ++w) r ^= lds[w];
-    partial[blockIdx.x] = r;
+    if (VBH_IN_SPAN(sp, partial + blockIdx.x, sizeof(uint32_t))) partial[blockIdx.x] = r;
   }
 }
 

@@ -28,13 +28,81 @@ template <> struct Vec<_Float16> { static constexpr int n = 8; };
 template <> struct Vec<__bf16> { static constexpr int n = 8; };
 
 // ---------------------------------------------------------------------------
-// loads / stores
+// debug bounds checks
+//
+// A build with VBH_DEBUG_BOUNDS defined (libvbhip_debug.so, `python -m
+// dslperfgap_amd.build` makes it next to the release library) checks every
+// global-memory access of every kernel before making it: the accessed bytes
+// must lie inside the buffer the access belongs to.  Each kernel describes its
+// buffers as Spans made from its own size arguments (VBH_SPAN(pointer,
+// elements)), and every load / store helper below takes the Span of its
+// buffer.  A failing access is not made (a load yields zeros, a store is
+// dropped); it is counted in this translation unit's record together with the
+// source line of the Span's VBH_SPAN, and the host reads the records through
+// vbh_debug_bounds.  In a release build a Span is an empty struct and every
+// check the constant true, so the generated code is the code without them.
+// ---------------------------------------------------------------------------
+
+struct Span {
+#ifdef VBH_DEBUG_BOUNDS
+  uintptr_t lo, hi;  // the buffer's bytes [lo, hi)
+  int line;          // source line of the VBH_SPAN that made it
+#endif
+};
+
+#ifdef VBH_DEBUG_BOUNDS
+// This translation unit's record: [0] failed checks, [1] the Span line of the
+// first failure (0: none).
+static __device__ unsigned g_bounds_record[2];
+// Bytes taken off the end of every Span (vbh_debug_bounds_slack): a test sets
+// it to watch the checks fail on accesses near a buffer's end, which are then
+// skipped, never made out of bounds.
+static __device__ long long g_bounds_slack;
+
+template <typename T>
+__device__ __forceinline__ Span make_span(const T* p, int64_t elems, int line) {
+  const uintptr_t lo = reinterpret_cast<uintptr_t>(p);
+  return Span{lo, lo + static_cast<uintptr_t>(elems > 0 ? elems : 0) * sizeof(T), line};
+}
+
+// The `bytes` at `p` lie inside `s` (less the slack); otherwise count the
+// failure (vector atomics on the record) and return false.
+__device__ __forceinline__ bool in_span(const Span& s, const void* p, int bytes) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  const long long room = static_cast<long long>(s.hi - s.lo) - g_bounds_slack;
+  if (a >= s.lo && static_cast<long long>(a - s.lo) + bytes <= room) return true;
+  atomicAdd(&g_bounds_record[0], 1u);
+  atomicCAS(&g_bounds_record[1], 0u, static_cast<unsigned>(s.line));
+  return false;
+}
+
+#define VBH_SPAN(p, elems) ::vbh::make_span((p), static_cast<int64_t>(elems), __LINE__)
+#define VBH_IN_SPAN(s, p, bytes) ::vbh::in_span((s), (p), static_cast<int>(bytes))
+#else
+// the constant true: the access is made as if unchecked (the pointer and size
+// are not evaluated; naming the empty Span keeps it a used variable)
+#define VBH_SPAN(p, elems) ::vbh::Span{}
+#define VBH_IN_SPAN(s, p, bytes) (static_cast<void>(s), true)
+#endif
+
+// Elements a [rows, cols] matrix with row stride `ld` spans (for Spans).
+__device__ __forceinline__ int64_t strided_extent(int64_t rows, int64_t ld, int64_t cols) {
+  return rows > 0 ? (rows - 1) * ld + cols : 0;
+}
+
+// ---------------------------------------------------------------------------
+// loads / stores (each takes the Span of the buffer it accesses)
 // ---------------------------------------------------------------------------
 
 // Read V consecutive elements at p (V == Vec<T>::n: one 16-byte load, p 16-byte
 // aligned; V == 1: one element) and widen them to fp32.
 template <typename T, int V>
-__device__ __forceinline__ void load_f32(const T* __restrict__ p, float* o) {
+__device__ __forceinline__ void load_f32(const T* __restrict__ p, float* o, const Span& s) {
+  if (!VBH_IN_SPAN(s, p, V * sizeof(T))) {
+#pragma unroll
+    for (int k = 0; k < V; ++k) o[k] = 0.f;
+    return;
+  }
   if constexpr (V == 1) {
     o[0] = static_cast<float>(p[0]);
   } else {
@@ -47,7 +115,8 @@ __device__ __forceinline__ void load_f32(const T* __restrict__ p, float* o) {
 
 // Round V fp32 values to T (round-to-nearest-even, NaN preserved) and store.
 template <typename T, int V>
-__device__ __forceinline__ void store_from_f32(T* __restrict__ p, const float* o) {
+__device__ __forceinline__ void store_from_f32(T* __restrict__ p, const float* o, const Span& s) {
+  if (!VBH_IN_SPAN(s, p, V * sizeof(T))) return;
   if constexpr (V == 1) {
     p[0] = static_cast<T>(o[0]);
   } else {
@@ -67,8 +136,10 @@ template <typename T> struct Raw<T, 1> { typedef T type; };
 // 16-byte (or scalar) load; NT marks the access nontemporal (streamed data
 // that is touched once), which keeps it from displacing reused lines.
 template <typename T, int V, bool NT>
-__device__ __forceinline__ typename Raw<T, V>::type load_raw(const T* __restrict__ p) {
+__device__ __forceinline__ typename Raw<T, V>::type load_raw(const T* __restrict__ p,
+                                                             const Span& s) {
   typedef typename Raw<T, V>::type R;
+  if (!VBH_IN_SPAN(s, p, sizeof(R))) return R{};
   const R* q = reinterpret_cast<const R*>(p);
   if constexpr (NT) return __builtin_nontemporal_load(q);
   else return *q;
@@ -100,8 +171,9 @@ __device__ __forceinline__ void reload_barrier(typename Raw<T, V>::type (&r)[IT]
 }
 
 template <typename T, int V, bool NT>
-__device__ __forceinline__ void store_raw(T* __restrict__ p, const float* o) {
+__device__ __forceinline__ void store_raw(T* __restrict__ p, const float* o, const Span& s) {
   typedef typename Raw<T, V>::type R;
+  if (!VBH_IN_SPAN(s, p, sizeof(R))) return;
   R r;
   if constexpr (V == 1) {
     r = static_cast<T>(o[0]);
@@ -157,10 +229,11 @@ struct OutWindow {
   }
 
   // Round V fp32 values to T and store them at `p`, which is element `off` of
-  // the window.
+  // the window; `s` is the Span of the output buffer.
   template <int V>
-  __device__ __forceinline__ void store(T* p, int off, const float* o) const {
+  __device__ __forceinline__ void store(T* p, int off, const float* o, const Span& s) const {
     if constexpr (SP == kStoreThrough && V * sizeof(T) == 16) {
+      if (!VBH_IN_SPAN(s, p, 16)) return;
       typedef typename Raw<T, V>::type R;
       typedef int i32x4 __attribute__((ext_vector_type(4)));
       R r;
@@ -170,7 +243,7 @@ struct OutWindow {
                                              off * static_cast<int>(sizeof(T)), 0,
                                              kCacheNtSc1);
     } else {
-      store_raw<T, V, SP != kStoreCached>(p, o);
+      store_raw<T, V, SP != kStoreCached>(p, o, s);
     }
   }
 };
@@ -394,5 +467,38 @@ __device__ __forceinline__ float exp_shifted(float x, float mb) {
 __device__ __forceinline__ float shift_residual(float m, float mb) {
   return fmaf(m, kLog2e, -mb);
 }
+
+#ifdef VBH_DEBUG_BOUNDS
+// Host side of the records: every translation unit that includes this header
+// registers a reader of its own record (and setter of its slack) with the
+// library (capi.hip), which combines them in vbh_debug_bounds.
+typedef hipError_t (*BoundsRecordFn)(unsigned* failed, unsigned* line, const long long* slack,
+                                     bool clear);
+int register_bounds_record(const char* file, BoundsRecordFn fn);
+
+// Read this translation unit's record on the current device into *failed /
+// *line; with `clear` zero it, with `slack` non-null set the slack.
+static hipError_t bounds_record_here(unsigned* failed, unsigned* line, const long long* slack,
+                                     bool clear) {
+  unsigned rec[2] = {0u, 0u};
+  hipError_t e = hipMemcpyFromSymbol(rec, HIP_SYMBOL(g_bounds_record), sizeof(rec), 0,
+                                     hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return e;
+  *failed = rec[0];
+  *line = rec[1];
+  if (clear) {
+    const unsigned zero[2] = {0u, 0u};
+    e = hipMemcpyToSymbol(HIP_SYMBOL(g_bounds_record), zero, sizeof(zero), 0,
+                          hipMemcpyHostToDevice);
+    if (e != hipSuccess) return e;
+  }
+  if (slack != nullptr)
+    e = hipMemcpyToSymbol(HIP_SYMBOL(g_bounds_slack), slack, sizeof(*slack), 0,
+                          hipMemcpyHostToDevice);
+  return e;
+}
+[[maybe_unused]] static const int g_bounds_registered =
+    register_bounds_record(__BASE_FILE__, &bounds_record_here);
+#endif
 
 }  // namespace vbh

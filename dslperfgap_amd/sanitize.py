@@ -3,7 +3,8 @@
 The C ABI's host code -- argument validation, size arithmetic, launch-geometry
 selection and workspace sizing in ``csrc/capi.hip``, the launchers, and the
 CPython argument parser ``csrc/vbhfast.c`` -- is rebuilt with AddressSanitizer
-and UndefinedBehaviorSanitizer in a copy of the repository, and the CPU test
+and UndefinedBehaviorSanitizer in a copy of the repository (the release library
+and the bounds-checked libvbhip_debug.so alike), and the CPU test
 tier of the C ABI and the unified API runs against it with the sanitizer
 runtime preloaded.  Device code is built exactly as for the product (the GPU
 sanitizer is not used: only host code is instrumented, through ``-Xarch_host``
@@ -62,29 +63,37 @@ def copy_tree(dst: Path) -> Path:
     return dst
 
 
+LIBS = ((False, "libvbhip.so"), (True, "libvbhip_debug.so"))
+
+
 def build_sanitized(tree: Path) -> None:
     pkg = tree / "dslperfgap_amd"
     obj_dir = pkg / "_build"
-    obj_dir.mkdir(exist_ok=True)
+    (obj_dir / "debug").mkdir(parents=True, exist_ok=True)
     hipcc = b._hipcc()
     flags = [f if not f.startswith("-I") else f"-I{tree / 'include'}" for f in b.DEVICE_FLAGS]
 
-    def compile_one(src: Path) -> Path:
-        obj = obj_dir / (src.stem + ".o")
-        cmd = [hipcc, *flags, *HOST_SAN, "-c", str(src), "-o", str(obj)]
+    def compile_one(unit) -> Path:
+        src, debug = unit
+        obj = (obj_dir / "debug" if debug else obj_dir) / (src.stem + ".o")
+        cmd = [hipcc, *flags, *HOST_SAN, *(["-DVBH_DEBUG_BOUNDS"] if debug else []), "-c",
+               str(src), "-o", str(obj)]
         res = subprocess.run(cmd, capture_output=True, text=True)
         if res.returncode != 0:
             raise RuntimeError(f"hipcc (sanitized) failed for {src.name}:\n{res.stderr[-4000:]}")
         return obj
 
     sources = sorted((pkg / "csrc").glob("*.hip"))
-    with ThreadPoolExecutor(max_workers=min(len(sources), os.cpu_count() or 1)) as pool:
-        objs = list(pool.map(compile_one, sources))
-    cmd = [hipcc, f"--offload-arch={b.ARCH}", "-shared", "-fPIC", *HOST_SAN,
-           "-Xarch_host", "-shared-libsan", "-o", str(pkg / "libvbhip.so"), *map(str, objs)]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"sanitized link failed:\n{res.stderr[-4000:]}")
+    units = [(src, debug) for debug, _ in LIBS for src in sources]
+    with ThreadPoolExecutor(max_workers=min(len(units), os.cpu_count() or 1)) as pool:
+        objs = list(pool.map(compile_one, units))
+    for i, (_, name) in enumerate(LIBS):
+        cmd = [hipcc, f"--offload-arch={b.ARCH}", "-shared", "-fPIC", *HOST_SAN,
+               "-Xarch_host", "-shared-libsan", "-o", str(pkg / name),
+               *map(str, objs[i * len(sources):(i + 1) * len(sources)])]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"sanitized link of {name} failed:\n{res.stderr[-4000:]}")
     clang = "/opt/rocm/llvm/bin/clang"
     fast = pkg / ("_vbhfast" + sysconfig.get_config_var("EXT_SUFFIX"))
     cmd = [clang, "-O1", "-g", "-shared", "-fPIC", "-Wall", "-Werror", "-fno-omit-frame-pointer",
@@ -94,7 +103,9 @@ def build_sanitized(tree: Path) -> None:
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"sanitized _vbhfast build failed:\n{res.stderr[-4000:]}")
-    (pkg / "libvbhip.srchash").write_text(b.source_hash(pkg, tree / "include") + "\n")
+    digest = b.source_hash(pkg, tree / "include") + "\n"
+    for _, name in LIBS:
+        (pkg / name).with_suffix(".srchash").write_text(digest)
 
 
 def instrumented(path: Path) -> bool:
@@ -112,7 +123,7 @@ def run(tests=None, keep: str | None = None) -> subprocess.CompletedProcess:
         tree = copy_tree(tmp / "repo")
         build_sanitized(tree)
         pkg = tree / "dslperfgap_amd"
-        for so in [pkg / "libvbhip.so", *pkg.glob("_vbhfast*.so")]:
+        for so in [*(pkg / name for _, name in LIBS), *pkg.glob("_vbhfast*.so")]:
             if not instrumented(so):
                 raise RuntimeError(f"{so.name} is not instrumented")
         env = {k: v for k, v in os.environ.items() if k not in ("VBHIP_LIB", "PYTHONPATH")}

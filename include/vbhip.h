@@ -38,6 +38,7 @@ extern "C" {
 #define VBH_E_INVALID (-1)   /* bad size, null pointer, bad flag            */
 #define VBH_E_DTYPE (-2)     /* unsupported dtype or dtype combination       */
 #define VBH_E_RANGE (-3)     /* size beyond what the kernels index (2^31-1)  */
+#define VBH_E_UNSUPPORTED (-4) /* not available in this build of the library */
 
 /* operation codes for vbh_tune_override */
 #define VBH_OP_LAYER_NORM 0
@@ -280,6 +281,23 @@ int64_t vbh_stream_read_partial_bytes(int64_t bytes);
                                         written through the L2 (device scope) */
 #define VBH_TUNE_NO_WRITE_THROUGH 32 /* keep output stores in the L2            */
 int vbh_tune_override(int op, int tpr, int block, int flags);
+
+/* Debug bounds checks.  libvbhip_debug.so is the library built with
+ * VBH_DEBUG_BOUNDS: there every global-memory access of every kernel first
+ * checks that its bytes lie inside the buffer it belongs to (each kernel's
+ * extent of that buffer, from the entry point's sizes); an access that fails
+ * is not made (a load yields zeros, a store is dropped) and is counted.
+ * vbh_debug_bounds waits for the device, writes the number of failed checks
+ * since the last clear to *failed and, when there were any, "<file>:<line>" of
+ * the first failing buffer's description to `where` (when non-null), and with
+ * clear != 0 resets the count.  vbh_debug_bounds_slack takes `bytes` off the
+ * end of every buffer's allowed extent (0 restores), so that a test can watch
+ * checks fail, on accesses that are then skipped rather than made.  Both act
+ * on the current device.  The release library returns VBH_E_UNSUPPORTED.
+ * No counterpart in the reference (its kernels are Python DSL code); this is
+ * the debug-build bounds check for the library's own kernels. */
+int vbh_debug_bounds(int64_t* failed, char* where, int64_t where_len, int clear);
+int vbh_debug_bounds_slack(int64_t bytes);
 
 #ifdef __cplusplus
 }

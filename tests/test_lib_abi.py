@@ -368,3 +368,42 @@ def test_header_change_is_a_source_change(tmp_path):
     hdr.write_text(hdr.read_text() + "\n/* touched */\n")
     bad = _load_in(tree)
     assert "IMPORTERROR" in bad.stdout and "built from other sources" in bad.stdout, bad.stdout
+
+
+def test_release_library_has_no_bounds_checks():
+    """The debug-bounds entry points exist in the release library and say it
+    is not the checked build (before any HIP call)."""
+    n = ctypes.c_int64(-1)
+    _expect(_lib.E_UNSUPPORTED, "vbh_debug_bounds", ctypes.byref(n), None, 0, 1,
+            match="VBH_DEBUG_BOUNDS")
+    _expect(_lib.E_UNSUPPORTED, "vbh_debug_bounds_slack", 16, match="VBH_DEBUG_BOUNDS")
+
+
+def test_debug_library_exports_the_abi():
+    """libvbhip_debug.so, the bounds-checked build, exports the header's ABI
+    and rejects bad arguments of its debug entry points before any HIP call
+    (loaded in a child process, next to no other copy of the library)."""
+    import subprocess
+    import sys
+
+    from dslperfgap_amd.build import DEBUG_LIB_PATH
+
+    assert DEBUG_LIB_PATH.exists(), "run `python -m dslperfgap_amd.build` first"
+    code = f"""
+import ctypes, sys
+lib = ctypes.CDLL({str(DEBUG_LIB_PATH)!r})
+names = {sorted(_declared())!r}
+missing = [n for n in names if not hasattr(lib, n)]
+assert not missing, missing
+assert lib.vbh_abi_version() == {_lib.ABI_VERSION}
+lib.vbh_debug_bounds.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_int64, ctypes.c_int]
+assert lib.vbh_debug_bounds(None, None, 0, 0) == {_lib.E_INVALID}
+lib.vbh_debug_bounds_slack.argtypes = [ctypes.c_int64]
+assert lib.vbh_debug_bounds_slack(-16) == {_lib.E_INVALID}
+lib.vbh_last_error.restype = ctypes.c_char_p
+print(lib.vbh_last_error().decode())
+"""
+    res = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True,
+                         timeout=120)
+    assert res.returncode == 0, res.stderr[-3000:]
+    assert "negative byte count" in res.stdout
