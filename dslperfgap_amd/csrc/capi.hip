@@ -675,7 +675,8 @@ int64_t vbh_softmax_workspace_bytes(int64_t rows, int64_t cols, int in_dtype) {
   const int vn = 16 / elt_size(in_dtype);
   if (g_tpr[VBH_OP_SOFTMAX].load() || g_block[VBH_OP_SOFTMAX].load()) return 0;
   const RowSplit sp = softmax_split(rows, cols, vn);
-  return sp.segs > 1 ? rows * sp.segs * static_cast<int64_t>(sizeof(float)) : 0;
+  // one SegPair (two fp32 values) per segment
+  return sp.segs > 1 ? rows * sp.segs * 2 * static_cast<int64_t>(sizeof(float)) : 0;
 }
 
 int vbh_softmax_fwd_ws(const void* x, void* y, int64_t rows, int64_t cols, int in_dtype,
@@ -701,9 +702,9 @@ int vbh_softmax_fwd_ws(const void* x, void* y, int64_t rows, int64_t cols, int i
   const int64_t need = vbh_softmax_workspace_bytes(rows, cols, in_dtype);
   if (need > 0 && (vec_ok || mis_ok) && workspace != nullptr && workspace_bytes >= need &&
       aligned16(workspace)) {
-    // segment logsumexps (fp32): the [rows * segs, cols / segs] view, or the
-    // MIS kernel's segment mode; then one pass over x that combines each row's
-    // segments and writes y
+    // segment SegPairs (fp32 max, sum of exp): the [rows * segs, cols / segs]
+    // view, or the MIS kernel's segment mode; then one pass over x that
+    // combines each row's segments and writes y
     const RowSplit sp = softmax_split(rows, cols, vn);
     const int segs = sp.segs;
     const int64_t units = rows * segs;
@@ -713,13 +714,13 @@ int vbh_softmax_fwd_ws(const void* x, void* y, int64_t rows, int64_t cols, int i
     g2.mis = !vec_ok;
     if (vec_ok || use_mis(g1, vn)) {
       if (int rc = check_grid(units, g1)) return rc;
-      float* seg_lse = static_cast<float*>(workspace);
+      float* seg_pairs = static_cast<float*>(workspace);
       hipError_t e =
-          vec_ok ? launch_logsumexp(x, seg_lse, units, seg_cols, in_dtype, kF32, g1, s)
-                 : launch_logsumexp(x, seg_lse, units, static_cast<int>(cols), in_dtype, kF32,
-                                    g1, s, segs, seg_cols);
+          vec_ok ? launch_logsumexp_pairs(x, seg_pairs, units, seg_cols, in_dtype, g1, s)
+                 : launch_logsumexp_pairs(x, seg_pairs, units, static_cast<int>(cols), in_dtype,
+                                          g1, s, segs, seg_cols);
       if (e == hipSuccess)
-        e = launch_softmax_apply(x, y, seg_lse, rows, static_cast<int>(cols), segs, in_dtype,
+        e = launch_softmax_apply(x, y, seg_pairs, rows, static_cast<int>(cols), segs, in_dtype,
                                  out_dtype, log_mode, g2, s);
       return hip_status(e, "softmax launch");
     }
@@ -761,7 +762,8 @@ int64_t vbh_logsumexp_workspace_bytes(int64_t rows, int64_t cols, int in_dtype) 
   const int vn = 16 / elt_size(in_dtype);
   if (g_tpr[VBH_OP_LOGSUMEXP].load() || g_block[VBH_OP_LOGSUMEXP].load()) return 0;
   const RowSplit sp = split_row(rows, cols, vn, kSplitMaxRows);
-  return sp.segs > 1 ? rows * sp.segs * static_cast<int64_t>(sizeof(float)) : 0;
+  // one SegPair (two fp32 values) per segment
+  return sp.segs > 1 ? rows * sp.segs * 2 * static_cast<int64_t>(sizeof(float)) : 0;
 }
 
 int vbh_logsumexp_fwd_ws(const void* x, void* y, int64_t rows, int64_t cols, int in_dtype,
@@ -782,9 +784,9 @@ int vbh_logsumexp_fwd_ws(const void* x, void* y, int64_t rows, int64_t cols, int
   const int64_t need = vbh_logsumexp_workspace_bytes(rows, cols, in_dtype);
   if (need > 0 && aligned16(x) && workspace != nullptr && workspace_bytes >= need &&
       aligned16(workspace)) {
-    // segment results in fp32, then a logsumexp over each row's segments;
-    // rows of whole vectors as a [rows * segs, seg_cols] view, other rows
-    // through the MIS kernel's segment mode
+    // segment SegPairs in fp32, then each row's combined from them; rows of
+    // whole vectors as a [rows * segs, seg_cols] view, other rows through the
+    // MIS kernel's segment mode
     const RowSplit sp = split_row(rows, cols, vn, kSplitMaxRows);
     const int segs = sp.segs;
     const int64_t units = rows * segs;
@@ -792,14 +794,12 @@ int vbh_logsumexp_fwd_ws(const void* x, void* y, int64_t rows, int64_t cols, int
     Geometry g1 = geometry_for(VBH_OP_LOGSUMEXP, seg_cols, vn, units);
     if (vec_ok || use_mis(g1, vn)) {
       if (int rc = check_grid(units, g1)) return rc;
-      const Geometry g2 = geometry_for(VBH_OP_LOGSUMEXP, segs, segs % 4 == 0 ? 4 : 1, rows);
-      if (int rc = check_grid(rows, g2)) return rc;
+      float* pairs = static_cast<float*>(workspace);
       hipError_t e =
-          vec_ok ? launch_logsumexp(x, workspace, units, seg_cols, in_dtype, kF32, g1, s)
-                 : launch_logsumexp(x, workspace, units, static_cast<int>(cols), in_dtype, kF32,
-                                    g1, s, segs, seg_cols);
-      if (e == hipSuccess)
-        e = launch_logsumexp(workspace, y, rows, segs, kF32, out_dtype, g2, s);
+          vec_ok ? launch_logsumexp_pairs(x, pairs, units, seg_cols, in_dtype, g1, s)
+                 : launch_logsumexp_pairs(x, pairs, units, static_cast<int>(cols), in_dtype, g1,
+                                          s, segs, seg_cols);
+      if (e == hipSuccess) e = launch_logsumexp_combine(pairs, y, rows, segs, out_dtype, s);
       return hip_status(e, "logsumexp launch");
     }
   }
@@ -897,8 +897,9 @@ int vbh_cross_entropy_fwd_ws(const void* logits, const void* labels, int logits_
       p.ncb = segs;
       p.split = 1;
       p.empty_neg_inf = 1;
+      p.pair_out = 1;
       hipError_t e = launch_cross_entropy_fwd(p, g1, s);
-      if (e == hipSuccess) e = launch_cross_entropy_combine(a, p.loss, p.lse, segs, s);
+      if (e == hipSuccess) e = launch_cross_entropy_combine(a, p.loss, p.lse, p.z_loss, segs, s);
       return hip_status(e, "cross_entropy_fwd launch");
     }
   }

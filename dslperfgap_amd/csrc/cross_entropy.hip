@@ -37,6 +37,10 @@ struct CeScalars {
   // as a logsumexp would, not the golden's NaN; the second stage applies the
   // golden's rule to the whole row
   int empty_neg_inf;
+  // first stage of a split row: each segment's SegPair (max of the scaled
+  // logits, sum of exp(x * scale - max)) goes to z_out (max) and lse_out (sum),
+  // both otherwise unused there; ce_combine merges them
+  int pair_out;
   // logit_scale * log2(e): exp(x * scale - m) = 2^(x * exp_scale - m * log2(e)),
   // one FMA per logit ahead of v_exp_f32
   float exp_scale;
@@ -62,6 +66,7 @@ CeScalars make_scalars(float smoothing, float logit_scale, float lse_square_scal
   c.has_smoothing = has_smoothing;
   c.split = split;
   c.empty_neg_inf = 0;
+  c.pair_out = 0;
   c.exp_scale = static_cast<float>(static_cast<double>(logit_scale) * 1.4426950408889634);
   c.scale_pos = logit_scale > 0.f && logit_scale <= 3.4028234663852886e38f;
   return c;
@@ -115,6 +120,14 @@ __device__ __forceinline__ void ce_store(float lse, float sum_logits, bool in_bl
   }
   if (VBH_IN_SPAN(so.loss, loss + idx, sizeof(float))) loss[idx] = l;
   if (VBH_IN_SPAN(so.z, z_out + idx, sizeof(float))) z_out[idx] = z;
+}
+
+// A split row's first stage: the segment's SegPair (max m, sum t of
+// exp(x * scale - m)) over its lse and z_loss slots.
+__device__ __forceinline__ void ce_store_pair(float m, float t, float* lse_out, float* z_out,
+                                              int64_t idx, const CeOutSpans& so) {
+  if (VBH_IN_SPAN(so.lse, lse_out + idx, sizeof(float))) lse_out[idx] = t;
+  if (VBH_IN_SPAN(so.z, z_out + idx, sizeof(float))) z_out[idx] = m;
 }
 
 // Segments whose start is not on a 16-byte boundary (rows not a multiple of
@@ -217,18 +230,29 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
   float se[V], sl[V];
 #pragma unroll
   for (int k = 0; k < V; ++k) se[k] = sl[k] = 0.f;
+  // exp(x * scale - m) of a raw logit x: one FMA ahead of v_exp_f32
+  // (2^(x * scale * log2 e - m * log2 e)), or on a multiply and a subtract
+  // where m is too large for that form (shift_fma_ok)
+  const bool fma_ok = shift_fma_ok(m);
   const float mb = m * kLog2e;
+  const float es = c.exp_scale;
+  auto efma = [=](float x) { return __builtin_amdgcn_exp2f(fmaf(x, es, -mb)); };
+  auto esub = [=](float x) { return fast_exp(x * scale - m); };
+  auto sum_exp = [&](auto ex) {
 #pragma unroll
-  for (int i = 0; i < IT; ++i) {
-    if (i * tpr + g < nvec) {
+    for (int i = 0; i < IT; ++i) {
+      if (i * tpr + g < nvec) {
 #pragma unroll
-      for (int k = 0; k < V; ++k) {
-        const float x = raw_at<T, V>(xr[i], k);
-        se[k] += __builtin_amdgcn_exp2f(fmaf(x, c.exp_scale, -mb));
-        if constexpr (SL) sl[k] += x * scale;
+        for (int k = 0; k < V; ++k) {
+          const float x = raw_at<T, V>(xr[i], k);
+          se[k] += ex(x);
+          if constexpr (SL) sl[k] += x * scale;
+        }
       }
     }
-  }
+  };
+  if (fma_ok) sum_exp(efma);
+  else sum_exp(esub);
 #pragma unroll
   for (int w = V / 2; w >= 1; w /= 2)
 #pragma unroll
@@ -237,11 +261,11 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
       sl[k] += sl[k + w];
     }
   if (hv) {
-    se[0] += __builtin_amdgcn_exp2f(fmaf(hr, c.exp_scale, -mb));
+    se[0] += fma_ok ? efma(hr) : esub(hr);
     sl[0] += hx;
   }
   if (tv) {
-    se[0] += __builtin_amdgcn_exp2f(fmaf(tr, c.exp_scale, -mb));
+    se[0] += fma_ok ? efma(tr) : esub(tr);
     sl[0] += tx;
   }
   const float s = group_allreduce<Sum>(se[0], tpr, lds[1]);
@@ -249,11 +273,17 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
   if constexpr (SL) sum_logits = group_allreduce<Sum>(sl[0], tpr, lds[2]);
 
   if (live && g == 0) {
-    float lse = (fast_log(s) - shift_residual(m, mb) * kLn2) + m;
+    float lse = (fast_log(s) - (fma_ok ? shift_residual(m, mb) : 0.f) * kLn2) + m;
     // all -inf (the sum of logits is -inf, not NaN): -inf in a first stage
     if (c.empty_neg_inf && m == kNegInf && sum_logits == sum_logits) lse = kNegInf;
-    ce_store(lse, sum_logits, in_block, logit_label, ignored, c, loss, lse_out, z_out,
-             static_cast<int64_t>(cb) * n_rows + row, so);
+    const int64_t idx = static_cast<int64_t>(cb) * n_rows + row;
+    ce_store(lse, sum_logits, in_block, logit_label, ignored, c, loss, lse_out, z_out, idx, so);
+    if (c.pair_out) {
+      const float t = m == kNegInf
+                          ? 0.f
+                          : (fma_ok ? s * __builtin_amdgcn_exp2f(-shift_residual(m, mb)) : s);
+      ce_store_pair(m, t, lse_out, z_out, idx, so);
+    }
   }
 }
 
@@ -320,52 +350,46 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_stream(
   float logit_label = 0.f;
   if (!ignored && in_block && VBH_IN_SPAN(sx, logits + row * ld + adj, sizeof(T)))
     logit_label = static_cast<float>(logits[row * ld + adj]) * c.logit_scale;
-  ce_store(lse, gl, in_block, logit_label, ignored, c, loss, lse_out, z_out,
-           static_cast<int64_t>(cb) * n_rows + row, so);
+  const int64_t idx = static_cast<int64_t>(cb) * n_rows + row;
+  ce_store(lse, gl, in_block, logit_label, ignored, c, loss, lse_out, z_out, idx, so);
+  if (c.pair_out) ce_store_pair(has_nan ? __builtin_nanf("") : gm, finite ? gs : 0.f, lse_out,
+                                z_out, idx, so);
 }
 
 // Second stage of a split row (one column block per row, cut into `segs`
-// segments that a first stage reduced with SPLIT semantics into seg_loss /
-// seg_lse at flat index k * n_rows + row).  One lane per row: the row's lse is
-// the logsumexp of its segments' lse under the golden's rule (a NaN logit, a
-// +inf or an all -inf row give NaN: every segment lse NaN or -inf), and the
+// segments that a first stage reduced with SPLIT semantics into seg_loss, and
+// into SegPairs seg_max / seg_sum, at flat index k * n_rows + row).  One lane
+// per row: the row's lse = M + log S from its segments' pairs under the
+// golden's rule (a NaN logit, a +inf or an all -inf row give NaN), and the
 // loss adds the lse term the first stage left out (pytorch_impl.py:54-70):
 // lse where the row holds the label, smoothing * lse elsewhere with smoothing,
 // 0 with SPLIT; plus z = lse_square_scale * lse^2 without SPLIT.  The segment
 // losses sum to the rest of the golden's loss (-logit_label and the smoothing
 // sums are additive over segments).
 __global__ __launch_bounds__(256) void ce_combine(
-    const float* __restrict__ seg_loss, const float* __restrict__ seg_lse,
-    const void* __restrict__ labels, int label_i64, float* __restrict__ loss,
-    float* __restrict__ lse_out, float* __restrict__ z_out, int64_t n_rows, int n_cols,
-    int segs, CeScalars c) {
+    const float* __restrict__ seg_loss, const float* __restrict__ seg_sum,
+    const float* __restrict__ seg_max, const void* __restrict__ labels, int label_i64,
+    float* __restrict__ loss, float* __restrict__ lse_out, float* __restrict__ z_out,
+    int64_t n_rows, int n_cols, int segs, CeScalars c) {
   const int64_t row = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (row >= n_rows) return;
-  const Span ssl = VBH_SPAN(seg_loss, segs * n_rows), sse = VBH_SPAN(seg_lse, segs * n_rows);
+  const Span ssl = VBH_SPAN(seg_loss, segs * n_rows), sss = VBH_SPAN(seg_sum, segs * n_rows);
+  const Span ssm = VBH_SPAN(seg_max, segs * n_rows);
   const Span sb = VBH_LABEL_SPAN(labels, label_i64, n_rows);
   const CeOutSpans so{VBH_SPAN(loss, n_rows), VBH_SPAN(lse_out, n_rows), VBH_SPAN(z_out, n_rows)};
-  float mx = kNegInf, rest = 0.f;
-  bool nan = false;
+  float rest = 0.f;
   for (int k = 0; k < segs; ++k) {
-    float v, sl;
-    load_f32<float, 1>(seg_lse + static_cast<int64_t>(k) * n_rows + row, &v, sse);
-    nan |= v != v;
-    mx = fmaxf(mx, v);
+    float sl;
     load_f32<float, 1>(seg_loss + static_cast<int64_t>(k) * n_rows + row, &sl, ssl);
     rest += sl;
   }
-  float lse;
-  if (nan || mx == kNegInf) {
-    lse = __builtin_nanf("");
-  } else {
-    float s = 0.f;
-    for (int k = 0; k < segs; ++k) {
-      float v;
-      load_f32<float, 1>(seg_lse + static_cast<int64_t>(k) * n_rows + row, &v, sse);
-      s += fast_exp(v - mx);
-    }
-    lse = fast_log(s) + mx;
-  }
+  const RowPairs rp = combine_seg_pairs(segs, [&](int k, float* mt) {
+    const int64_t i = static_cast<int64_t>(k) * n_rows + row;
+    load_f32<float, 1>(seg_max + i, &mt[0], ssm);
+    load_f32<float, 1>(seg_sum + i, &mt[1], sss);
+  });
+  // a +inf max gives inf - inf in the golden: NaN, as an all -inf row does
+  const float lse = rp.nan || __builtin_isinf(rp.m) ? __builtin_nanf("") : fast_log(rp.s) + rp.m;
   if (VBH_IN_SPAN(so.lse, lse_out + row, sizeof(float))) lse_out[row] = lse;
   const int64_t label = read_label(labels, label_i64, row, sb);
   float l = 0.f, z = 0.f;
@@ -394,15 +418,21 @@ constexpr int kBwdLanes = kCeBwdLanes;
 // 2^(x * exp_scale - lb) * 2^-res with lb = lse * log2 e rounded and res its
 // rounding error (exact, one FMA), so each element costs one FMA ahead of
 // v_exp_f32; 2^-res rides on the factor (1 + 2 * lss * lse) that multiplies p.
+// Rows whose lse is too large for that form (shift_fma_ok; `fma` false) take
+// exp(x * logit_scale - lse) on a multiply and a subtract, with pf = 1 + 2 * lss * lse.
 struct CeBwdRow {
-  float lb, pf, hit, smooth_neg, scale;
+  float lse, lb, pf, hit, smooth_neg, scale;
+  bool fma;
 };
 
 // dlogits of one element: q = p + 2 * lss * lse * p, minus the (smoothed)
-// one-hot (`is_label`); times dloss * logit_scale.
+// one-hot (`is_label`); times dloss * logit_scale.  FMA: the row's form of p.
+template <bool FMA>
 __device__ __forceinline__ float ce_grad(float xv, bool is_label, const CeBwdRow& b,
                                          const CeScalars& c) {
-  float q = __builtin_amdgcn_exp2f(fmaf(xv, c.exp_scale, -b.lb)) * b.pf;
+  const float p = FMA ? __builtin_amdgcn_exp2f(fmaf(xv, c.exp_scale, -b.lb))
+                      : fast_exp(xv * c.logit_scale - b.lse);
+  float q = p * b.pf;
   if (is_label) q = q - b.hit;
   if (c.has_smoothing) q = q - b.smooth_neg;
   return b.scale * q;
@@ -449,8 +479,11 @@ __global__ __launch_bounds__(kBwdLanes) void ce_bwd_tiles(
   const float dl = label != c.ignored_index ? dlv : 0.f;
   const int64_t adj = label - c.class_start;
   CeBwdRow b;
+  b.lse = lse_r;
+  // the workgroup's tile is one row's: a scalar branch on the row's form
+  b.fma = __builtin_amdgcn_readfirstlane(static_cast<int>(shift_fma_ok(lse_r))) != 0;
   b.lb = lse_r * kLog2e;
-  b.pf = __builtin_amdgcn_exp2f(-shift_residual(lse_r, b.lb)) *
+  b.pf = (b.fma ? __builtin_amdgcn_exp2f(-shift_residual(lse_r, b.lb)) : 1.0f) *
          (1.0f + c.two_lse_square_scale * lse_r);
   // (dl * logit_scale) is a Python-double product in the golden
   b.scale = static_cast<float>(static_cast<double>(dl) * c.logit_scale);
@@ -462,8 +495,13 @@ __global__ __launch_bounds__(kBwdLanes) void ce_bwd_tiles(
   if (j < nvec) {
     const int64_t rel = adj - head - static_cast<int64_t>(j) * V;  // label's place in r
     float o[V];
+    if (b.fma) {
 #pragma unroll
-    for (int k = 0; k < V; ++k) o[k] = ce_grad(raw_at<T, V>(r, k), rel == k, b, c);
+      for (int k = 0; k < V; ++k) o[k] = ce_grad<true>(raw_at<T, V>(r, k), rel == k, b, c);
+    } else {
+#pragma unroll
+      for (int k = 0; k < V; ++k) o[k] = ce_grad<false>(raw_at<T, V>(r, k), rel == k, b, c);
+    }
     out.template store<V>(dr + static_cast<int64_t>(j) * V, static_cast<int>(threadIdx.x) * V, o,
                           sd);
   }
@@ -472,14 +510,15 @@ __global__ __launch_bounds__(kBwdLanes) void ce_bwd_tiles(
     if (t < head) {
       float v;
       load_f32<T, 1>(logits + in0 + t, &v, sx);
-      const float o = ce_grad(v, adj == t, b, c);
+      const float o = b.fma ? ce_grad<true>(v, adj == t, b, c) : ce_grad<false>(v, adj == t, b, c);
       store_from_f32<T, 1>(dr - head + t, &o, sd);
     }
     if (t < tail) {
       const int64_t k = static_cast<int64_t>(nvec) * V + t;
       float v;
       load_f32<T, 1>(lr + k, &v, sx);
-      const float o = ce_grad(v, adj == head + k, b, c);
+      const float o = b.fma ? ce_grad<true>(v, adj == head + k, b, c)
+                            : ce_grad<false>(v, adj == head + k, b, c);
       store_from_f32<T, 1>(dr + k, &o, sd);
     }
   }
@@ -493,6 +532,7 @@ hipError_t launch_cross_entropy_fwd(const CeArgs& a, const Geometry& g, hipStrea
       make_scalars(a.smoothing, a.logit_scale, a.lse_square_scale, a.total_classes,
                    a.ignored_index, a.class_start, a.has_smoothing, a.split);
   c.empty_neg_inf = a.empty_neg_inf;
+  c.pair_out = a.pair_out;
   const int64_t nseg = a.n_rows * a.ncb;
   dispatch_float_type(a.logits_dt, [&](auto tt) {
     using T = typename decltype(tt)::type;
@@ -535,12 +575,13 @@ hipError_t launch_cross_entropy_fwd(const CeArgs& a, const Geometry& g, hipStrea
 }
 
 hipError_t launch_cross_entropy_combine(const CeArgs& a, const float* seg_loss,
-                                        const float* seg_lse, int segs, hipStream_t s) {
+                                        const float* seg_sum, const float* seg_max, int segs,
+                                        hipStream_t s) {
   const CeScalars c =
       make_scalars(a.smoothing, a.logit_scale, a.lse_square_scale, a.total_classes,
                    a.ignored_index, a.class_start, a.has_smoothing, a.split);
   launch_kernel(ce_combine, dim3((a.n_rows + 255) / 256), dim3(256), 0, s, seg_loss,
-                     seg_lse, a.labels, a.label_i64, a.loss, a.lse, a.z_loss, a.n_rows,
+                     seg_sum, seg_max, a.labels, a.label_i64, a.loss, a.lse, a.z_loss, a.n_rows,
                      a.n_cols, segs, c);
   return hipGetLastError();
 }

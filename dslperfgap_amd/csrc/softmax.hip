@@ -15,6 +15,7 @@
 // ViperBench/logsumexp/pytorch_impl.py:3-5 (torch.logsumexp, dim=-1: the max
 // used for the shift is replaced by 0 when it is infinite).
 #include <algorithm>
+#include <type_traits>
 
 #include "vbh_device.h"
 #include "vbh_launch.h"
@@ -24,6 +25,11 @@ namespace vbh {
 namespace {
 
 constexpr float kNegInf = -__builtin_huge_valf();
+
+// fp16 values stay within 65504 < 2^24, so a row of fp16 inputs always takes
+// the one-FMA exp form (shift_fma_ok): the kernels leave the other one out.
+template <typename T>
+constexpr bool kFarShiftFree = std::is_same<T, _Float16>::value;
 
 // The lane's vectors of the row; those past the row's end hold -inf, which
 // the row max ignores and exp maps to 0, so lane_max and lane_sum_exp need no
@@ -60,11 +66,11 @@ __device__ __forceinline__ float lane_max(const typename Raw<T, V>::type (&xr)[I
   return r;
 }
 
-// sum over the lane's values of exp(v - m), given mb = m * log2 e (see
-// exp_shifted; the -inf filler adds 0).  KEEP (fp32 rows only) leaves each
+// sum over the lane's values of exp(v - m), in the row's form `ex` (ExpFma or
+// ExpSub; the -inf filler adds 0).  KEEP (fp32 rows only) leaves each
 // exp(v - m) in place of v, for a softmax output pass that then only multiplies.
-template <typename T, int V, int IT, bool KEEP = false>
-__device__ __forceinline__ float lane_sum_exp(typename Raw<T, V>::type (&xr)[IT], float mb) {
+template <typename T, int V, int IT, bool KEEP = false, class Ex>
+__device__ __forceinline__ float lane_sum_exp(typename Raw<T, V>::type (&xr)[IT], Ex ex) {
   static_assert(!KEEP || sizeof(T) == 4, "exp values are kept in fp32 registers only");
   float a[V];
 #pragma unroll
@@ -73,7 +79,7 @@ __device__ __forceinline__ float lane_sum_exp(typename Raw<T, V>::type (&xr)[IT]
   for (int i = 0; i < IT; ++i)
 #pragma unroll
     for (int k = 0; k < V; ++k) {
-      const float e = exp_shifted(raw_at<T, V>(xr[i], k), mb);
+      const float e = ex(raw_at<T, V>(xr[i], k));
       if constexpr (KEEP) {
         if constexpr (V == 1) xr[i] = e;
         else xr[i][k] = e;
@@ -138,10 +144,14 @@ __global__ __launch_bounds__(kMaxBlock) void softmax_rows(const Ti* __restrict__
   reload_barrier<Ti, V, IT>(xr);
   // fp32 softmax keeps each exp(x - m) for the output pass
   constexpr bool KEEP = !LOG && sizeof(Ti) == 4;
+  const bool fma_ok = kFarShiftFree<Ti> || shift_fma_ok(m);
   const float mb = m * kLog2e;
-  float le = lane_sum_exp<Ti, V, IT, KEEP>(xr, mb);
-  if (hv) le += exp_shifted(hx, mb);
-  if (tv) le += exp_shifted(tx, mb);
+  const ExpFma efma{mb};
+  const ExpSub esub{m};
+  float le = fma_ok ? lane_sum_exp<Ti, V, IT, KEEP>(xr, efma)
+                    : lane_sum_exp<Ti, V, IT, KEEP>(xr, esub);
+  if (hv) le += fma_ok ? efma(hx) : esub(hx);
+  if (tv) le += fma_ok ? efma(tx) : esub(tx);
   const float s = group_allreduce<Sum>(le, tpr, lds[1]);
   if (!live) return;
   reload_barrier<Ti, V, IT>(xr);
@@ -149,29 +159,35 @@ __global__ __launch_bounds__(kMaxBlock) void softmax_rows(const Ti* __restrict__
   const OutWindow<To, SP> out(y + first * cols, std::min<int64_t>(rpb, rows - first) * cols);
   To* yr = y + start + mr.head;
   const int yoff = static_cast<int>(row - first) * cols + mr.head;
-  const float ls = LOG ? fast_log(s) - shift_residual(m, mb) * kLn2 : 0.f;
+  const float ls = LOG ? fast_log(s) - (fma_ok ? shift_residual(m, mb) : 0.f) * kLn2 : 0.f;
   const float r = LOG ? 0.f : __builtin_amdgcn_rcpf(s);  // v_rcp_f32, 1 ulp
+  auto emit = [&](auto ex) {
 #pragma unroll
-  for (int i = 0; i < IT; ++i) {
-    const int j = i * tpr + g;
-    if (j < nvec) {
-      float o[V];
+    for (int i = 0; i < IT; ++i) {
+      const int j = i * tpr + g;
+      if (j < nvec) {
+        float o[V];
 #pragma unroll
-      for (int k = 0; k < V; ++k) {
-        const float v = raw_at<Ti, V>(xr[i], k);
-        if constexpr (LOG) o[k] = (v - m) - ls;
-        else if constexpr (KEEP) o[k] = v * r;
-        else o[k] = exp_shifted(v, mb) * r;
+        for (int k = 0; k < V; ++k) {
+          const float v = raw_at<Ti, V>(xr[i], k);
+          if constexpr (LOG) o[k] = (v - m) - ls;
+          else if constexpr (KEEP) o[k] = v * r;
+          else o[k] = ex(v) * r;
+        }
+        out.template store<V>(yr + static_cast<int64_t>(j) * V, yoff + j * V, o, sy);
       }
-      out.template store<V>(yr + static_cast<int64_t>(j) * V, yoff + j * V, o, sy);
     }
-  }
+  };
+  // only a 16-bit softmax recomputes its exps here
+  if constexpr (LOG || KEEP) emit(efma);
+  else if (fma_ok) emit(efma);
+  else emit(esub);
   if (hv) {
-    const float o = LOG ? (hx - m) - ls : exp_shifted(hx, mb) * r;
+    const float o = LOG ? (hx - m) - ls : (fma_ok ? efma(hx) : esub(hx)) * r;
     store_from_f32<To, 1>(y + start + g, &o, sy);
   }
   if (tv) {
-    const float o = LOG ? (tx - m) - ls : exp_shifted(tx, mb) * r;
+    const float o = LOG ? (tx - m) - ls : (fma_ok ? efma(tx) : esub(tx)) * r;
     store_from_f32<To, 1>(yr + static_cast<int64_t>(nvec) * V + g, &o, sy);
   }
 }
@@ -179,8 +195,9 @@ __global__ __launch_bounds__(kMaxBlock) void softmax_rows(const Ti* __restrict__
 // `rows` units of `cols` columns.  MIS launches may instead split each row of
 // `cols` columns into `segs` segments of `seg_cols` columns (the last one
 // shorter): unit u is then segment u % segs of row u / segs, and y[u] its
-// logsumexp.
-template <typename Ti, typename To, int V, int IT, bool NT, bool MIS>
+// logsumexp.  PAIR (first stage of a split row; To is float): y[2u], y[2u+1]
+// get the unit's SegPair -- its max and its sum of exp(x - max) -- instead.
+template <typename Ti, typename To, int V, int IT, bool NT, bool MIS, bool PAIR = false>
 __global__ __launch_bounds__(kMaxBlock) void logsumexp_rows(const Ti* __restrict__ x,
                                                             To* __restrict__ y, int64_t rows,
                                                             int cols, int tpr, int segs,
@@ -194,7 +211,7 @@ __global__ __launch_bounds__(kMaxBlock) void logsumexp_rows(const Ti* __restrict
   if (!live) row = rows - 1;
   // x holds rows / segs rows of `cols` in the MIS segment mode
   const Span sx = VBH_SPAN(x, (MIS && segs > 1 ? rows / segs : rows) * cols);
-  const Span sy = VBH_SPAN(y, rows);
+  const Span sy = VBH_SPAN(y, PAIR ? 2 * rows : rows);
   int64_t start = row * cols;
   int len = cols;
   if (MIS && segs > 1) {
@@ -216,31 +233,66 @@ __global__ __launch_bounds__(kMaxBlock) void logsumexp_rows(const Ti* __restrict
   float lm = lane_max<Ti, V, IT>(xr);
   if (hv) lm = max_nan(lm, hx);
   if (tv) lm = max_nan(lm, tx);
-  float m = group_allreduce<Max>(lm, tpr, lds[0]);
+  const float m_raw = group_allreduce<Max>(lm, tpr, lds[0]);
   reload_barrier<Ti, V, IT>(xr);
-  if (__builtin_isinf(m)) m = 0.f;
+  const float m = __builtin_isinf(m_raw) ? 0.f : m_raw;
+  const bool fma_ok = kFarShiftFree<Ti> || shift_fma_ok(m);
   const float mb = m * kLog2e;
-  float le = lane_sum_exp<Ti, V, IT>(xr, mb);
-  if (hv) le += exp_shifted(hx, mb);
-  if (tv) le += exp_shifted(tx, mb);
+  const ExpFma efma{mb};
+  const ExpSub esub{m};
+  float le = fma_ok ? lane_sum_exp<Ti, V, IT>(xr, efma) : lane_sum_exp<Ti, V, IT>(xr, esub);
+  if (hv) le += fma_ok ? efma(hx) : esub(hx);
+  if (tv) le += fma_ok ? efma(tx) : esub(tx);
   const float s = group_allreduce<Sum>(le, tpr, lds[1]);
   if (live && g == 0) {
-    const float r = (fast_log(s) - shift_residual(m, mb) * kLn2) + m;
-    store_from_f32<To, 1>(y + row, &r, sy);
+    if constexpr (PAIR) {
+      // the sum relative to m itself (2^residual taken back out); an all -inf
+      // segment sums to 0
+      const float t = m_raw == kNegInf
+                          ? 0.f
+                          : (fma_ok ? s * __builtin_amdgcn_exp2f(-shift_residual(m, mb)) : s);
+      const float pair[2] = {m_raw, t};
+      store_from_f32<float, 2>(reinterpret_cast<float*>(y) + 2 * row, pair, sy);
+    } else {
+      const float r = (fast_log(s) - (fma_ok ? shift_residual(m, mb) : 0.f) * kLn2) + m;
+      store_from_f32<To, 1>(y + row, &r, sy);
+    }
   }
+}
+
+// Second stage of a split logsumexp: one lane per row combines the row's
+// `segs` SegPairs (pairs[2 * (row * segs + k)]) under torch's rules (NaN
+// anywhere: NaN; a +inf max: +inf; all -inf: -inf).
+template <typename To>
+__global__ __launch_bounds__(256) void logsumexp_pairs_combine(const float* __restrict__ pairs,
+                                                               To* __restrict__ y, int64_t rows,
+                                                               int segs) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (row >= rows) return;
+  const Span sp = VBH_SPAN(pairs, 2 * rows * segs), sy = VBH_SPAN(y, rows);
+  const RowPairs rp = combine_seg_pairs(segs, [&](int k, float* mt) {
+    load_f32<float, 2>(pairs + 2 * (row * segs + k), mt, sp);
+  });
+  float r;
+  if (rp.nan) r = __builtin_nanf("");
+  else if (__builtin_isinf(rp.m)) r = rp.m;
+  else r = fast_log(rp.s) + rp.m;
+  store_from_f32<To, 1>(y + row, &r, sy);
 }
 
 // ---------------------------------------------------------------------------
 // second stage of a split softmax / log_softmax (rows of whole vectors)
 //
-// The first stage writes the logsumexp of each of a row's `segs` equal
-// segments (logsumexp_rows over the [rows * segs, cols / segs] view).  Here
-// one kApplyLanes-lane workgroup owns one tile of kApplyLanes vectors of a row,
-// one 16-byte vector per lane (the copy kernel's shape).  Every wave combines
-// the row's segment results itself (segs <= 64: one per lane): M = their max,
-// log S = log(sum exp(l_k - M)), and writes (x - M) - log S or its exp.  A row
-// with a NaN segment, a +inf segment (a +inf element) or only -inf segments
-// (only -inf elements) is all NaN, as torch's softmax / log_softmax give.
+// The first stage writes the SegPair (max m_k, sum t_k of exp(x - m_k)) of
+// each of a row's `segs` segments (logsumexp_rows<PAIR> over the
+// [rows * segs, cols / segs] view).  Here one kApplyLanes-lane workgroup owns
+// one tile of kApplyLanes vectors of a row, one 16-byte vector per lane (the
+// copy kernel's shape).  Every wave combines the row's pairs itself
+// (segs <= 64: one per lane): M = max m_k, the row max, and
+// S = sum t_k exp(m_k - M), and writes (x - M) - log S or its exp.  (A
+// logsumexp per segment would not do: where |M| is large, m_k + log t_k rounds
+// the log away.)  A row with a NaN, a +inf element or only -inf elements is all
+// NaN, as torch's softmax / log_softmax give.
 // MIS rows (not whole vectors; the first stage ran the MIS segment mode): the
 // tiles cover each row's aligned body, and tile 0 also writes the row's scalar
 // head and tail (lanes t < head, t < tail).
@@ -248,7 +300,7 @@ __global__ __launch_bounds__(kMaxBlock) void logsumexp_rows(const Ti* __restrict
 
 template <typename Ti, typename To, int V, bool LOG, int SP, bool MIS>
 __global__ __launch_bounds__(kApplyLanes) void softmax_apply_tiles(
-    const Ti* __restrict__ x, To* __restrict__ y, const float* __restrict__ seg_lse, int cols,
+    const Ti* __restrict__ x, To* __restrict__ y, const float* __restrict__ seg_pairs, int cols,
     int segs, uint32_t tiles_per_row) {
   const uint32_t row32 = blockIdx.x / tiles_per_row;
   const int tix = static_cast<int>(blockIdx.x - row32 * tiles_per_row);
@@ -256,7 +308,8 @@ __global__ __launch_bounds__(kApplyLanes) void softmax_apply_tiles(
   // the grid is the row count times tiles_per_row
   const Span sx = VBH_SPAN(x, static_cast<int64_t>(gridDim.x / tiles_per_row) * cols);
   const Span sy = VBH_SPAN(y, static_cast<int64_t>(gridDim.x / tiles_per_row) * cols);
-  const Span sl = VBH_SPAN(seg_lse, static_cast<int64_t>(gridDim.x / tiles_per_row) * segs);
+  const Span sl =
+      VBH_SPAN(seg_pairs, static_cast<int64_t>(gridDim.x / tiles_per_row) * segs * 2);
   const int64_t start = row * cols;
   const MisRow mr = MIS ? mis_row<V>(start, cols) : MisRow{0, cols / V, 0};
   const int nvec = mr.nvec;
@@ -268,12 +321,13 @@ __global__ __launch_bounds__(kApplyLanes) void softmax_apply_tiles(
 
   const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
   const bool has = lane < segs;
-  float l = kNegInf;
-  if (has) load_f32<float, 1>(seg_lse + row * segs + lane, &l, sl);
-  const float m = wave_allreduce<Max>(l, kWave);
-  const float nan = wave_allreduce<Max>(l != l ? 1.f : 0.f, kWave);
+  float mt[2] = {kNegInf, 0.f};
+  if (has) load_f32<float, 2>(seg_pairs + 2 * (row * segs + lane), mt, sl);
+  const float m = wave_allreduce<Max>(mt[0], kWave);
+  const float nan = wave_allreduce<Max>(mt[0] != mt[0] || mt[1] != mt[1] ? 1.f : 0.f, kWave);
   const bool bad = nan > 0.f || __builtin_isinf(m);
-  const float sum = wave_allreduce<Sum>(has && !bad ? fast_exp(l - m) : 0.f, kWave);
+  const float sum = wave_allreduce<Sum>(
+      has && !bad && mt[0] != kNegInf ? mt[1] * fast_exp(mt[0] - m) : 0.f, kWave);
   const float ls = fast_log(sum);
 
   auto value = [&](float v) {
@@ -389,7 +443,8 @@ __global__ __launch_bounds__(kMaxBlock) void softmax_stream(const Ti* __restrict
   }
 }
 
-template <typename Ti, typename To, int V>
+// PAIR: as logsumexp_rows<PAIR>, the row's SegPair into y[2 row], y[2 row + 1].
+template <typename Ti, typename To, int V, bool PAIR = false>
 __global__ __launch_bounds__(kMaxBlock) void logsumexp_stream(const Ti* __restrict__ x,
                                                               To* __restrict__ y, int cols) {
   __shared__ float lds[3 * kMaxWaves];
@@ -397,14 +452,20 @@ __global__ __launch_bounds__(kMaxBlock) void logsumexp_stream(const Ti* __restri
   const int64_t row = blockIdx.x;
   // one workgroup per row: the grid is the row count
   const Span sx = VBH_SPAN(x, static_cast<int64_t>(gridDim.x) * cols);
-  const Span sy = VBH_SPAN(y, static_cast<int64_t>(gridDim.x));
+  const Span sy = VBH_SPAN(y, static_cast<int64_t>(gridDim.x) * (PAIR ? 2 : 1));
   const RowStats st = stream_stats<Ti, V>(x + row * cols, nvec, lds, sx);
   if (threadIdx.x == 0) {
-    float r;
-    if (st.nan != 0.f) r = __builtin_nanf("");
-    else if (st.m == kNegInf || st.m == -kNegInf) r = st.m;
-    else r = fast_log(st.s) + st.m;
-    store_from_f32<To, 1>(y + row, &r, sy);
+    const bool inf = st.m == kNegInf || st.m == -kNegInf;
+    if constexpr (PAIR) {
+      const float pair[2] = {st.nan != 0.f ? __builtin_nanf("") : st.m, inf ? 0.f : st.s};
+      store_from_f32<float, 2>(reinterpret_cast<float*>(y) + 2 * row, pair, sy);
+    } else {
+      float r;
+      if (st.nan != 0.f) r = __builtin_nanf("");
+      else if (inf) r = st.m;
+      else r = fast_log(st.s) + st.m;
+      store_from_f32<To, 1>(y + row, &r, sy);
+    }
   }
 }
 
@@ -505,46 +566,79 @@ hipError_t launch_softmax(const void* x, void* y, int64_t rows, int cols, int id
   return err;
 }
 
-hipError_t launch_logsumexp(const void* x, void* y, int64_t rows, int cols, int idt, int odt,
-                            const Geometry& g, hipStream_t s, int segs, int seg_cols) {
+namespace {
+
+// logsumexp_rows / logsumexp_stream over `rows` units (PAIR: their SegPairs,
+// fp32, into y)
+template <bool PAIR, class Ti, class To>
+hipError_t launch_logsumexp_units(const void* x, void* y, int64_t rows, int cols,
+                                  const Geometry& g, hipStream_t s, int segs, int seg_cols) {
   hipError_t err = hipErrorInvalidValue;
-  auto body = [&](auto ti, auto to) {
-    using Ti = typename decltype(ti)::type;
-    using To = typename decltype(to)::type;
-    constexpr int VN = Vec<Ti>::n;
-    auto go = [&](auto vc) {
-      constexpr int V = decltype(vc)::value;
-      if (g.stream) {
-        launch_kernel((logsumexp_stream<Ti, To, V>), dim3(rows), dim3(g.block), 0, s,
-                           static_cast<const Ti*>(x), static_cast<To*>(y), cols);
+  constexpr int VN = Vec<Ti>::n;
+  auto go = [&](auto vc) {
+    constexpr int V = decltype(vc)::value;
+    if (g.stream) {
+      launch_kernel((logsumexp_stream<Ti, To, V, PAIR>), dim3(rows), dim3(g.block), 0, s,
+                    static_cast<const Ti*>(x), static_cast<To*>(y), cols);
+      err = hipGetLastError();
+      return;
+    }
+    dispatch_maxit(g.maxit, [&](auto mc) {
+      constexpr int M = decltype(mc)::value;
+      if constexpr (M <= lane_cap(V)) {
+        auto launch = [&](auto kern) {
+          launch_kernel(kern, dim3(grid_for(rows, g)), dim3(g.block), 0, s,
+                        static_cast<const Ti*>(x), static_cast<To*>(y), rows, cols, g.tpr, segs,
+                        seg_cols);
+        };
+        if (V > 1 && g.mis) launch(logsumexp_rows<Ti, To, V, M, true, V != 1, PAIR>);
+        else if (g.nt) launch(logsumexp_rows<Ti, To, V, M, true, false, PAIR>);
+        else launch(logsumexp_rows<Ti, To, V, M, false, false, PAIR>);
         err = hipGetLastError();
-        return;
       }
-      dispatch_maxit(g.maxit, [&](auto mc) {
-        constexpr int M = decltype(mc)::value;
-        if constexpr (M <= lane_cap(V)) {
-          auto launch = [&](auto kern) {
-            launch_kernel(kern, dim3(grid_for(rows, g)), dim3(g.block), 0, s,
-                               static_cast<const Ti*>(x), static_cast<To*>(y), rows, cols,
-                               g.tpr, segs, seg_cols);
-          };
-          if (V > 1 && g.mis) launch(logsumexp_rows<Ti, To, V, M, true, V != 1>);
-          else if (g.nt) launch(logsumexp_rows<Ti, To, V, M, true, false>);
-          else launch(logsumexp_rows<Ti, To, V, M, false, false>);
-          err = hipGetLastError();
-        }
-      });
-    };
-    if (g.v == 1) go(std::integral_constant<int, 1>{});
-    else go(std::integral_constant<int, VN>{});
+    });
   };
-  if (!dispatch_in_out(idt, odt, body) && idt == kF32)
-    // second stage of a split logsumexp: fp32 segment results in, the output type out
-    dispatch_float_type(odt, [&](auto t) { body(TypeTag<float>{}, t); });
+  if (g.v == 1) go(std::integral_constant<int, 1>{});
+  else go(std::integral_constant<int, VN>{});
   return err;
 }
 
-hipError_t launch_softmax_apply(const void* x, void* y, const float* seg_lse, int64_t rows,
+}  // namespace
+
+hipError_t launch_logsumexp(const void* x, void* y, int64_t rows, int cols, int idt, int odt,
+                            const Geometry& g, hipStream_t s, int segs, int seg_cols) {
+  hipError_t err = hipErrorInvalidValue;
+  dispatch_in_out(idt, odt, [&](auto ti, auto to) {
+    using Ti = typename decltype(ti)::type;
+    using To = typename decltype(to)::type;
+    err = launch_logsumexp_units<false, Ti, To>(x, y, rows, cols, g, s, segs, seg_cols);
+  });
+  return err;
+}
+
+hipError_t launch_logsumexp_pairs(const void* x, float* pairs, int64_t units, int cols, int idt,
+                                  const Geometry& g, hipStream_t s, int segs, int seg_cols) {
+  hipError_t err = hipErrorInvalidValue;
+  dispatch_float_type(idt, [&](auto ti) {
+    using Ti = typename decltype(ti)::type;
+    err = launch_logsumexp_units<true, Ti, float>(x, pairs, units, cols, g, s, segs, seg_cols);
+  });
+  return err;
+}
+
+hipError_t launch_logsumexp_combine(const float* pairs, void* y, int64_t rows, int segs,
+                                    int odt, hipStream_t s) {
+  hipError_t err = hipErrorInvalidValue;
+  dispatch_float_type(odt, [&](auto to) {
+    using To = typename decltype(to)::type;
+    launch_kernel(logsumexp_pairs_combine<To>, dim3((rows + 255) / 256), dim3(256), 0, s, pairs,
+                  static_cast<To*>(y), rows, segs);
+    err = hipGetLastError();
+  });
+  return err;
+}
+
+hipError_t launch_softmax_apply(const void* x, void* y, const float* seg_pairs, int64_t rows,
                                 int cols, int segs, int idt, int odt, int log_mode,
                                 const Geometry& g, hipStream_t s) {
   // MIS rows: the tiles cover at most cols / V body vectors per row
@@ -558,7 +652,7 @@ hipError_t launch_softmax_apply(const void* x, void* y, const float* seg_lse, in
       constexpr int SP = decltype(sp)::value;
       auto launch = [&](auto kern) {
         launch_kernel(kern, dim3(rows * tiles), dim3(kApplyLanes), 0, s,
-                           static_cast<const Ti*>(x), static_cast<To*>(y), seg_lse, cols, segs,
+                           static_cast<const Ti*>(x), static_cast<To*>(y), seg_pairs, cols, segs,
                            static_cast<uint32_t>(tiles));
       };
       if (g.mis) {

@@ -468,6 +468,66 @@ __device__ __forceinline__ float shift_residual(float m, float mb) {
   return fmaf(m, kLog2e, -mb);
 }
 
+// The residual is up to half an ulp of m * log2 e, so it grows with |m|: at
+// |m| = 1e9 it reaches 18 (every exp scaled by 2^-18), at 1e10 it is 440 and
+// every exp of the row underflows, and above FLT_MAX / log2 e = 2.36e38 mb
+// itself overflows.  Up to |m| = 2^24 it stays within +-1 (m * log2 e < 2^25,
+// whose ulp is 2), which no row sum can turn into an overflow or a lost term.
+// Rows whose finite shift is larger take exp(x - m) on a subtract instead; the
+// choice is made once per row (shift_fma_ok), outside any barrier.  Infinite
+// and NaN shifts keep the FMA form, whose special values follow x - m.
+constexpr float kShiftFmaMax = 16777216.0f;  // 2^24
+
+__device__ __forceinline__ bool shift_fma_ok(float m) {
+  return !(__builtin_fabsf(m) > kShiftFmaMax) || __builtin_isinf(m);
+}
+
+// exp(x - m) of one row's values, in the form shift_fma_ok picked for the row:
+struct ExpFma {  // 2^(x * log2 e - mb), mb = m * log2 e
+  float mb;
+  __device__ __forceinline__ float operator()(float x) const { return exp_shifted(x, mb); }
+};
+struct ExpSub {  // exp(x - m) on a subtract
+  float m;
+  __device__ __forceinline__ float operator()(float x) const { return fast_exp(x - m); }
+};
+
+// The first stage of a split row writes one SegPair per segment: its max m
+// (NaN if it holds a NaN, -inf if it holds only -inf) and t, the sum over it of
+// exp(x - m) (0 for an all -inf segment).  A second stage merges a row's pairs
+// with combine_seg_pairs: M = max m_k, S = sum t_k * exp(m_k - M) over the
+// segments whose m_k > -inf, and `nan` if any m_k or t_k is NaN (S is then
+// meaningless, as it is when M is infinite).  The row's logsumexp M + log S is
+// then rounded once, as in a single pass; a logsumexp per segment would round
+// m_k + log t_k first, which loses the log entirely where |m_k| is large.
+struct RowPairs {
+  float m, s;
+  bool nan;
+};
+
+// load(k, mt) puts segment k's (m_k, t_k) into mt[0], mt[1]
+template <class Load>
+__device__ __forceinline__ RowPairs combine_seg_pairs(int segs, Load&& load) {
+  const float neg_inf = -__builtin_huge_valf();
+  float mx = neg_inf;
+  bool nan = false;
+  for (int k = 0; k < segs; ++k) {
+    float mt[2];
+    load(k, mt);
+    nan |= mt[0] != mt[0] || mt[1] != mt[1];
+    mx = fmaxf(mx, mt[0]);
+  }
+  float s = 0.f;
+  if (!nan && !__builtin_isinf(mx)) {
+    for (int k = 0; k < segs; ++k) {
+      float mt[2];
+      load(k, mt);
+      if (mt[0] != neg_inf) s += mt[1] * fast_exp(mt[0] - mx);
+    }
+  }
+  return RowPairs{mx, s, nan};
+}
+
 #ifdef VBH_DEBUG_BOUNDS
 // Host side of the records: every translation unit that includes this header
 // registers a reader of its own record (and setter of its slack) with the

@@ -170,12 +170,12 @@ hipError_t launch_softmax(const void* x, void* y, int64_t rows, int cols, int id
 hipError_t launch_softmax_dim(const void* x, void* y, int64_t outer, int n,
                               int64_t inner, int idt, int odt, int log_mode,
                               hipStream_t s);
-// Second stage of a split softmax / log_softmax over rows of whole 16-byte
-// vectors: y from x and each row's `segs` (<= 64) segment logsumexps, one
-// kApplyLanes-lane workgroup per tile of kApplyLanes vectors; g.nt / g.wt
-// select the store policy.
+// Second stage of a split softmax / log_softmax: y from x and each row's
+// `segs` (<= 64) segment SegPairs (seg_pairs[2 * (row * segs + k)], written by
+// launch_logsumexp_pairs), one kApplyLanes-lane workgroup per tile of
+// kApplyLanes vectors; g.nt / g.wt select the store policy.
 constexpr int kApplyLanes = 256;
-hipError_t launch_softmax_apply(const void* x, void* y, const float* seg_lse, int64_t rows,
+hipError_t launch_softmax_apply(const void* x, void* y, const float* seg_pairs, int64_t rows,
                                 int cols, int segs, int idt, int odt, int log_mode,
                                 const Geometry& g, hipStream_t s);
 // segs > 1 (MIS geometry only): each of rows / segs rows of `cols` columns is
@@ -183,6 +183,16 @@ hipError_t launch_softmax_apply(const void* x, void* y, const float* seg_lse, in
 hipError_t launch_logsumexp(const void* x, void* y, int64_t rows, int cols, int idt,
                             int odt, const Geometry& g, hipStream_t s, int segs = 1,
                             int seg_cols = 0);
+// First stage of a split row: launch_logsumexp's units (same segs / seg_cols
+// rule), each writing its SegPair (max, sum of exp(x - max)) as two fp32 values
+// into pairs[2 * unit].
+hipError_t launch_logsumexp_pairs(const void* x, float* pairs, int64_t units, int cols, int idt,
+                                  const Geometry& g, hipStream_t s, int segs = 1,
+                                  int seg_cols = 0);
+// Second stage of a split logsumexp: y[row] (dtype odt) from the row's `segs`
+// SegPairs at pairs[2 * (row * segs + k)].
+hipError_t launch_logsumexp_combine(const float* pairs, void* y, int64_t rows, int segs,
+                                    int odt, hipStream_t s);
 
 struct CeArgs {
   const void* logits;
@@ -206,13 +216,15 @@ struct CeArgs {
   int has_smoothing;
   int split;
   int empty_neg_inf = 0;  // first stage of a split row (see ce_combine)
+  int pair_out = 0;       // first stage of a split row: SegPairs to z_loss (max), lse (sum)
 };
 hipError_t launch_cross_entropy_fwd(const CeArgs& a, const Geometry& g, hipStream_t s);
 // Second stage of a split row: `a` describes the caller's launch (one column
 // block per row); seg_loss / seg_lse hold the first stage's `segs` segments
 // per row at flat index k * n_rows + row.
 hipError_t launch_cross_entropy_combine(const CeArgs& a, const float* seg_loss,
-                                        const float* seg_lse, int segs, hipStream_t s);
+                                        const float* seg_sum, const float* seg_max, int segs,
+                                        hipStream_t s);
 
 struct CeBwdArgs {
   const float* dloss;

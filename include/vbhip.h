@@ -87,10 +87,10 @@ int vbh_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols,
 
 /* vbh_softmax_fwd with a caller-provided workspace (16-byte aligned).  Few
  * long rows split into segments (of whole 16-byte vectors, the last one
- * shorter where rows are not whole vectors): a first launch writes the
- * logsumexp of each row segment into the workspace (the two-stage shape of
- * ViperBench/logsumexp/triton_impl.py:48-71), a second reads x again and
- * writes y from each row's segments.  The workspace must hold
+ * shorter where rows are not whole vectors): a first launch writes each row
+ * segment's max and sum of exp(x - max) into the workspace (the two-stage
+ * shape of ViperBench/logsumexp/triton_impl.py:48-71), a second reads x again
+ * and writes y from each row's segments.  The workspace must hold
  * vbh_softmax_workspace_bytes(rows, cols, in_dtype) bytes; when that is 0, or
  * the workspace is null or smaller, this is vbh_softmax_fwd.  The workspace is
  * scratch of this call (stream-ordered, as for vbh_logsumexp_fwd_ws). */
@@ -122,10 +122,10 @@ int vbh_logsumexp_fwd(const void* x, void* y, int64_t rows, int64_t cols,
 
 /* vbh_logsumexp_fwd with a caller-provided device workspace (16-byte aligned).
  * When a launch has few rows (fewer than 256) of many 16-byte vectors, each
- * row is split into segments reduced in parallel into the workspace, then
- * combined by a logsumexp over each row's segment results -- the two-stage
- * shape of ViperBench/logsumexp/triton_impl.py:48-71 (block partials, then a
- * logsumexp over them), with the second stage on the GPU.  The workspace must
+ * row is split into segments reduced in parallel into the workspace (each
+ * segment's max and sum of exp(x - max)), then combined per row -- the
+ * two-stage shape of ViperBench/logsumexp/triton_impl.py:48-71 (block partials,
+ * then a logsumexp over them), with the second stage on the GPU.  The workspace must
  * hold vbh_logsumexp_workspace_bytes(rows, cols, in_dtype) bytes; when that is
  * 0, or the workspace is null or smaller, this is vbh_logsumexp_fwd.  The
  * workspace is scratch of this call (stream-ordered: reuse it after the call's
@@ -161,9 +161,10 @@ int vbh_cross_entropy_fwd(const void* logits, const void* labels, int logits_dty
  * launch has few long rows, each row is cut into segments reduced in parallel
  * as column blocks with SPLIT semantics -- the vocab-parallel form of the
  * golden (pytorch_impl.py:38-52: a row's loss is the logsumexp of its blocks'
- * lse plus the sum of their SPLIT losses) -- then one lane per row combines
- * them into the caller's outputs, with the golden's NaN rule for the whole
- * row.  Workspace size from vbh_cross_entropy_workspace_bytes; fallback and
+ * lse plus the sum of their SPLIT losses; each segment's lse is kept as its
+ * max and sum of exp(x - max), so the row's lse is rounded once) -- then one
+ * lane per row combines them into the caller's outputs, with the golden's NaN
+ * rule for the whole row.  Workspace size from vbh_cross_entropy_workspace_bytes; fallback and
  * reuse as for vbh_logsumexp_fwd_ws. */
 int vbh_cross_entropy_fwd_ws(const void* logits, const void* labels, int logits_dtype,
                              int label_dtype, void* loss, void* lse, void* z_loss,

@@ -238,19 +238,21 @@ def test_split_workspace_sizes():
     """The row split is a pure function of the launch shape: few rows of at
     least 256 KiB split (segments of >= 512 16-byte vectors, a power of two per
     row, about 1024 segments per launch), many rows or shorter rows do not, and
-    an overridden geometry turns it off."""
+    an overridden geometry turns it off.  A logsumexp or softmax segment keeps
+    its max and its sum of exp (two fp32 values), a cross-entropy segment its
+    loss, max and sum (three)."""
     h = _lib.lib()
     lse, red = h.vbh_logsumexp_workspace_bytes, h.vbh_reduce_workspace_bytes
     assert lse(8192, 4096, _lib.F32) == 0                 # many rows
-    assert lse(128, 131072, _lib.F32) == 128 * 8 * 4      # 8 segments of 4096 vectors
-    assert lse(1, 65536, _lib.F32) == 1 * 32 * 4          # capped by the segment size
-    assert lse(300, 131072, _lib.F32) == 300 * 4 * 4      # long rows: up to 511 rows
+    assert lse(128, 131072, _lib.F32) == 128 * 8 * 8      # 8 segments of 4096 vectors
+    assert lse(1, 65536, _lib.F32) == 1 * 32 * 8          # capped by the segment size
+    assert lse(300, 131072, _lib.F32) == 300 * 4 * 8      # long rows: up to 511 rows
     assert lse(384, 32768, _lib.F32) == 0                 # not long enough for that
     assert lse(64, 50304, _lib.F32) == 0                  # 200 KB rows: not worth a split
     assert lse(1, 65536, _lib.F16) == 0                   # 128 KB row
     assert lse(4, 1000, _lib.F32) == 0                    # too short to split
-    assert lse(4, 65537, _lib.F32) == 4 * 32 * 4          # not whole vectors: 31 x 2052 + 1925
-    assert lse(333, 50257, _lib.F32) == 333 * 4 * 4       # long rows, 4 segments of 12568
+    assert lse(4, 65537, _lib.F32) == 4 * 32 * 8          # not whole vectors: 31 x 2052 + 1925
+    assert lse(333, 50257, _lib.F32) == 333 * 4 * 8       # long rows, 4 segments of 12568
     assert lse(4, 65536, 9) == 0 and lse(0, 65536, _lib.F32) == 0
     assert red(128, 131072, 1, _lib.F32, _lib.REDUCE_MEAN) == 128 * 8 * 4
     assert red(128, 131072, 1, _lib.F32, _lib.REDUCE_MAX) == 128 * 8 * (8 + 4)
@@ -258,16 +260,16 @@ def test_split_workspace_sizes():
     assert red(300, 131072, 1, _lib.F32, _lib.REDUCE_MEAN) == 0  # long rows: logsumexp only
     assert red(128, 131072, 4, _lib.F32, _lib.REDUCE_MEAN) == 0  # middle axis: not split
     sm = h.vbh_softmax_workspace_bytes
-    assert sm(128, 131072, _lib.F32) == 128 * 8 * 4       # as logsumexp's few-rows split
+    assert sm(128, 131072, _lib.F32) == 128 * 8 * 8       # as logsumexp's few-rows split
     assert sm(8192, 4096, _lib.F32) == 0 and sm(300, 131072, _lib.F32) == 0
     assert sm(200, 65536, _lib.F32) == 0                  # 129 rows or more: not split
     assert sm(64, 65536, _lib.F32) == 0                   # fp32 33-64 rows: 32768 vectors
-    assert sm(64, 65536, _lib.BF16) == 64 * 16 * 4        # 16-bit 33-64 rows: 6144 vectors
-    assert sm(8, 32000, _lib.F32) == 8 * 8 * 4            # a decode step over a 32000 vocabulary
+    assert sm(64, 65536, _lib.BF16) == 64 * 16 * 8        # 16-bit 33-64 rows: 6144 vectors
+    assert sm(8, 32000, _lib.F32) == 8 * 8 * 8            # a decode step over a 32000 vocabulary
     assert sm(8, 16384, _lib.F32) == 0                    # 4096 vectors: not worth a split
-    assert sm(4, 65537, _lib.F32) == 4 * 32 * 4           # rows not whole vectors: 2052-column segments
-    assert sm(8, 50257, _lib.F32) == 8 * 16 * 4           # GPT-2's vocabulary, 16 x 3144 columns
-    assert sm(1, 131072, _lib.BF16) == 1 * 32 * 4
+    assert sm(4, 65537, _lib.F32) == 4 * 32 * 8           # rows not whole vectors: 2052-column segments
+    assert sm(8, 50257, _lib.F32) == 8 * 16 * 8           # GPT-2's vocabulary, 16 x 3144 columns
+    assert sm(1, 131072, _lib.BF16) == 1 * 32 * 8
     ce = h.vbh_cross_entropy_workspace_bytes
     assert ce(64, 128256, 1 << 17, _lib.F32) == 3 * 64 * 16 * 4  # one block per row
     assert ce(64, 128256, 32768, _lib.F32) == 0           # several column blocks: not split
@@ -282,8 +284,8 @@ def test_split_workspace_sizes():
     finally:
         _lib.tune_override(_lib.OP_LOGSUMEXP, 0, 0, 0)
         _lib.tune_override(_lib.OP_SOFTMAX, 0, 0, 0)
-    assert _lib.softmax_workspace_bytes(128, 131072, _lib.F32) == 128 * 8 * 4
-    assert _lib.logsumexp_workspace_bytes(128, 131072, _lib.F32) == 128 * 8 * 4
+    assert _lib.softmax_workspace_bytes(128, 131072, _lib.F32) == 128 * 8 * 8
+    assert _lib.logsumexp_workspace_bytes(128, 131072, _lib.F32) == 128 * 8 * 8
 
 
 def test_split_entry_points_check_arguments():
