@@ -17,7 +17,18 @@ device events on the launch stream and by a roctx range
 ``vbh-timed:<workload>:<K>`` that profiles select their dispatches by.
 ``value`` = algorithmic bytes x K / event time of the timed region.
 
+The headline line also carries ``per_config``: every measured config (C1-C5
+and the C4 backward), each timed the same way over its own rotation with
+enough launches for about 50 ms of device time (median of 3 such runs), next
+to a same-size yardstick (the stream copy, or the streaming read for the
+read-only kernels, moving the same bytes per launch through the same >= 2 GiB
+rotation) and to the same launches replayed from a HIP graph (no host work
+between kernels).  C1 adds the HIP runtime's own device-to-device copy
+(hipMemcpyAsync) of its size; C4 adds its full step, the row pass followed by
+the scalar mean of the 8192 row losses on the GPU (``full_step``).
+
   python bench.py [--steps K] [--warmup W] [--workload KEY] [--all] [--no-cpu]
+                  [--no-per-config]
 
 Prints ONE JSON line on stdout (``--all``: one per workload).  Progress goes
 to stderr.  Only one GPU is used: ``--gpus`` above 1 exits with a message.
@@ -112,6 +123,98 @@ def cpu_baseline(w, cpu_args, budget_s: float) -> dict:
 
 
 DEVICE_WARM_S = 0.5
+
+# the configs of BASELINE.json (and the C4 backward) in the per_config block
+PER_CONFIG = ("C1_layer_norm", "C2_rms_norm", "C3_softmax", "C3_log_softmax", "C3_logsumexp",
+              "C4_cross_entropy", "C4_cross_entropy_bwd", "C5_layer_norm")
+PER_CONFIG_DEVICE_S = 0.05   # device time of one timed run per config
+PER_CONFIG_REPEATS = 3
+
+
+def timed_rate(launch, nbytes, device_s=PER_CONFIG_DEVICE_S, repeats=PER_CONFIG_REPEATS):
+    """Median over `repeats` runs of back-to-back launches (about `device_s`
+    of device time each, event-timed, after a 0.3 s warm-up): GB/s and
+    microseconds per launch."""
+    harness.warm_gpu(launch, 0.3)
+    probe = harness.time_back_to_back(launch, 20, 2)["event_ms"] / 20
+    n = int(min(5000, max(100, device_s * 1e3 / max(probe, 1e-6))))
+    runs = sorted(harness.time_back_to_back(launch, n, 2)["event_ms"] / n for _ in range(repeats))
+    ms = runs[len(runs) // 2]
+    return {"value": round(nbytes / (ms * 1e-3) / 1e9, 2), "latency_us": round(ms * 1e3, 3),
+            "launches": n, "repeats": repeats,
+            "latency_us_runs": [round(r * 1e3, 3) for r in runs]}
+
+
+def yardstick(kind, nbytes):
+    """The stream copy (kind "copy": nbytes moved, half read, half written) or
+    the streaming read (kind "read") at one launch's byte count, cycling
+    through >= 2 GiB."""
+    if kind == "read":
+        launch, moved, _ = harness.read_rotation("cuda:0", nbytes)
+    else:
+        launch, moved, _ = harness.copy_rotation("cuda:0", nbytes)
+    r = timed_rate(launch, moved)
+    del launch
+    return {"kind": kind, "bytes": moved, "value": r["value"], "latency_us": r["latency_us"]}
+
+
+def per_config(peaks) -> dict:
+    """One entry per measured config: value, latency, fractions of the vendor
+    peak and of the measured peak of its kind, the same-size yardstick and the
+    graph-replayed latency; C1 and C4 carry their extra studies."""
+    out = {}
+    for key in PER_CONFIG:
+        w = WORKLOADS[key]
+        log(f"[bench] per_config {key}")
+        cpu_args = w.make()
+        rot = harness.make_rotation(w, cpu_args, "cuda:0")
+        n_rows = cpu_args[0].shape[0]
+        del cpu_args
+        r = timed_rate(rot.launch, w.bytes_per_launch)
+        g = harness.graph_replay_ms(rot.launch, rot.copies * max(1, 64 // rot.copies))
+        graph_us = g["ms_per_launch"] * 1e3
+        y = yardstick(w.peak_kind, w.bytes_per_launch)
+        e = {
+            "value": r["value"], "unit": "GB/s", "latency_us": r["latency_us"],
+            "frac": round(r["value"] / VENDOR_PEAK_GBPS, 4),
+            "frac_of_measured_peak": round(r["value"] * 1e9 / peaks[w.peak_kind], 4),
+            "peak_kind": w.peak_kind,
+            "algorithmic_bytes": w.bytes_per_launch,
+            "launches": r["launches"], "repeats": r["repeats"],
+            "latency_us_runs": r["latency_us_runs"],
+            "graph_replay": {"latency_us": round(graph_us, 3),
+                             "value": round(w.bytes_per_launch / (graph_us * 1e-6) / 1e9, 2),
+                             "launches_per_graph": g["launches_per_graph"],
+                             "replays": g["replays"]},
+            "same_size_yardstick": y,
+            "frac_of_same_size_yardstick": round(r["value"] / y["value"], 4),
+        }
+        if key == "C1_layer_norm":
+            launch, moved, _ = harness.runtime_copy_rotation("cuda:0", w.bytes_per_launch)
+            rc = timed_rate(launch, moved)
+            del launch
+            e["runtime_copy_same_size"] = {
+                "what": "hipMemcpyAsync device-to-device (torch copy_) of "
+                        f"{moved // 2} B per launch, >= 2 GiB rotation",
+                "value": rc["value"], "latency_us": rc["latency_us"]}
+            e["frac_of_runtime_copy_same_size"] = round(r["value"] / rc["value"], 4)
+        if key == "C4_cross_entropy":
+            launch, scalars = harness.ce_mean_step(rot, n_rows)
+            full_bytes = w.bytes_per_launch + n_rows * 4 + 4
+            f = timed_rate(launch, full_bytes)
+            torch.cuda.synchronize()
+            e["full_step"] = {
+                "what": "cross_entropy_fwd row pass, then the mean of the 8192 row losses "
+                        "(vbh_reduce_fwd) on the same stream",
+                "value": f["value"], "latency_us": f["latency_us"],
+                "mean_latency_us": round(f["latency_us"] - r["latency_us"], 3),
+                "algorithmic_bytes": full_bytes,
+                "loss_mean": float(scalars[0].item())}
+            del launch, scalars
+        out[key] = e
+        del rot
+        torch.cuda.empty_cache()
+    return out
 
 
 def run_workload(key, steps, warmup, peaks, with_cpu, cpu_budget):
@@ -220,6 +323,8 @@ def main():
     ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS))
     ap.add_argument("--all", action="store_true", help="every measured workload, one line each")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-per-config", action="store_true",
+                    help="leave the per_config block out of the headline line")
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="seconds of timed CPU work for the CPU baseline")
     ap.add_argument("--copy-at", type=int, nargs="+", metavar="BYTES",
@@ -253,6 +358,9 @@ def main():
     keys = sorted(WORKLOADS) if args.all else [args.workload]
     for key in keys:
         line = run_workload(key, args.steps, args.warmup, peaks, not args.no_cpu, args.cpu_budget)
+        if key == HEADLINE and not args.all and not args.no_per_config:
+            line["per_config"] = per_config(peaks)
+            line["full_step"] = line["per_config"][HEADLINE]["full_step"]
         print(json.dumps(line), flush=True)
 
 

@@ -9,7 +9,8 @@
 // written once in the input dtype.
 //   LayerNorm statistics are the exact two-pass ones over the register-resident
 //   row: the row sum gives the mean, then the sum of squared deviations from it
-//   gives the biased variance (two all-reduces of plain sums).
+//   gives the biased variance (two all-reduces of plain sums); fp32 rows are
+//   first shifted by their first element (kShiftLN).
 //   Weight / bias slices are loaded together with the row when the registers
 //   allow, so a row costs one memory round trip.
 // Persistent pipelined path (vbh_tune_override / heuristic): the grid holds as
@@ -18,7 +19,7 @@
 //   its next row before reducing the current one.
 // Streaming path (rows wider than the register budget): one 1024-lane
 //   workgroup per row; a Welford/Chan statistics pass, then an output pass that
-//   reads the row again.
+//   reads the row again, both on the row shifted by its first element.
 //
 // Semantics: ViperBench/layer_norm/pytorch_impl.py:5-12 (F.layer_norm, biased
 // variance, y = (x - mean) * rstd * w + b) and ViperBench/rms_norm/pytorch_impl.py:8-10
@@ -173,6 +174,44 @@ __device__ __forceinline__ float mean_of(float sum, int cols) {
   return fmaf(fmaf(-q, n, sum), inv, q);
 }
 
+// fp32 LayerNorm rows are shifted by their first element x0 before their
+// statistics, in the row's registers, and normalized in that shifted form:
+// y = ((x - x0) - mean') * rstd * w + b with mean' = mean(x - x0).  The row
+// mean as an fp32 number carries a rounding of up to half an ulp of |mean|,
+// which x - mean divides by the row's deviation: at |mean| / std = 1000 that
+// is 1e-4 of every output, in torch's fp32 LayerNorm too.  Shifted, the mean
+// is that of x - x0, within a few deviations of 0, and x - x0 itself is exact
+// where it matters (Sterbenz: x within a factor 2 of x0), so the error stays
+// near 1e-6 at any |mean| / std.  One subtract per element; 16-bit rows keep
+// their raw values (their output rounding, 2^-8 or 2^-11, dwarfs the mean's).
+template <typename T>
+constexpr bool kShiftLN = sizeof(T) == 4;
+
+template <typename T, int V, int IT, bool FULL = false>
+__device__ __forceinline__ void shift_row(typename Raw<T, V>::type (&xr)[IT], float x0, int nvec,
+                                          int g, int tpr) {
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    if (FULL || i * tpr + g < nvec) {  // padding vectors stay 0
+      if constexpr (V == 1) {
+        xr[i] -= x0;
+      } else {
+#pragma unroll
+        for (int k = 0; k < V; ++k) xr[i][k] -= x0;
+      }
+    }
+  }
+}
+
+// The shift of a row starting at `xr`: its first element for fp32 rows, else 0.
+template <typename T>
+__device__ __forceinline__ float row_shift(const T* __restrict__ xr, const Span& s) {
+  if constexpr (!kShiftLN<T>) return 0.f;
+  float x0;
+  load_f32<T, 1>(xr, &x0, s);
+  return x0;
+}
+
 // Weight / bias slices ride along with the row when they take at most 32
 // VGPRs in raw storage; otherwise they are read after the reduction.
 template <typename TW, int V, int IT> constexpr bool kEarlyLN = 2 * raw_vgprs<TW>(V, IT) <= 32;
@@ -211,6 +250,7 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_rows(
   const Span sx = VBH_SPAN(x, rows * cols), sy = VBH_SPAN(y, rows * cols);
   const Span sw = VBH_SPAN(w, cols), sb = VBH_SPAN(b, cols);
 
+  const float x0 = row_shift<T>(x + row * cols, sx);
   RT xr[IT];
   load_raw_row<T, V, IT, SP != kStoreCached>(x + row * cols, nvec, g, tpr, xr, sx);
   constexpr bool kEarly = kEarlyLN<TW, V, IT>;
@@ -219,6 +259,7 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_rows(
     load_raw_row<TW, V, IT, false>(w, nvec, g, tpr, wr, sw);
     if (b != nullptr) load_raw_row<TW, V, IT, false>(b, nvec, g, tpr, br, sb);
   }
+  if constexpr (kShiftLN<T>) shift_row<T, V, IT>(xr, x0, nvec, g, tpr);
 
   const float mean =
       mean_of(group_allreduce<Sum>(lane_sum<T, V, IT>(xr), tpr, lds[0]), cols);
@@ -380,11 +421,17 @@ __global__ __launch_bounds__(kMaxBlock) void norm_rows_mis(
   load_raw_row<T, V, IT, SP != kStoreCached>(xb, nvec, g, tpr, xr, sx);
   const bool hv = g < mr.head, tv = g < mr.tail;
   const int tcol = mr.head + nvec * V + g;  // this lane's tail column
-  const float hx = hv && VBH_IN_SPAN(sx, x + start + g, sizeof(T)) ? static_cast<float>(x[start + g])
-                                                              : 0.f;
-  const float tx =
+  float hx = hv && VBH_IN_SPAN(sx, x + start + g, sizeof(T)) ? static_cast<float>(x[start + g])
+                                                        : 0.f;
+  float tx =
       tv && VBH_IN_SPAN(sx, x + start + tcol, sizeof(T)) ? static_cast<float>(x[start + tcol]) : 0.f;
   float mean = 0.f, scale;
+  if constexpr (!RMS && kShiftLN<T>) {  // shifted by the row's first element
+    const float x0 = row_shift<T>(x + start, sx);
+    shift_row<T, V, IT>(xr, x0, nvec, g, tpr);
+    if (hv) hx -= x0;
+    if (tv) tx -= x0;
+  }
   if constexpr (RMS) {
     const float ss = group_allreduce<Sum>(lane_sumsq<T, V, IT>(xr) + hx * hx + tx * tx, tpr,
                                           lds[0]);
@@ -485,7 +532,9 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_pipe(
   // Rows past the end: zero registers.  The guarded kernels get them from a
   // load helper whose guards are all false (which schedules better for fp32
   // rows than plain register zeroing); FULL never reaches the first branch.
+  float x0 = 0.f, x0n = 0.f;  // the rows' shifts (kShiftLN)
   if (base + grp < rows) {
+    x0 = row_shift<T>(x + (base + grp) * cols, sx);
     load_raw_row<T, V, IT, kNT, FULL>(x + (base + grp) * cols, nvec, g, tpr, cur, sx);
   } else {
     if constexpr (FULL) zero_row<T, V, IT>(cur);
@@ -496,11 +545,13 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_pipe(
     const int64_t row = base + grp;
     const int64_t next = row + stride;
     if (next < rows) {
+      x0n = row_shift<T>(x + next * cols, sx);
       load_raw_row<T, V, IT, kNT, FULL>(x + next * cols, nvec, g, tpr, nxt, sx);
     } else {
       if constexpr (FULL) zero_row<T, V, IT>(nxt);
       else load_raw_row<T, V, IT, kNT>(x, 0, g, tpr, nxt, sx);
     }
+    if constexpr (kShiftLN<T>) shift_row<T, V, IT, FULL>(cur, x0, nvec, g, tpr);
 
     const float mean =
         mean_of(group_allreduce<Sum>(lane_sum<T, V, IT>(cur), tpr, lds[par][0]), cols);
@@ -528,6 +579,7 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_pipe(
     }
 #pragma unroll
     for (int i = 0; i < IT; ++i) cur[i] = nxt[i];
+    x0 = x0n;
     par ^= 1;
   }
 }
@@ -615,10 +667,16 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_stream(
   const Span sx = VBH_SPAN(x, static_cast<int64_t>(gridDim.x) * cols);
   const Span sy = VBH_SPAN(y, static_cast<int64_t>(gridDim.x) * cols);
   const Span sw = VBH_SPAN(w, cols), sb = VBH_SPAN(b, cols);
+  // both passes work on x - x0 (x0 the row's first element; see kShiftLN),
+  // in fp32 whatever the storage type
+  float x0;
+  load_f32<T, 1>(xr, &x0, sx);
   Moments m{0.f, 0.f, 0.f};
   for (int j = threadIdx.x; j < nvec; j += tpr) {
     float v[V];
     load_f32<T, V>(xr + static_cast<int64_t>(j) * V, v, sx);
+#pragma unroll
+    for (int k = 0; k < V; ++k) v[k] -= x0;
     float s = 0.f;
 #pragma unroll
     for (int k = 0; k < V; ++k) s += v[k];
@@ -643,7 +701,7 @@ __global__ __launch_bounds__(kMaxBlock) void layer_norm_stream(
       for (int k = 0; k < V; ++k) bv[k] = 0.f;
     }
 #pragma unroll
-    for (int k = 0; k < V; ++k) o[k] = (v[k] - mean) * rstd * wv[k] + bv[k];
+    for (int k = 0; k < V; ++k) o[k] = ((v[k] - x0) - mean) * rstd * wv[k] + bv[k];
     store_from_f32<T, V>(yr + static_cast<int64_t>(j) * V, o, sy);
   }
 }

@@ -290,6 +290,80 @@ def read_rotation(device, nbytes: int, min_footprint: int = 2 << 30):
     return launch, size, copies
 
 
+def runtime_copy_rotation(device, traffic_bytes: int, min_footprint: int = 2 << 30):
+    """(launch, bytes moved per launch, copies): the HIP runtime's own
+    device-to-device copy (torch's ``copy_`` between contiguous buffers of one
+    GPU, a hipMemcpyAsync) of ``traffic_bytes / 2`` bytes per launch, cycling
+    through enough buffer pairs that no launch hits the Infinity Cache -- a
+    same-size yardstick that is not this library's own code."""
+    half = max(16, (traffic_bytes // 2) // 16 * 16)
+    copies = max(2, math.ceil(min_footprint / (2 * half)))
+    bufs = [(torch.empty(half, dtype=torch.uint8, device=device),
+             torch.empty(half, dtype=torch.uint8, device=device)) for _ in range(copies)]
+    for a, _ in bufs:
+        a.fill_(1)
+
+    def launch(k):
+        a, b = bufs[k % copies]
+        b.copy_(a)
+
+    launch.buffers = bufs
+    return launch, 2 * half, copies
+
+
+def graph_replay_ms(launch: Callable[..., None], launches: int, replays: int = 20) -> dict:
+    """Device time per launch when `launches` consecutive launches (launch(k,
+    stream) for k = 0 .. launches - 1) are captured into one HIP graph and the
+    graph is replayed `replays` times back to back: the launch sequence with no
+    host work between kernels.  Returns the per-launch ms (events around the
+    replays) and the launch count."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up outside the capture
+        for k in range(launches):
+            launch(k, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        st = torch.cuda.current_stream().cuda_stream
+        for k in range(launches):
+            launch(k, st)
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(replays):
+        graph.replay()
+    e.record()
+    e.synchronize()
+    ms = s.elapsed_time(e) / (replays * launches)
+    del graph
+    return {"ms_per_launch": ms, "launches_per_graph": launches, "replays": replays}
+
+
+def ce_mean_step(rot: "Rotation", n_rows: int):
+    """(launch, scalars): the cross-entropy forward of a rotation's copy k
+    followed by the scalar mean of its first n_rows losses on the GPU
+    (vbh_reduce_fwd, mean over the contiguous loss.view(-1)[:n_rows]) -- the
+    full step of a mean-reduced loss.  scalars[k % copies] holds copy k's mean."""
+    dev = rot.outputs[0][0].device
+    scalars = [torch.empty((), dtype=torch.float32, device=dev) for _ in range(rot.copies)]
+    losses = [o[0].data_ptr() for o in rot.outputs]
+    outs = [t.data_ptr() for t in scalars]
+    stream = _bridge.stream(dev)
+    call = _lib.call
+    copies = rot.copies
+
+    def launch(k, st=stream):
+        rot.launch(k, st)
+        call("vbh_reduce_fwd", losses[k % copies], outs[k % copies], None, 1, n_rows, 1,
+             _lib.F32, _lib.F32, _lib.REDUCE_MEAN, st)
+
+    return launch, scalars
+
+
 def copy_rate_at(device, traffic_bytes: int, reps: int = 200,
                  min_footprint: int = 2 << 30) -> float:
     """Copy rate (bytes/s, read + write) when one launch moves `traffic_bytes`
@@ -351,50 +425,50 @@ def make_rotation(w: Workload, cpu_args: tuple, device, min_footprint: int = 2 <
         wdt = _float_code(cpu_args[1])
         argv = [(p(i[0]), p(i[1]), p(i[2]), p(o)) for i, o in zip(ins, outs)]
 
-        def launch(k):
+        def launch(k, st=stream):
             a = argv[k % copies]
-            call("vbh_layer_norm_fwd", a[0], a[1], a[2], a[3], rows, cols, eps, dt, wdt, stream)
+            call("vbh_layer_norm_fwd", a[0], a[1], a[2], a[3], rows, cols, eps, dt, wdt, st)
     elif w.fn == "rms_norm":
         eps = float(cpu_args[3])
         wdt = _float_code(cpu_args[2])
         argv = [(p(i[0]), p(i[2]), p(o)) for i, o in zip(ins, outs)]
 
-        def launch(k):
+        def launch(k, st=stream):
             a = argv[k % copies]
-            call("vbh_rms_norm_fwd", a[0], a[1], a[2], rows, cols, eps, dt, wdt, stream)
+            call("vbh_rms_norm_fwd", a[0], a[1], a[2], rows, cols, eps, dt, wdt, st)
     elif w.fn in ("softmax", "log_softmax"):
         mode = 1 if w.fn == "log_softmax" else 0
         argv = [(p(i[0]), p(o)) for i, o in zip(ins, outs)]
 
-        def launch(k):
+        def launch(k, st=stream):
             a = argv[k % copies]
-            call("vbh_softmax_fwd", a[0], a[1], rows, cols, dt, dt, mode, stream)
+            call("vbh_softmax_fwd", a[0], a[1], rows, cols, dt, dt, mode, st)
     elif w.fn == "logsumexp":
         argv = [(p(i[0]), p(o)) for i, o in zip(ins, outs)]
 
-        def launch(k):
+        def launch(k, st=stream):
             a = argv[k % copies]
-            call("vbh_logsumexp_fwd", a[0], a[1], rows, cols, dt, dt, stream)
+            call("vbh_logsumexp_fwd", a[0], a[1], rows, cols, dt, dt, st)
     elif w.fn == "cross_entropy_fwd":
         (_, labels, sm, scale, lss, ign, total, start, bs, has_sm, split) = cpu_args
         ldt = _bridge.LABEL_CODES[labels.dtype]
         argv = [(p(i[0]), p(i[1]), p(o[0]), p(o[1]), p(o[2])) for i, o in zip(ins, outs)]
 
-        def launch(k):
+        def launch(k, st=stream):
             a = argv[k % copies]
             call("vbh_cross_entropy_fwd", a[0], a[1], dt, ldt, a[2], a[3], a[4], rows, cols, cols,
                  float(sm), float(scale), float(lss), int(ign), int(total), int(start), int(bs),
-                 int(has_sm), int(split), stream)
+                 int(has_sm), int(split), st)
     elif w.fn == "cross_entropy_bwd":
         (_, _, _, labels, sm, scale, lss, ign, total, start, _bs, has_sm) = cpu_args
         ldt = _bridge.LABEL_CODES[labels.dtype]
         argv = [(p(i[0]), p(i[1]), p(i[2]), p(i[3]), p(o)) for i, o in zip(ins, outs)]
 
-        def launch(k):
+        def launch(k, st=stream):
             a = argv[k % copies]
             call("vbh_cross_entropy_bwd", a[0], a[1], a[2], a[3], a[4], dt, ldt, rows, cols, cols,
                  cols, 1, float(sm), float(scale), float(lss), int(ign), int(total), int(start),
-                 int(has_sm), stream)
+                 int(has_sm), st)
     else:
         raise KeyError(w.fn)
     return Rotation(w, copies, launch, outs, ins)

@@ -17,6 +17,11 @@ E_lib = t_pytorch / t_hip x 100 (experiments/_harness.py:142-146) on device
 times.  Rows are written in the reference's profile.csv column order, extra
 columns appended.
 
+A case or an implementation that raises does not end the sweep: as in
+ViperBench/benchmark.py:388-428, it gets a row whose measured columns read
+``ERROR`` (the message is printed), and the next one runs; the CSV is written
+at the end either way.
+
     python -m dslperfgap_amd.viperbench.benchmark [--out profile.MI355X.csv]
 """
 from __future__ import annotations
@@ -73,6 +78,71 @@ def cases(include_configs=True):
     return out
 
 
+def measure(fn, dev_args, cpu_args, traffic, warmup, iters) -> dict:
+    """One implementation on one case: the reference protocol's latency and
+    peak memory, and the HBM-cycled device time."""
+    torch.cuda.empty_cache()
+    lat, mem = profile_fn_mem(fn, dev_args, warmup, iters)
+    return {"latency_ms": lat, "peak_memory_mb": mem,
+            "device_us": device_time_us(fn, cpu_args, traffic)}
+
+
+def impls_for(kernel: str, fn_name: str):
+    return [("pytorch", lambda: harness.library_fn(kernel)),
+            ("hip", lambda: _hip_fn(kernel, fn_name))]
+
+
+def _error_row(kernel, size, impl, desc, err) -> dict:
+    msg = f"{type(err).__name__}: {err}"[:80]
+    print(f"{kernel:<14} {size:<17} {impl:<8} {'ERROR':>11}  {msg}", flush=True)
+    return {"kernel": kernel, "size": size, "impl": impl, "input_desc": desc,
+            "latency_ms": "ERROR", "peak_memory_mb": "ERROR", "device_us": "ERROR",
+            "achieved_GBps": "ERROR", "e_lib_pct": ""}
+
+
+def run_cases(case_list, impls=impls_for, measure_fn=measure, to_dev=to_device) -> list[dict]:
+    """Profile every (case, implementation); a failure gives an ERROR row and
+    the sweep goes on."""
+    rows = []
+    for kernel, size, fn_name, desc, make, is_slow in case_list:
+        warmup, iters = (3, 5) if is_slow else (10, 100)
+        try:
+            cpu_args = make()
+            dev_args = to_dev(cpu_args, "cuda")
+            traffic = harness.essential_work(kernel, dev_args)
+        except Exception as e:  # inputs could not be built: every impl errs
+            rows += [_error_row(kernel, size, impl, desc, e) for impl, _ in
+                     impls(kernel, fn_name)]
+            continue
+        dev_us = {}
+        for impl, get_fn in impls(kernel, fn_name):
+            try:
+                m = measure_fn(get_fn(), dev_args, cpu_args, traffic, warmup, iters)
+            except Exception as e:
+                rows.append(_error_row(kernel, size, impl, desc, e))
+                continue
+            dev_us[impl] = m["device_us"]
+            gbps = traffic / (m["device_us"] * 1e-6) / 1e9
+            e_lib = (100.0 * dev_us["pytorch"] / m["device_us"]) if "pytorch" in dev_us else None
+            rows.append({"kernel": kernel, "size": size, "impl": impl, "input_desc": desc,
+                         "latency_ms": round(m["latency_ms"], 4),
+                         "peak_memory_mb": round(m["peak_memory_mb"], 2),
+                         "device_us": round(m["device_us"], 2), "achieved_GBps": round(gbps, 1),
+                         "e_lib_pct": round(e_lib, 1) if e_lib is not None else ""})
+            print(f"{kernel:<14} {size:<17} {impl:<8} {m['latency_ms']:>11.4f} "
+                  f"{m['peak_memory_mb']:>11.2f} {m['device_us']:>10.2f} {gbps:>8.1f} "
+                  f"{(e_lib if e_lib is not None else float('nan')):>8.1f}  {desc}", flush=True)
+        del dev_args
+    return rows
+
+
+def write_csv(path, rows) -> None:
+    with open(path, "w", newline="") as f:
+        writer = csv.DictWriter(f, fieldnames=FIELDS)
+        writer.writeheader()
+        writer.writerows(rows)
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--out", default="profile.MI355X.csv")
@@ -82,35 +152,12 @@ def main(argv=None):
     if not torch.cuda.is_available():
         print("no GPU visible", file=sys.stderr)
         return 1
-    rows = []
     print(f"{'Kernel':<14} {'Size':<17} {'Impl':<8} {'Latency(ms)':>11} {'PeakMem(MB)':>11} "
           f"{'device_us':>10} {'GB/s':>8} {'E_lib%':>8}  Input", flush=True)
-    for kernel, size, fn_name, desc, make, is_slow in cases(not args.no_configs):
-        if args.kernels and kernel not in args.kernels:
-            continue
-        warmup, iters = (3, 5) if is_slow else (10, 100)
-        cpu_args = make()
-        dev_args = to_device(cpu_args, "cuda")
-        traffic = harness.essential_work(kernel, dev_args)
-        impls = [("pytorch", harness.library_fn(kernel)), ("hip", _hip_fn(kernel, fn_name))]
-        dev_us = {}
-        for impl, fn in impls:
-            torch.cuda.empty_cache()
-            lat, mem = profile_fn_mem(fn, dev_args, warmup, iters)
-            dev_us[impl] = device_time_us(fn, cpu_args, traffic)
-            gbps = traffic / (dev_us[impl] * 1e-6) / 1e9
-            e_lib = 100.0 * dev_us["pytorch"] / dev_us[impl]
-            rows.append({"kernel": kernel, "size": size, "impl": impl, "input_desc": desc,
-                         "latency_ms": round(lat, 4), "peak_memory_mb": round(mem, 2),
-                         "device_us": round(dev_us[impl], 2), "achieved_GBps": round(gbps, 1),
-                         "e_lib_pct": round(e_lib, 1)})
-            print(f"{kernel:<14} {size:<17} {impl:<8} {lat:>11.4f} {mem:>11.2f} "
-                  f"{dev_us[impl]:>10.2f} {gbps:>8.1f} {e_lib:>8.1f}  {desc}", flush=True)
-        del dev_args
-    with open(args.out, "w", newline="") as f:
-        writer = csv.DictWriter(f, fieldnames=FIELDS)
-        writer.writeheader()
-        writer.writerows(rows)
+    chosen = [c for c in cases(not args.no_configs)
+              if not args.kernels or c[0] in args.kernels]
+    rows = run_cases(chosen)
+    write_csv(args.out, rows)
     print(f"\nResults written to {args.out}", flush=True)
     return 0
 

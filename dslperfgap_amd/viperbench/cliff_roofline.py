@@ -28,6 +28,10 @@ streaming read for logsumexp, cross entropy and mean / max / argmax, which
 write almost nothing), and the achieved rate as a fraction of it
 (``frac_of_measured_peak_hbm``).
 
+An entry that raises does not end the sweep: as exp_cliff_roofline.py:450-461
+does, it gets a row with the measured columns empty and the note
+``ENTRY_ERROR: <type>: <message>``, and the next entry runs.
+
     python -m dslperfgap_amd.viperbench.cliff_roofline [--kernels a,b] [--out PATH]
 """
 from __future__ import annotations
@@ -149,6 +153,51 @@ def make_row(kernel: str, t_lib: float | None, t_opt: float, t_hbm: float | None
     }
 
 
+def error_row(kernel: str, err: Exception) -> dict:
+    """The row of an entry that raised (exp_cliff_roofline.py:452-461)."""
+    _fn, dtype, shape, _make, _lines = ENTRIES[kernel]
+    row = {f: "" for f in FIELDS}
+    row.update(kernel=kernel, dsl="hip", dtype=dtype, shape=shape,
+               note=f"ENTRY_ERROR: {type(err).__name__}: {str(err)[:120]}")
+    return row
+
+
+def measure_entry(kernel: str, warmup: int, reps: int, peak: float, peak_note: str,
+                  peaks: dict) -> dict:
+    """One entry's row: torch's and the hip impl's times, then the HBM-cycled one."""
+    fn_name, _dtype, _shape, make, _lines = ENTRIES[kernel]
+    cpu_args = make()
+    dev = to_device(cpu_args, "cuda")
+    hip = getattr(importlib.import_module(f"dslperfgap_amd.viperbench.{kernel}.hip_impl"),
+                  fn_name)
+    t_lib = time_ref_protocol(harness.library_fn(kernel), dev, warmup, reps)
+    t_opt = time_ref_protocol(hip, dev, warmup, reps)
+    work = harness.essential_work(kernel, dev)
+    del dev
+    torch.cuda.empty_cache()
+    t_hbm = device_time_us(hip, cpu_args, work) * 1e-3
+    return make_row(kernel, t_lib, t_opt, t_hbm, work, peak, peak_note, peaks)
+
+
+def run_entries(kernels, measure, log=print) -> list[dict]:
+    """measure(kernel) for each kernel; one that raises gets an ENTRY_ERROR row."""
+    rows = []
+    for kernel in kernels:
+        try:
+            row = measure(kernel)
+        except Exception as e:
+            log(f"  [error] {kernel} (hip): {type(e).__name__}: {str(e)[:120]}")
+            rows.append(error_row(kernel, e))
+        else:
+            rows.append(row)
+            log(f"{kernel:<15}{row['dtype']:<6}{row['t_lib_ms']:>10}{row['t_opt_ms']:>10}"
+                f"{row['E_lib_opt']:>10}{row['roofline_frac_opt']:>10}{row['t_opt_hbm_ms']:>10}"
+                f"{row['roofline_frac_opt_hbm']:>10}{row['frac_of_measured_peak_hbm']:>9}")
+        if torch.cuda.is_available():
+            torch.cuda.empty_cache()
+    return rows
+
+
 def write_rows(path: Path, rows: list[dict], meta: dict) -> None:
     path.parent.mkdir(parents=True, exist_ok=True)
     with open(path, "w", newline="") as f:
@@ -177,27 +226,11 @@ def main(argv=None) -> int:
     peaks = {"copy": harness.copy_peak("cuda:0"), "read": harness.read_peak("cuda:0")}
     print(f"measured stream-copy rate: {peaks['copy'] / 1e9:.1f} GB/s, streaming read: "
           f"{peaks['read'] / 1e9:.1f} GB/s", flush=True)
-    rows = []
     print(f"{'kernel':<15}{'dtype':<6}{'t_lib':>10}{'t_opt':>10}{'E_lib_opt':>10}"
           f"{'roof_opt':>10}{'t_hbm':>10}{'roof_hbm':>10}{'of_meas':>9}", flush=True)
-    for kernel in kernels:
-        fn_name, dtype, _shape, make, _lines = ENTRIES[kernel]
-        cpu_args = make()
-        dev = to_device(cpu_args, "cuda")
-        hip = getattr(importlib.import_module(f"dslperfgap_amd.viperbench.{kernel}.hip_impl"),
-                      fn_name)
-        t_lib = time_ref_protocol(harness.library_fn(kernel), dev, args.warmup, args.reps)
-        t_opt = time_ref_protocol(hip, dev, args.warmup, args.reps)
-        work = harness.essential_work(kernel, dev)
-        del dev
-        torch.cuda.empty_cache()
-        t_hbm = device_time_us(hip, cpu_args, work) * 1e-3
-        row = make_row(kernel, t_lib, t_opt, t_hbm, work, peak, peak_note, peaks)
-        rows.append(row)
-        print(f"{kernel:<15}{dtype:<6}{t_lib:>10.4f}{t_opt:>10.4f}{row['E_lib_opt']:>10}"
-              f"{row['roofline_frac_opt']:>10}{t_hbm:>10.4f}{row['roofline_frac_opt_hbm']:>10}"
-              f"{row['frac_of_measured_peak_hbm']:>9}",
-              flush=True)
+    rows = run_entries(kernels, lambda k: measure_entry(k, args.warmup, args.reps, peak,
+                                                        peak_note, peaks),
+                       log=lambda m: print(m, flush=True))
     out = Path(args.out) if args.out else RESULTS / device_slug(meta["gpu_name"], meta["sm"]) / \
         "cliff_roofline.csv"
     write_rows(out, rows, meta)

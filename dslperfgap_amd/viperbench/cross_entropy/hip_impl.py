@@ -108,3 +108,25 @@ def cross_entropy_bwd(
                    float(logit_scale), float(lse_square_scale), int(ignored_index),
                    int(total_classes), int(class_start_idx), int(bool(HAS_SMOOTHING)))
     return dlogits
+
+
+def loss_mean(loss, n_rows):
+    """The scalar loss of a mean-reduced cross entropy: the mean of the first
+    ``n_rows`` flat positions of the forward's ``loss`` -- with one column
+    block per row, the per-row losses (``loss.view(-1)[:n_rows].mean()``, the
+    scalar of BASELINE.json's C4 config).  Computed on the GPU by the library's
+    mean reduction (vbh_reduce_fwd: fp32 row sum, then / n_rows); returns a 0-d
+    fp32 tensor on loss's device."""
+    what = "cross_entropy loss_mean"
+    dev = _bridge.require_gpu(what, loss)
+    n_rows = int(n_rows)
+    flat = loss.reshape(-1)
+    if loss.dtype != torch.float32:
+        raise TypeError(f"{what}: loss must be fp32, got {loss.dtype}")
+    if not 0 < n_rows <= flat.numel():
+        raise ValueError(f"{what}: n_rows {n_rows} outside 1..{flat.numel()}")
+    flat = flat[:n_rows].contiguous()
+    out = _bridge.empty(flat, ())
+    _bridge.launch("vbh_reduce_fwd", dev, flat.data_ptr(), out.data_ptr(), None, 1, n_rows, 1,
+                   _lib.F32, _lib.F32, _lib.REDUCE_MEAN)
+    return out

@@ -112,7 +112,8 @@ WORKLOADS = {
                  make_c3, 16384 * 4096 * 4 + 16384 * 4, "f32", "read"),
         Workload("C4_cross_entropy", "cross_entropy", "cross_entropy_fwd",
                  "cross_entropy fwd fp32 logits[8192,32000]~N(0,2), int64 targets, "
-                 "BLOCK_SIZE=32768 (one block per row), mean of the 8192 row losses",
+                 "BLOCK_SIZE=32768 (one block per row): the row pass (per-row loss, lse, "
+                 "z_loss); the scalar mean of the 8192 losses is timed as full_step",
                  make_c4, 8192 * 32000 * 4 + 8192 * 8 + 3 * 8192 * 4, "f32", "read"),
         Workload("C4_cross_entropy_bwd", "cross_entropy", "cross_entropy_bwd",
                  "cross_entropy bwd fp32 logits[8192,32000] (C4's inputs), lse of the forward, "

@@ -21,7 +21,8 @@ import torch
 
 from dslperfgap_amd import _lib
 from dslperfgap_amd.viperbench.argmax.hip_impl import argmax
-from dslperfgap_amd.viperbench.cross_entropy.hip_impl import cross_entropy_bwd, cross_entropy_fwd
+from dslperfgap_amd.viperbench.cross_entropy.hip_impl import (cross_entropy_bwd,
+                                                              cross_entropy_fwd, loss_mean)
 from dslperfgap_amd.viperbench.layer_norm.hip_impl import layer_norm
 from dslperfgap_amd.viperbench.log_softmax.hip_impl import log_softmax
 from dslperfgap_amd.viperbench.logsumexp.hip_impl import logsumexp
@@ -175,12 +176,19 @@ def test_measured_configs_full_size(key):
     if w.fn == "cross_entropy_fwd":
         n_rows, n_cols = args[0].shape
         check_ce(got, want, n_rows, n_cols, args[8], args[10], STRICT, key)
-        # scalar: mean of the per-row losses, within 1e-4 relative
-        hip_mean = got[0].reshape(-1)[:n_rows].double().mean().item()
+        # scalar: the HIP mean of the per-row losses (loss_mean, on the GPU),
+        # within 1e-4 relative of the oracle's and of torch's own mean-reduced
+        # cross entropy in fp64
+        scalar = loss_mean(got[0], n_rows)
+        assert scalar.device.type == "cuda" and scalar.dim() == 0
+        hip_mean = scalar.item()
         ref_mean = want[0].reshape(-1)[:n_rows].double().mean().item()
         assert abs(hip_mean - ref_mean) <= 1e-4 * abs(ref_mean), (hip_mean, ref_mean)
         lib = torch.nn.functional.cross_entropy(args[0].double(), args[1]).item()
         assert abs(hip_mean - lib) <= 1e-4 * abs(lib), (hip_mean, lib)
+        # and of the mean of its own row losses in fp64 (the reduction alone)
+        own = got[0].reshape(-1)[:n_rows].double().mean().item()
+        assert abs(hip_mean - own) <= 1e-6 * abs(own), (hip_mean, own)
     elif w.fn == "cross_entropy_bwd":
         # dloss = 1/n_rows scales every entry; compare at the fp32 bar after
         # undoing it (an absolute 1e-5 would pass anything at this scale)

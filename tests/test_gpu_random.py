@@ -5,7 +5,10 @@ Each case draws from its own generator (seed 5000 + family offset + index),
 so a failing case is reproduced by its test id alone.  Tolerances are the
 reference's loose per-dtype set (ViperBench/test_utils.py:12-25, loose_tol):
 fp32 2e-5, fp16 2e-3, bf16 2e-2 for atol and rtol; max values and all indices
-must match exactly (ViperBench/argmax/test.py:38-42).
+must match exactly (ViperBench/argmax/test.py:38-42).  LayerNorm is held to an
+fp64 LayerNorm of the same inputs instead, at those tolerances widened per row
+by twice the golden's own error there (_close_ln), since the golden itself
+errs by about 1e-4 on ill-conditioned fp32 rows.
 """
 import os
 import random
@@ -61,36 +64,45 @@ def _shape(r: random.Random, min_ndim=1, max_ndim=3, last=None):
     return tuple(dims + [last])
 
 
-def _close(got, want, dtype, what, extra_atol=0.0):
+def _close(got, want, dtype, what):
     assert got.device.type == "cuda", what
     assert got.shape == want.shape and got.dtype == want.dtype, (what, got.shape, want.shape,
                                                                  got.dtype, want.dtype)
     tol = TOL[dtype]
     g, w = got.float().cpu(), want.float()
-    if not torch.allclose(g, w, atol=tol + extra_atol, rtol=tol, equal_nan=True):
+    if not torch.allclose(g, w, atol=tol, rtol=tol, equal_nan=True):
         err = (g - w).abs().nan_to_num(0.0).max().item()
-        raise AssertionError(f"{what}: max_err={err:.3e} tol={tol} + {extra_atol:.2e}")
+        raise AssertionError(f"{what}: max_err={err:.3e} tol={tol}")
 
 
-def _ln_rounding_allowance(x, norm, w) -> float:
-    """The part of any fp32 LayerNorm's error that the input's conditioning
-    sets: the row mean carries a few roundings of |mean| (2^-24 each) whatever
-    the algorithm, and x - mean divides it by the row's standard deviation, so
-    a row of mean -50 and deviation 0.05 gets errors of about 1e-4 in every
-    fp32 implementation (torch's CPU LayerNorm included, measured against fp64:
-    up to 2.1e-4 at |mean| / std = 1000).  Allowance: 16 such roundings (the
-    streaming kernel's chunked Welford merges for rows beyond the register
-    budget reached 6), times |mean| / std of the worst row and the largest
-    |weight|; rows with std 0 (x - mean exactly 0) contribute none.  For
-    N(0, 1) rows it is below 1e-6; a wrong mean (one element off) still errs
-    by orders of magnitude more."""
+def _close_ln(got, x, norm, w, b, what):
+    """LayerNorm against fp64: every element within the loose tolerance of an
+    fp64 LayerNorm of the same inputs, widened per row by twice the error that
+    the reference golden itself (torch's LayerNorm in x's dtype, the oracle)
+    makes on that row against the same fp64 result.  So the HIP result may
+    never be worse than twice the golden's own error plus the reference's
+    tolerance; on ill-conditioned rows (|mean| / std up to 1000), where any
+    fp32 LayerNorm that subtracts a rounded mean errs by about 1e-4, the
+    golden's error is what sets the bar, measured rather than assumed."""
+    dtype = x.dtype
+    assert got.device.type == "cuda", what
+    assert got.shape == x.shape and got.dtype == dtype, (what, got.shape, got.dtype)
     n = 1
     for d in norm:
         n *= d
-    rows = x.double().reshape(-1, n)
-    std = rows.std(1, unbiased=False)
-    cond = torch.where(std > 0, rows.mean(1).abs() / std.clamp_min(1e-300), torch.zeros_like(std))
-    return 16 * 2.0 ** -24 * cond.max().item() * w.double().abs().max().item()
+    truth = torch.nn.functional.layer_norm(x.double(), tuple(norm), w.double(),
+                                           None if b is None else b.double(), 1e-5)
+    golden = ref.layer_norm(x, w, b).double()
+    g = got.double().cpu().reshape(-1, n)
+    t = truth.reshape(-1, n)
+    golden_err = (golden.reshape(-1, n) - t).abs().amax(1, keepdim=True)
+    tol = TOL[dtype]
+    bound = tol + tol * t.abs() + 2 * golden_err
+    err = (g - t).abs()
+    if not bool((err <= bound).all()):
+        r = int((err - bound).amax(1).argmax())
+        raise AssertionError(f"{what}: row {r} err {err[r].max().item():.3e} against fp64, "
+                             f"golden's own {golden_err[r].item():.3e}, tol {tol}")
 
 
 def _same(got, want, what):
@@ -119,8 +131,7 @@ def test_random_norms(i):
     print(f"[gpu] norms {tag}", flush=True)
     xd, wd = x.to(DEV), w.to(DEV)
     bd = b.to(DEV) if b is not None else None
-    _close(layer_norm(xd, wd, bd), ref.layer_norm(x, w, b), dtype, "layer_norm " + tag,
-           _ln_rounding_allowance(x, norm, w))
+    _close_ln(layer_norm(xd, wd, bd), x, norm, w, b, "layer_norm " + tag)
     eps = r.choice([1e-5, 1e-6])
     _close(rms_norm(xd, norm, wd, eps), ref.rms_norm(x, norm, w, eps), dtype, "rms_norm " + tag)
 
