@@ -99,7 +99,7 @@ constexpr int64_t kShortRowVecs = 32;
 constexpr int kItShort[kNumOps] = {2, 2, 2, 2, 4, 4};
 constexpr int kMinLanesShort[kNumOps] = {4, 8, 8, 8, 2, 4};
 
-int it_target(int op, int64_t nvec, int vec) {
+int it_target(int op, int64_t nvec, int vec, bool column_blocks) {
   if (vec > 1 && nvec <= kShortRowVecs) {
     int it = kItShort[op];
     while (it > 1 && nvec / it < kMinLanesShort[op]) it /= 2;
@@ -124,7 +124,13 @@ int it_target(int op, int64_t nvec, int vec) {
       (nvec & (nvec - 1)) == 0)
     return 2;
   if (vec > 1) {
-    if (op == VBH_OP_CROSS_ENTROPY) return 8;
+    // cross entropy: 8 where a segment is a whole row (the sweep above); 4
+    // where rows are cut into column blocks (BLOCK_SIZE < n_cols).  MI355X, 8
+    // -> 4 at 512 MB per launch: fp32 4096 x 32768 at BLOCK_SIZE 512 / 1024 /
+    // 2048 / 4096 +10.5 / +11.0 / +6.7 / +4.2%, fp32 16384 x 4096 at 1024
+    // +13.0%, bf16 4096 x 32768 at 1024 / 2048 +7.7 / +3.7%; whole rows of
+    // 512-2048 columns lose 2-7% at 4.
+    if (op == VBH_OP_CROSS_ENTROPY) return column_blocks ? 4 : 8;
     if (op == VBH_OP_LOGSUMEXP && nvec > kMidRowVecs) return 8;
     if (op == VBH_OP_REDUCE && nvec > (vec == 8 ? int64_t(1024) : kMidRowVecs)) return 8;
   }
@@ -263,8 +269,22 @@ RowSplit split_row(int64_t rows, int64_t cols, int vn, int64_t long_from) {
 // MI355X, 50257 columns: fp32 log_softmax 2407 GB/s scalar, 4811 at 50256.
 constexpr int64_t kMisMinVecs = 4;  // shorter rows keep the scalar kernel
 
-// `units`: row groups of the launch (see fill_it); `out_bytes`: bytes it writes.
-Geometry geometry_for(int op, int64_t cols, int vec, int64_t units, int64_t out_bytes = 0) {
+// logsumexp rows of 512 lanes at 8 vectors per lane (4096-vector rows: fp32
+// 16384, 16-bit 32768 columns) run two to a 1024-lane workgroup.  MI355X, one
+// -> two per workgroup: fp32 4096 / 8192 / 16384 x 16384 +7.0 / +6.1 / +5.4%,
+// fp16 2048 / 4096 / 8192 x 32768 +4.7 / +8.7 / +8.2%.  Not bf16: its kernel
+// keeps the row widened to fp32 as well (105 VGPRs against 58 for fp16), so
+// two 16-wave workgroups do not fit a CU (bf16 8192 x 32768 -26%).
+bool lse_two_rows_per_block(const Geometry& g, int dtype) {
+  return !g.stream && g.tpr == 8 * kWave && g.maxit == 8 && dtype >= 0 && dtype != kBF16;
+}
+
+// `units`: row groups of the launch (see fill_it); `out_bytes`: bytes it
+// writes; `column_blocks`: the units are column blocks of longer rows (cross
+// entropy with BLOCK_SIZE < n_cols); `dtype`: the input type where a rule
+// depends on it (-1: not given).
+Geometry geometry_for(int op, int64_t cols, int vec, int64_t units, int64_t out_bytes = 0,
+                      bool column_blocks = false, int dtype = -1) {
   const int over = g_flags[op].load();
   int flags = kFlagNontemporal;
   if (over & kFlagNontemporal) flags |= kFlagNontemporal;
@@ -272,8 +292,9 @@ Geometry geometry_for(int op, int64_t cols, int vec, int64_t units, int64_t out_
   const bool norm = op == VBH_OP_LAYER_NORM || op == VBH_OP_RMS_NORM;
   if (norm && !(over & kFlagNoPersist)) flags |= kFlagPersist;
   const int64_t nvec = cols / vec;
-  Geometry g = pick_geometry(cols, vec, fill_it(it_target(op, nvec, vec), nvec, units),
-                             g_tpr[op].load(), g_block[op].load(), flags);
+  Geometry g =
+      pick_geometry(cols, vec, fill_it(it_target(op, nvec, vec, column_blocks), nvec, units),
+                    g_tpr[op].load(), g_block[op].load(), flags);
   if (g.persist && !(over & kFlagPersist) && g.tpr < kPersistMinTpr[op]) g.persist = false;
   // LayerNorm row groups of exactly 2 waves run 4 to a 512-lane workgroup
   // instead of one per 128-lane workgroup.  MI355X, persistent kernel, default
@@ -281,6 +302,8 @@ Geometry geometry_for(int op, int64_t cols, int vec, int64_t units, int64_t out_
   // 4096 5207 -> 5303, fp32 1536 4161 -> 4414 at 33.6 MB (5416 -> 5386 at 134 MB).
   if (op == VBH_OP_LAYER_NORM && !g.stream && g.tpr == 2 * kWave && g_block[op].load() <= 0)
     g.block = 8 * kWave;
+  if (op == VBH_OP_LOGSUMEXP && lse_two_rows_per_block(g, dtype) && g_block[op].load() <= 0)
+    g.block = 16 * kWave;
   const bool full_output =
       op == VBH_OP_LAYER_NORM || op == VBH_OP_RMS_NORM || op == VBH_OP_SOFTMAX;
   bool wt = full_output && write_through_ok(out_bytes, units);
@@ -342,7 +365,7 @@ Geometry reduce_geometry(int64_t n, int vec, int64_t units) {
   const int64_t nvec = n / vec;
   int tpr = g_tpr[VBH_OP_REDUCE].load();
   if (tpr <= 0) {
-    const int per_lane = fill_it(it_target(VBH_OP_REDUCE, nvec, vec), nvec, units);
+    const int per_lane = fill_it(it_target(VBH_OP_REDUCE, nvec, vec, false), nvec, units);
     const int64_t lanes = (nvec + per_lane - 1) / per_lane;
     if (lanes <= kWave) {
       tpr = pow2ceil(lanes < 1 ? 1 : lanes);
@@ -435,6 +458,30 @@ int64_t resident_blocks(const void* kernel, int block, int max_per_cu) {
     per_cu.emplace(key, nb);
   }
   return static_cast<int64_t>(std::min(nb, max_per_cu)) * cus[dev];
+}
+
+// Input bytes a CU's resident persistent workgroups may hold in flight (each
+// row group loads its next row while it reduces the current one), but never
+// fewer than 2 workgroups per CU (bf16 LayerNorm 16384 columns, 64 KiB per
+// workgroup: 1 lost 4.6% at 2048 rows; fp32 LayerNorm 4608 columns, 36 KiB:
+// 3 lost the 13% that 2 gain).  Uncapped,
+// small fp32 kernels put 3 workgroups on a CU; capped (MI355X, 64 MB per
+// call): fp32 RMSNorm 5120 columns +17.6%, LayerNorm 4608 / 5120 +13%, bf16
+// RMSNorm 10240 +10%, bf16 LayerNorm 8192 columns +0.8%, C1 / C5 and the other
+// shapes within 0.4%.  A 64 KiB cap starved fp32 LayerNorm (-12%).
+constexpr int64_t kPipeBytesPerCu = int64_t(96) << 10;
+// Workgroups of fewer lanes keep their full occupancy: at 2 waves each, the
+// cap left 12 waves per CU (bf16 LayerNorm 4096 columns -2.7%).
+constexpr int kPipeCapMinBlock = 256;
+
+int64_t pipe_grid(const void* kernel, const Geometry& g, int64_t rows, int64_t row_bytes) {
+  const int64_t per_block = 2 * (g.block / g.tpr) * row_bytes;  // current + next rows
+  const int64_t pb = std::max<int64_t>(per_block, 1);
+  const int max_per_cu = g.block < kPipeCapMinBlock
+                             ? 1 << 30
+                             : static_cast<int>(std::max<int64_t>(2, kPipeBytesPerCu / pb));
+  const int64_t cap = resident_blocks(kernel, g.block, max_per_cu);
+  return std::min<int64_t>(grid_for(rows, g), std::max<int64_t>(cap, 1));
 }
 
 Geometry pick_geometry(int64_t cols, int vec, int it_target, int tpr_override,
@@ -804,7 +851,8 @@ int vbh_logsumexp_fwd_ws(const void* x, void* y, int64_t rows, int64_t cols, int
     }
   }
   const bool mis_ok = !vec_ok && aligned16(x) && cols >= kMisMinVecs * vn;
-  Geometry g = geometry_for(VBH_OP_LOGSUMEXP, cols, vec_ok || mis_ok ? vn : 1, rows);
+  Geometry g =
+      geometry_for(VBH_OP_LOGSUMEXP, cols, vec_ok || mis_ok ? vn : 1, rows, 0, false, in_dtype);
   if (mis_ok && !use_mis(g, vn)) g = geometry_for(VBH_OP_LOGSUMEXP, cols, 1, rows);
   if (int rc = check_grid(rows, g)) return rc;
   return hip_status(launch_logsumexp(x, y, rows, static_cast<int>(cols), in_dtype, out_dtype,
@@ -905,8 +953,10 @@ int vbh_cross_entropy_fwd_ws(const void* logits, const void* labels, int logits_
   }
   const int64_t segments = mul_sat(n_rows, ncb);
   const bool mis_ok = !vec_ok && aligned16(logits) && bs >= kMisMinVecs * vn;
-  Geometry g = geometry_for(VBH_OP_CROSS_ENTROPY, bs, vec_ok || mis_ok ? vn : 1, segments);
-  if (mis_ok && !use_mis(g, vn)) g = geometry_for(VBH_OP_CROSS_ENTROPY, bs, 1, segments);
+  Geometry g = geometry_for(VBH_OP_CROSS_ENTROPY, bs, vec_ok || mis_ok ? vn : 1, segments, 0,
+                            ncb > 1);
+  if (mis_ok && !use_mis(g, vn))
+    g = geometry_for(VBH_OP_CROSS_ENTROPY, bs, 1, segments, 0, ncb > 1);
   if (int rc = check_grid(segments, g)) return rc;
   return hip_status(launch_cross_entropy_fwd(a, g, s), "cross_entropy_fwd launch");
 }

@@ -776,37 +776,14 @@ bool pipe_full(const Geometry& g, int64_t nvec, int it) {
          nvec == static_cast<int64_t>(it) * g.tpr;
 }
 
-// Input bytes a CU's resident persistent workgroups may hold in flight (each
-// row group loads its next row while it reduces the current one), but never
-// fewer than 2 workgroups per CU (bf16 LayerNorm 16384 columns, 64 KiB per
-// workgroup: 1 lost 4.6% at 2048 rows; fp32 LayerNorm 4608 columns, 36 KiB:
-// 3 lost the 13% that 2 gain).  Uncapped,
-// small fp32 kernels put 3 workgroups on a CU; capped (MI355X, 64 MB per
-// call): fp32 RMSNorm 5120 columns +17.6%, LayerNorm 4608 / 5120 +13%, bf16
-// RMSNorm 10240 +10%, bf16 LayerNorm 8192 columns +0.8%, C1 / C5 and the other
-// shapes within 0.4%.  A 64 KiB cap starved fp32 LayerNorm (-12%).
-constexpr int64_t kPipeBytesPerCu = int64_t(96) << 10;
-// Workgroups of fewer lanes keep their full occupancy: at 2 waves each, the
-// cap left 12 waves per CU (bf16 LayerNorm 4096 columns -2.7%).
-constexpr int kPipeCapMinBlock = 256;
-
 // Launch the register-resident kernel (one row group per row) or the
-// persistent one (grid capped at the resident capacity, and at
-// kPipeBytesPerCu of rows in flight per CU) through `launch`.
+// persistent one (grid capped at the resident capacity, and at the input
+// bytes a CU may hold in flight: pipe_grid) through `launch`.
 template <class RowsK, class PipeK, class Launch>
 hipError_t launch_rows_or_pipe(RowsK rows_k, PipeK pipe_k, bool persist, int64_t rows,
                                const Geometry& g, Launch&& launch, int64_t row_bytes) {
-  if (persist) {
-    const int64_t per_block = 2 * (g.block / g.tpr) * row_bytes;  // current + next rows
-    const int64_t pb = std::max<int64_t>(per_block, 1);
-    const int max_per_cu = g.block < kPipeCapMinBlock
-                               ? 1 << 30
-                               : static_cast<int>(std::max<int64_t>(2, kPipeBytesPerCu / pb));
-    const int64_t cap = resident_blocks(reinterpret_cast<const void*>(pipe_k), g.block, max_per_cu);
-    launch(pipe_k, std::min<int64_t>(grid_for(rows, g), std::max<int64_t>(cap, 1)));
-  } else {
-    launch(rows_k, grid_for(rows, g));
-  }
+  if (persist) launch(pipe_k, pipe_grid(reinterpret_cast<const void*>(pipe_k), g, rows, row_bytes));
+  else launch(rows_k, grid_for(rows, g));
   return hipGetLastError();
 }
 

@@ -93,6 +93,12 @@ constexpr int kPipeMaxIt = 4;
 // units); the occupancy is cached.
 int64_t resident_blocks(const void* kernel, int block, int max_per_cu = 1 << 30);
 
+// Grid of a persistent row kernel over `rows` rows of `row_bytes` input
+// bytes each: as many workgroups as are resident at once (capped by the input
+// bytes a CU may hold in flight, current and next rows), at most one per row
+// group.
+int64_t pipe_grid(const void* kernel, const Geometry& g, int64_t rows, int64_t row_bytes);
+
 // Register budget per lane for a register-resident row: 64 values (the
 // compiler widens every 16-bit value it reuses to an fp32 register), i.e. 16
 // fp32 or 8 bf16/fp16 vectors of 16 bytes, or 16 scalar elements for rows that
