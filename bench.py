@@ -28,7 +28,8 @@ between kernels).  C1 adds the HIP runtime's own device-to-device copy
 the scalar mean of the 8192 row losses on the GPU (``full_step``).
 
   python bench.py [--steps K] [--warmup W] [--workload KEY] [--all] [--no-cpu]
-                  [--no-per-config]
+                  [--no-per-config] [--graph] [--copy-at B ...] [--read-at B ...]
+                  [--runtime-copy-at B ...]
 
 Prints ONE JSON line on stdout (``--all``: one per workload).  Progress goes
 to stderr.  Only one GPU is used: ``--gpus`` above 1 exits with a message.
@@ -217,7 +218,7 @@ def per_config(peaks) -> dict:
     return out
 
 
-def run_workload(key, steps, warmup, peaks, with_cpu, cpu_budget):
+def run_workload(key, steps, warmup, peaks, with_cpu, cpu_budget, graph=False):
     w = WORKLOADS[key]
     log(f"[bench] {key}: generating inputs")
     cpu_args = w.make()
@@ -230,8 +231,20 @@ def run_workload(key, steps, warmup, peaks, with_cpu, cpu_budget):
     # tables, every HBM copy touched), then the `warmup` launches inside
     # time_back_to_back, then the timed region
     harness.warm_gpu(rot.launch, DEVICE_WARM_S)
-    r = harness.time_back_to_back(rot.launch, steps, warmup,
-                                  fence=_roctx.range_(f"vbh-timed:{key}:{steps}"))
+    per_graph = 0
+    if graph:
+        # the launches as replays of a HIP graph of per_graph consecutive
+        # launches: no host work between kernels, under a profiler too
+        per_graph = rot.copies * max(1, 64 // rot.copies)
+        g = harness.capture_graph(rot.launch, per_graph)
+        replays = max(1, steps // per_graph)
+        steps = replays * per_graph
+        r = harness.time_back_to_back(lambda i: g.replay(), replays,
+                                      max(1, warmup // per_graph),
+                                      fence=_roctx.range_(f"vbh-timed:{key}:{steps}"))
+    else:
+        r = harness.time_back_to_back(rot.launch, steps, warmup,
+                                      fence=_roctx.range_(f"vbh-timed:{key}:{steps}"))
     per_launch_ms = r["event_ms"] / steps
     value = w.bytes_per_launch * steps / (r["event_ms"] * 1e-3) / 1e9
     vendor_peak = VENDOR_PEAK_GBPS
@@ -255,6 +268,8 @@ def run_workload(key, steps, warmup, peaks, with_cpu, cpu_budget):
         "config": {"workload": key, "desc": w.desc, "hbm_copies": rot.copies},
         "latency_us": round(per_launch_ms * 1e3, 3),
         "latency_us_single_launch_median": round(single["median_ms"] * 1e3, 3),
+        "timing": (f"HIP graph replays of {per_graph} launches" if graph
+                   else "back-to-back launches from the host"),
         "roofline": {
             "bound": "hbm",
             "achieved": round(value, 2),
@@ -281,13 +296,19 @@ def run_workload(key, steps, warmup, peaks, with_cpu, cpu_budget):
 
 
 def run_copy_at(nbytes, steps, warmup, peaks, kind="copy"):
-    """The stream copy moving `nbytes` per launch (half read, half written), or
-    with kind "read" the streaming read of `nbytes`, rotated through >= 2 GiB
-    and timed like a workload: the yardstick of what a kernel of that size can
-    reach."""
+    """The stream copy moving `nbytes` per launch (half read, half written),
+    with kind "read" the streaming read of `nbytes`, or with kind
+    "runtime_copy" the HIP runtime's own device-to-device copy
+    (hipMemcpyAsync through torch's copy_) moving `nbytes`, rotated through
+    >= 2 GiB and timed like a workload: the yardstick of what a kernel of that
+    size can reach."""
     if kind == "read":
         launch, moved, copies = harness.read_rotation("cuda:0", nbytes)
         desc = f"vbh_stream_read of {moved} B per launch, {copies} buffers"
+    elif kind == "runtime_copy":
+        launch, moved, copies = harness.runtime_copy_rotation("cuda:0", nbytes)
+        desc = (f"hipMemcpyAsync device-to-device of {moved // 2} B per launch "
+                f"(read + write {moved} B), {copies} buffer pairs")
     else:
         launch, moved, copies = harness.copy_rotation("cuda:0", nbytes)
         desc = (f"vbh_stream_copy of {moved // 2} B per launch "
@@ -320,11 +341,15 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default=None, choices=sorted(WORKLOADS),
+                    help=f"default {HEADLINE} (none when only yardsticks are asked for)")
     ap.add_argument("--all", action="store_true", help="every measured workload, one line each")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-per-config", action="store_true",
                     help="leave the per_config block out of the headline line")
+    ap.add_argument("--graph", action="store_true",
+                    help="time the workloads' launches as replays of a HIP graph of "
+                         "consecutive launches (no host work between kernels)")
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="seconds of timed CPU work for the CPU baseline")
     ap.add_argument("--copy-at", type=int, nargs="+", metavar="BYTES",
@@ -333,6 +358,9 @@ def main():
     ap.add_argument("--read-at", type=int, nargs="+", metavar="BYTES",
                     help="instead of workloads: the streaming read of BYTES per launch, "
                          "one line per size")
+    ap.add_argument("--runtime-copy-at", type=int, nargs="+", metavar="BYTES",
+                    help="instead of workloads: the HIP runtime's device-to-device copy "
+                         "moving BYTES per launch (read + write), one line per size")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -348,16 +376,18 @@ def main():
     peaks = {"copy": harness.copy_peak("cuda:0"), "read": harness.read_peak("cuda:0")}
     log(f"[bench] measured stream-copy peak: {peaks['copy'] / 1e9:.1f} GB/s (read + write), "
         f"stream-read peak: {peaks['read'] / 1e9:.1f} GB/s")
-    if args.copy_at or args.read_at:
-        for nbytes in args.copy_at or []:
-            print(json.dumps(run_copy_at(nbytes, args.steps, args.warmup, peaks)), flush=True)
-        for nbytes in args.read_at or []:
-            print(json.dumps(run_copy_at(nbytes, args.steps, args.warmup, peaks, "read")),
+    yardsticks = args.copy_at or args.read_at or args.runtime_copy_at
+    for kind, sizes in (("copy", args.copy_at), ("read", args.read_at),
+                        ("runtime_copy", args.runtime_copy_at)):
+        for nbytes in sizes or []:
+            print(json.dumps(run_copy_at(nbytes, args.steps, args.warmup, peaks, kind)),
                   flush=True)
+    if yardsticks and not (args.all or args.workload):
         return
-    keys = sorted(WORKLOADS) if args.all else [args.workload]
+    keys = sorted(WORKLOADS) if args.all else [args.workload or HEADLINE]
     for key in keys:
-        line = run_workload(key, args.steps, args.warmup, peaks, not args.no_cpu, args.cpu_budget)
+        line = run_workload(key, args.steps, args.warmup, peaks, not args.no_cpu, args.cpu_budget,
+                            graph=args.graph)
         if key == HEADLINE and not args.all and not args.no_per_config:
             line["per_config"] = per_config(peaks)
             line["full_step"] = line["per_config"][HEADLINE]["full_step"]

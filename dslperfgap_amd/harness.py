@@ -311,12 +311,10 @@ def runtime_copy_rotation(device, traffic_bytes: int, min_footprint: int = 2 << 
     return launch, 2 * half, copies
 
 
-def graph_replay_ms(launch: Callable[..., None], launches: int, replays: int = 20) -> dict:
-    """Device time per launch when `launches` consecutive launches (launch(k,
-    stream) for k = 0 .. launches - 1) are captured into one HIP graph and the
-    graph is replayed `replays` times back to back: the launch sequence with no
-    host work between kernels.  Returns the per-launch ms (events around the
-    replays) and the launch count."""
+def capture_graph(launch: Callable[..., None], launches: int):
+    """A HIP graph (torch.cuda.CUDAGraph) holding `launches` consecutive
+    launches, launch(k, stream) for k = 0 .. launches - 1 on the capture
+    stream, after one eager pass of them on a side stream; replayed 3 times."""
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):  # warm-up outside the capture
@@ -332,6 +330,16 @@ def graph_replay_ms(launch: Callable[..., None], launches: int, replays: int = 2
     for _ in range(3):
         graph.replay()
     torch.cuda.synchronize()
+    return graph
+
+
+def graph_replay_ms(launch: Callable[..., None], launches: int, replays: int = 20) -> dict:
+    """Device time per launch when `launches` consecutive launches (launch(k,
+    stream) for k = 0 .. launches - 1) are captured into one HIP graph and the
+    graph is replayed `replays` times back to back: the launch sequence with no
+    host work between kernels.  Returns the per-launch ms (events around the
+    replays) and the launch count."""
+    graph = capture_graph(launch, launches)
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record()
     for _ in range(replays):

@@ -20,19 +20,23 @@ adds logsumexp and cross-entropy byte models), evaluated on meta tensors.
 Presets:
   configs    the five measured configs of ``bench.py --all`` (C1-C5)
   reference  the family at the reference's large shapes (cliff_roofline.py)
-  pipes      instruction counters of the configs (SQ_INSTS_*, SQ_WAVES,
-             VALUBusy; one or more ``--pmc`` runs of ``bench.py --all``)
+  pipes      instruction counters (SQ_INSTS_*, SQ_WAVES, VALUBusy) of the
+             configs (one or more ``--pmc`` runs of ``bench.py --all``) or,
+             with ``--of reference``, of the reference's large shapes (runs of
+             cliff_roofline.py)
+  timed      the kernel dispatches inside bench.py's timed roctx ranges
+             (``vbh-timed:<workload>:<steps>``) next to the lines bench.py
+             printed in the same run, whose per-launch event time the traced
+             period must agree with -- the headline (bench.py's default run,
+             C4), every config, or the copy / read / runtime-copy yardsticks
 
     python -m dslperfgap_amd.viperbench.rocprof_summary configs \\
         --trace D/trace/all_kernel_stats.csv --fetch D/fetch/all_counter_collection.csv \\
         --write D/write/all_counter_collection.csv --out-dir profiles
 
-    python -m dslperfgap_amd.viperbench.rocprof_summary headline \\
-        --trace D/c2trace/c2_kernel_stats.csv --bench-line D/c2_bench.jsonl --out-dir profiles
-
-``headline`` summarises the trace of bench.py's default run (C2) next to the
-line bench.py printed in the same run, whose per-launch event time the
-trace's average duration must agree with.
+    python -m dslperfgap_amd.viperbench.rocprof_summary timed \\
+        --kernel-trace D/c4/c4_kernel_trace.csv --markers D/c4/c4_marker_api_trace.csv \\
+        --bench-lines D/c4_bench.jsonl --out-dir profiles
 """
 from __future__ import annotations
 
@@ -64,7 +68,8 @@ CONFIG_KERNELS = [
     ("C2_rms_norm", r"rms_norm_rowsIDF16bDF16bLi8ELi2ELi\dE"),
     ("C3_log_softmax", r"softmax_rows<float, float, 4, 2, true, \d(, false)?>"),
     ("C3_softmax", r"softmax_rows<float, float, 4, 2, false, \d(, false)?>"),
-    ("C3_logsumexp", r"logsumexp_rows<float, float, 4, 8, true(, false)?>"),
+    ("C3_logsumexp", r"logsumexp_rows<float, float, 4, 8, true(, false){0,2}>|"
+                     r"logsumexp_rowsIffLi4ELi8ELb1E(Lb0E){0,2}E"),
     ("C4_cross_entropy", r"ce_fwd_rows<float, 4, 8, true(, false){0,2}>|"
                          r"ce_fwd_rowsIfLi4ELi8ELb1E(Lb0E){0,2}E"),
     ("C4_cross_entropy_bwd", r"ce_bwd_tiles<float, 4, \d(, false)?>|ce_bwd_tilesIfLi4ELi\dE"),
@@ -77,7 +82,8 @@ REFERENCE_KERNELS = [
     ("rms_norm", r"rms_norm_pipeIDF16_DF16_Li8ELi2ELi\dELb1E"),
     ("softmax", r"softmax_rowsIDF16_DF16_Li8ELi4ELb0ELi\dE"),
     ("log_softmax", r"softmax_rowsIDF16_DF16_Li8ELi4ELb1ELi\dE"),
-    ("logsumexp", r"logsumexp_rows<float, float, 4, 8, true(, false)?>"),
+    ("logsumexp", r"logsumexp_rows<float, float, 4, 8, true(, false){0,2}>|"
+                  r"logsumexp_rowsIffLi4ELi8ELb1E(Lb0E){0,2}E"),
     ("cross_entropy", r"ce_fwd_rows<float, 4, \d, true(, false){0,2}>|"
                       r"ce_fwd_rowsIfLi4ELi\dELb1E(Lb0E){0,2}E"),
     ("argmax", r"reduce_rowsIDF16_DF16_Li8ELi2E"),
@@ -373,8 +379,33 @@ def pipes_table(counters: dict, stats: dict, elements: dict, order) -> list[dict
     return rows
 
 
-def render_pipes(trace, pmcs, tail: int = 0, bench_lines=None) -> str:
-    kernels = CONFIG_KERNELS
+def reference_elements() -> dict:
+    """Input elements per launch of each kernel at the reference's large shape
+    (cliff_roofline.py's ENTRIES; 4-byte words for the 4 GiB yardsticks)."""
+    sq, wide = 8192 * 8192, 8192 * 32768
+    return {"layer_norm": sq, "rms_norm": sq, "softmax": 4096 * 32768,
+            "log_softmax": 4096 * 32768, "logsumexp": 8192 * 16384,
+            "cross_entropy": 4096 * 32768, "argmax": wide, "max_reduction": wide,
+            "mean_reduction": wide, COPY: (4 << 30) // 4, READ: (4 << 30) // 4}
+
+
+PIPE_TARGETS = {
+    "configs": dict(kernels=lambda: CONFIG_KERNELS, elements=lambda: config_elements(),
+                    cmd=lambda: PRESETS["configs"]["pmc_cmd"], file=PIPES_FILE,
+                    what="every measured workload (C1-C5, bench.py --all)",
+                    tail_note="bench.py's timed launches"),
+    "reference": dict(kernels=lambda: REFERENCE_KERNELS, elements=lambda: reference_elements(),
+                      cmd=lambda: ("python3 -u -m dslperfgap_amd.viperbench.cliff_roofline "
+                                   "--out RUN/cliff_pipes.csv"),
+                      file="reference_shapes_instruction_counters.txt",
+                      what="the family at the reference's large shapes (cliff_roofline.py)",
+                      tail_note="the HBM-cycled launches cliff_roofline.py times last"),
+}
+
+
+def render_pipes(trace, pmcs, tail: int = 0, bench_lines=None, of: str = "configs") -> str:
+    tgt = PIPE_TARGETS[of]
+    kernels = tgt["kernels"]()
     order = [k for k, _ in kernels]
     stats = read_stats(trace, kernels)
     counters = read_counters(pmcs, kernels, tail)
@@ -382,9 +413,9 @@ def render_pipes(trace, pmcs, tail: int = 0, bench_lines=None) -> str:
     if missing:
         raise ValueError(f"pipes: no kernel in the rocprofv3 files matched {missing}; "
                          "update the symbol patterns")
-    rows = pipes_table(counters, stats, config_elements(), order)
+    rows = pipes_table(counters, stats, tgt["elements"](), order)
     tdir, tpre = _dir_prefix(trace, "_kernel_stats.csv")
-    cmd = PRESETS["configs"]["pmc_cmd"]
+    cmd = tgt["cmd"]().replace("RUN", str(Path(tdir).parent))
     runs = []
     for path in pmcs:
         d, pre = _dir_prefix(path, "_counter_collection.csv")
@@ -393,16 +424,16 @@ def render_pipes(trace, pmcs, tail: int = 0, bench_lines=None) -> str:
         runs.append(f"  timeout -s KILL 400 rocprofv3 --pmc {' '.join(names)} \\\n"
                     f"      --output-format csv -d {d} -o {pre} -- {cmd}")
     head = [
-        "rocprofv3 instruction counters -- every measured workload (C1-C5, bench.py --all) "
-        "(MI355X, gfx950)", "",
+        f"rocprofv3 instruction counters -- {tgt['what']} (MI355X, gfx950)", "",
         "Commands (from the repository root, after `cd /tmp && export TMPDIR=/tmp`), one run",
         "per counter group, and the kernel trace the durations come from:", *runs,
         f"  rocprofv3 --kernel-trace --stats --output-format csv -d {tdir} -o {tpre} -- {cmd}",
         "Summary: python -m dslperfgap_amd.viperbench.rocprof_summary pipes \\",
-        "      --trace <stats csv> --pmc <counter csv> ... --tail 50 --bench-lines <bench.py lines>",
+        f"      --of {of} --trace <stats csv> --pmc <counter csv> ... --tail {tail}"
+        + (" --bench-lines <bench.py lines>" if of == "configs" else ""),
         "",
         "Counters are totals per dispatch (every shader engine of the 8 XCDs), averaged over",
-        "the last 50 dispatches of each workload's kernel (bench.py's timed launches; the",
+        f"the last {tail} dispatches of each workload's kernel ({tgt['tail_note']}; the",
         "yardsticks over all of theirs); per-wave figures divide by SQ_WAVES.",
         "VALU/64el = VALU instructions per 64 input elements (one wave64 instruction per",
         "element would be 1.0).  VALU floor = SQ_INSTS_VALU x 4 cycles / 1024 SIMDs at the",
@@ -468,9 +499,13 @@ def alg_bytes_of(key: str) -> int:
     """Algorithmic bytes per launch of a workload key, or of ``copy@N`` (the
     stream copy moving N bytes per launch, read + write) or ``read@N`` (the
     streaming read of N bytes per launch)."""
-    if key.startswith(("copy@", "read@")):
+    if key.startswith(YARDSTICK_KINDS):
         return int(key.split("@", 1)[1])
     return WORKLOADS[key].bytes_per_launch
+
+
+# bench.py's yardstick lines: key prefix -> command-line option
+YARDSTICK_KINDS = ("copy@", "read@", "runtime_copy@")
 
 
 def timed_row(dispatches: list[dict], rng: dict, alg_bytes: int) -> dict:
@@ -536,16 +571,24 @@ def render_timed(kernel_trace, markers, bench_lines) -> tuple[str, dict]:
     tdir, tpre = _dir_prefix(kernel_trace, "_kernel_trace.csv")
     rows = [timed_row(dispatches, r, alg_bytes_of(r["workload"])) for r in ranges]
     keys = [r["workload"] for r in rows]
-    if all(k.startswith(("copy@", "read@")) for k in keys):
-        sizes = {kind: [k.split("@", 1)[1] for k in keys if k.startswith(kind + "@")]
-                 for kind in ("copy", "read")}
-        args = " ".join(f"--{kind}-at " + " ".join(v) for kind, v in sizes.items() if v)
+    sizes = {kind: [k.split("@", 1)[1] for k in keys if k.startswith(kind + "@")]
+             for kind in ("copy", "read", "runtime_copy")}
+    yard = " ".join(f"--{kind.replace('_', '-')}-at " + " ".join(v)
+                    for kind, v in sizes.items() if v)
+    work = [k for k in keys if not k.startswith(YARDSTICK_KINDS)]
+    if len(work) > 1:
+        args = "--all"
+    elif work:
+        args = "" if work == ["C4_cross_entropy"] and not yard else f"--workload {work[0]}"
     else:
-        args = "--all" if len(rows) > 1 else (
-            "" if keys == ["C4_cross_entropy"] else f"--workload {keys[0]}")
+        args = ""
+    args = f"{args} {yard}".strip()
+    graphed = any("graph" in lines.get(k, {}).get("timing", "") for k in work)
     steps = rows[0]["steps"]
     step_arg = "" if steps == 1000 else f" --steps {steps}"
-    cmd = f"python3 -u bench.py {args}{step_arg} --no-cpu".replace("  ", " ")
+    extra = (" --graph" if graphed else "") + (" --no-per-config" if not args or
+                                                args == yard else "")
+    cmd = f"python3 -u bench.py {args}{step_arg} --no-cpu{extra}".replace("  ", " ")
     head = [f"rocprofv3 kernel trace of bench.py's timed regions (MI355X, gfx950)", "",
             "Command (from the repository root, after `cd /tmp && export TMPDIR=/tmp`):",
             f"  rocprofv3 --kernel-trace --marker-trace --output-format csv -d {tdir} -o {tpre} -- \\",
@@ -615,6 +658,8 @@ def main(argv=None) -> int:
     ap.add_argument("--tail", type=int, default=0,
                     help="counters: only the last TAIL dispatches of each workload's kernel "
                          "(bench.py's timed launches are each workload's last ones)")
+    ap.add_argument("--of", choices=sorted(PIPE_TARGETS), default="configs",
+                    help="pipes: the configs (bench.py --all) or the reference's large shapes")
     ap.add_argument("--out-dir", default=None, help="write the summaries here (else print)")
     args = ap.parse_args(argv)
     if args.preset == "timed":
@@ -635,9 +680,10 @@ def main(argv=None) -> int:
     if args.preset == "pipes":
         if not (args.trace and args.pmc):
             ap.error("pipes needs --trace and at least one --pmc")
-        txt = render_pipes(args.trace, args.pmc, tail=args.tail, bench_lines=args.bench_lines)
+        txt = render_pipes(args.trace, args.pmc, tail=args.tail, bench_lines=args.bench_lines,
+                           of=args.of)
         if args.out_dir:
-            Path(args.out_dir, PIPES_FILE).write_text(txt)
+            Path(args.out_dir, PIPE_TARGETS[args.of]["file"]).write_text(txt)
         else:
             sys.stdout.write(txt)
         return 0
