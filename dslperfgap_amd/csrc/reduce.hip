@@ -84,6 +84,37 @@ __device__ __forceinline__ ValIdx group_allreduce_vi(ValIdx a, int tpr, float* l
   return r;
 }
 
+// IEEE maximum of a 16-byte vector's values: NaN if one of them is NaN
+// (fp16 pairs go to v_pk_maximum3_f16, fp32 values to v_maximum3_f32).
+template <typename T, int V>
+__device__ __forceinline__ float vec_max_nan(const typename Raw<T, V>::type& r) {
+  float m = raw_at<T, V>(r, 0);
+#pragma unroll
+  for (int k = 1; k < V; ++k) m = max_nan(m, raw_at<T, V>(r, k));
+  return m;
+}
+
+// The first element of `r` equal to `m` (the vector's maximum, so one
+// exists), or its first NaN when `m` is NaN: (its value, its position in `r`).
+// A NaN comes back as the canonical quiet NaN.
+template <typename T, int V>
+__device__ __forceinline__ ValIdx first_max_at(const typename Raw<T, V>::type& r, float m) {
+  const bool nan = m != m;
+  ValIdx f{m, V - 1};
+#pragma unroll
+  for (int k = V - 1; k >= 0; --k) {
+    const float v = raw_at<T, V>(r, k);
+    if (nan ? v != v : v == m) f = ValIdx{v, k};
+  }
+  if (nan) f.v = __builtin_nanf("");
+  return f;
+}
+
+// An element as a (value, position) candidate, a NaN as the canonical one.
+__device__ __forceinline__ ValIdx candidate(float v, int i) {
+  return ValIdx{v != v ? __builtin_nanf("") : v, i};
+}
+
 template <typename T, int V, int OP>
 __device__ __forceinline__ void write_result(void* vals, int64_t* idx, int64_t o, float sum_or_v,
                                              int i, int n, const Span& sv, const Span& si) {
@@ -163,22 +194,15 @@ __global__ __launch_bounds__(kMaxBlock) void reduce_rows(const Ti* __restrict__ 
     s = group_allreduce<Sum>(s, tpr, lds);
     if (live && g == 0) write_result<To, V, OP>(vals, idx, row, s, 0, n, sv, si);
   } else {
-    // A lane visits its positions in increasing order, so a later value only
-    // wins when it is strictly larger (or the first NaN).  Per 16-byte vector:
-    // an fmax tree and a NaN test; the index search runs only when the vector
-    // beats the lane's best, which is rare after the first few vectors.
-    ValIdx best{kNegInf, n};  // an empty lane loses to any element
-    bool done = false;        // a NaN was found: nothing later can win
-    if (hv) {
-      float v;
-      load_f32<Ti, 1>(x + start + g, &v, sx);
-      if (v != v) {
-        best = ValIdx{__builtin_nanf(""), g};
-        done = true;
-      } else {
-        best = ValIdx{v, g};
-      }
-    }
+    // The lane's vectors are visited in increasing position order.  Per vector
+    // only its IEEE maximum (NaN if it holds one) is formed and compared with
+    // the lane's best; the winning vector is kept raw, and the position of its
+    // first maximal (or first NaN) element is looked up once, after the loop.
+    // A later vector wins only with a strictly larger maximum, or with the
+    // first NaN, so the lane's result is its first maximal position.
+    float bv = kNegInf;  // best vector's maximum
+    int bj = -1;         // its vector index (-1: none yet)
+    RT braw = RT{};
     for (int base = g; base < nvec; base += kChunk * tpr) {
       RT r[kChunk];
 #pragma unroll
@@ -189,38 +213,29 @@ __global__ __launch_bounds__(kMaxBlock) void reduce_rows(const Ti* __restrict__ 
 #pragma unroll
       for (int c = 0; c < kChunk; ++c) {
         const int j = base + c * tpr;
-        if (done || j >= nvec) continue;
-        float v[V];
-#pragma unroll
-        for (int k = 0; k < V; ++k) v[k] = raw_at<Ti, V>(r[c], k);
-        float m = v[0];
-        bool nan = v[0] != v[0];
-#pragma unroll
-        for (int k = 1; k < V; ++k) {
-          m = fmaxf(m, v[k]);
-          nan |= v[k] != v[k];
-        }
-        if (nan) {  // first NaN of the vector (unrolled selects, no indexed registers)
-          int kk = V - 1;
-#pragma unroll
-          for (int k = V - 1; k >= 0; --k)
-            if (v[k] != v[k]) kk = k;
-          best = ValIdx{__builtin_nanf(""), head + j * V + kk};
-          done = true;
-        } else if (m > best.v || best.i == n) {  // first position of the vector max
-          int kk = V - 1;
-#pragma unroll
-          for (int k = V - 1; k >= 0; --k)
-            if (v[k] == m) kk = k;
-          best = ValIdx{m, head + j * V + kk};
-        }
+        const float m = vec_max_nan<Ti, V>(r[c]);
+        const bool win = j < nvec && (bj < 0 || m > bv || (m != m && bv == bv));
+        bv = win ? m : bv;
+        bj = win ? j : bj;
+        braw = win ? r[c] : braw;
       }
     }
-    if (tv && !done) {
+    ValIdx best{kNegInf, n};  // an empty lane loses to any element
+    if (bj >= 0) {
+      const ValIdx f = first_max_at<Ti, V>(braw, bv);
+      best = ValIdx{f.v, head + bj * V + f.i};
+    }
+    // the head element precedes every body position and the tail element
+    // follows them; pick() orders by value (NaN largest), then position
+    if (hv) {
+      float v;
+      load_f32<Ti, 1>(x + start + g, &v, sx);
+      best = pick(candidate(v, g), best);
+    }
+    if (tv) {
       float v;
       load_f32<Ti, 1>(x + start + tail0 + g, &v, sx);
-      if (v != v) best = ValIdx{__builtin_nanf(""), tail0 + g};
-      else if (v > best.v || best.i == n) best = ValIdx{v, tail0 + g};
+      best = pick(best, candidate(v, tail0 + g));
     }
     best = group_allreduce_vi(best, tpr, lds);
     if (live && g == 0) write_result<To, V, OP>(vals, idx, row, best.v, best.i, n, sv, si);
