@@ -115,6 +115,15 @@ int it_target(int op, int64_t nvec, int vec, bool column_blocks) {
   // 896 vectors 2 per lane loses 1-8%, from 1664 vectors on 13 or more waves
   // per row lose 6%)
   if (op == VBH_OP_LAYER_NORM && vec == 8 && nvec > 1024 && nvec <= 1536) return 2;
+  // 16-bit LayerNorm rows that 4 vectors per lane would leave short of whole
+  // waves (so the guarded persistent kernel runs) but 2 per lane fill exactly
+  // (the unguarded one): 2 vectors per lane.  MI355X, 8192 rows, 4 -> 2: bf16
+  // 3072 columns 4188 -> 5303 GB/s, 5120 4891 -> 5501, fp16 7168 5369 -> 5667;
+  // bf16 2048 x 7168 3779 -> 4916, 4096 x 5120 4292 -> 5044.  Rows that 4 per
+  // lane already fill keep 4 (bf16 6144 columns: 5539 at 4, 5453 at 2).
+  if (op == VBH_OP_LAYER_NORM && vec == 8 && nvec > 4 * kWave && nvec <= 2 * kMaxBlock &&
+      nvec % (4 * kWave) != 0 && nvec % (2 * kWave) == 0)
+    return 2;
   // fp32 LayerNorm rows of 128 or 256 vectors (512 / 1024 columns): 2 vectors
   // per lane, so 1024 columns take a 2-wave row group, persistent in 512-lane
   // workgroups (below).  MI355X, 4 -> 2 per lane: 1024 columns 4575 -> 4720
