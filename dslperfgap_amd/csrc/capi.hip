@@ -288,6 +288,12 @@ bool lse_two_rows_per_block(const Geometry& g, int dtype) {
   return !g.stream && g.tpr == 8 * kWave && g.maxit == 8 && dtype >= 0 && dtype != kBF16;
 }
 
+// 16-bit LayerNorm rows of exactly 2 waves: launches of up to this many rows
+// run one row group per workgroup, with this many bytes of rows in flight per
+// CU (geometry_for)
+constexpr int64_t kLn2WaveRows = 16384;
+constexpr int64_t kLn2WaveBytes = int64_t(64) << 10;
+
 // `units`: row groups of the launch (see fill_it); `out_bytes`: bytes it
 // writes; `column_blocks`: the units are column blocks of longer rows (cross
 // entropy with BLOCK_SIZE < n_cols); `dtype`: the input type where a rule
@@ -309,8 +315,20 @@ Geometry geometry_for(int op, int64_t cols, int vec, int64_t units, int64_t out_
   // instead of one per 128-lane workgroup.  MI355X, persistent kernel, default
   // -> 512 lanes: fp32 2048 columns 5314 -> 5558 GB/s at 134 MB per call, bf16
   // 4096 5207 -> 5303, fp32 1536 4161 -> 4414 at 33.6 MB (5416 -> 5386 at 134 MB).
-  if (op == VBH_OP_LAYER_NORM && !g.stream && g.tpr == 2 * kWave && g_block[op].load() <= 0)
-    g.block = 8 * kWave;
+  // Except 16-bit rows that fill the 2 waves exactly, in launches of up to
+  // kLn2WaveRows rows: one row group per 128-lane workgroup, where the
+  // unguarded persistent kernel runs (it needs a workgroup of one row group),
+  // at most kLn2WaveBytes of rows in flight per CU.  MI355X, bf16 4096
+  // columns, 512-lane workgroups -> this: 1024 rows 2348 -> 3183 GB/s, 2048
+  // 2985 -> 4603, 4096 3982 -> 4934, 8192 4734 -> 5545, 16384 5334 -> 5753;
+  // larger launches keep 512 lanes (65536 rows: 5813 against 5118).
+  if (op == VBH_OP_LAYER_NORM && !g.stream && g.tpr == 2 * kWave && g_block[op].load() <= 0) {
+    if (vec == 8 && cols % vec == 0 && cols / vec == int64_t(g.maxit) * g.tpr &&
+        units <= kLn2WaveRows)
+      g.pipe_bytes = kLn2WaveBytes;
+    else
+      g.block = 8 * kWave;
+  }
   if (op == VBH_OP_LOGSUMEXP && lse_two_rows_per_block(g, dtype) && g_block[op].load() <= 0)
     g.block = 16 * kWave;
   const bool full_output =
@@ -495,9 +513,11 @@ constexpr int kPipeCapMinBlock = 256;
 int64_t pipe_grid(const void* kernel, const Geometry& g, int64_t rows, int64_t row_bytes) {
   const int64_t per_block = 2 * (g.block / g.tpr) * row_bytes;  // current + next rows
   const int64_t pb = std::max<int64_t>(per_block, 1);
-  const int max_per_cu = g.block < kPipeCapMinBlock
-                             ? 1 << 30
-                             : static_cast<int>(std::max<int64_t>(2, kPipeBytesPerCu / pb));
+  const int max_per_cu =
+      g.pipe_bytes > 0 ? static_cast<int>(std::max<int64_t>(1, g.pipe_bytes / pb))
+      : g.block < kPipeCapMinBlock
+          ? 1 << 30
+          : static_cast<int>(std::max<int64_t>(2, kPipeBytesPerCu / pb));
   const int64_t cap = resident_blocks(kernel, g.block, max_per_cu);
   return std::min<int64_t>(grid_for(rows, g), std::max<int64_t>(cap, 1));
 }

@@ -41,6 +41,9 @@ struct Geometry {
   // rows not a multiple of V long: head / aligned body / tail per row (MIS
   // kernels; v is the vector width, tpr >= v)
   bool mis = false;
+  // persistent grid: input bytes of current and next rows a CU may hold in
+  // flight (0: pipe_grid's rule by workgroup size)
+  int64_t pipe_bytes = 0;
 };
 
 // The current device's hipFunction_t of `kernel` (a __global__ function of
