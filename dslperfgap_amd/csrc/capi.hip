@@ -289,10 +289,22 @@ bool lse_two_rows_per_block(const Geometry& g, int dtype) {
 }
 
 // 16-bit LayerNorm rows of exactly 2 waves: launches of up to this many rows
-// run one row group per workgroup, with this many bytes of rows in flight per
-// CU (geometry_for)
+// run one row group per workgroup (geometry_for)
 constexpr int64_t kLn2WaveRows = 16384;
-constexpr int64_t kLn2WaveBytes = int64_t(64) << 10;
+// Input bytes of current and next rows a CU may hold in flight in the
+// unguarded persistent LayerNorm / RMSNorm kernels (16-bit rows that fill
+// their row group, one row group per workgroup), at least 2 workgroups per CU,
+// where every workgroup still gets kPipeFullMinRows rows.  MI355X, interleaved
+// against pipe_grid's 96 KiB rule: LayerNorm bf16 8192 x 8192 5837 -> 5966
+// GB/s, 4096 x 8192 5382 -> 5540, 8192 x 5120 5481 -> 5579, fp16 16384 x 8192
+// 5956 -> 6118; RMSNorm fp16 8192 x 8192 6091 -> 6167, bf16 4096 x 8192 5768
+// -> 5816; but LayerNorm bf16 2048 x 8192 (4 rows per workgroup under the cap)
+// 5050 -> 4943, so launches of fewer rows keep the 96 KiB rule.  bf16
+// LayerNorm rows of 2 waves take the cap whatever their row count: 4
+// workgroups per CU instead of every resident one, +2 to +10% at 2048-16384
+// rows.
+constexpr int64_t kPipeFullBytesPerCu = int64_t(64) << 10;
+constexpr int kPipeFullMinRows = 8;
 
 // `units`: row groups of the launch (see fill_it); `out_bytes`: bytes it
 // writes; `column_blocks`: the units are column blocks of longer rows (cross
@@ -318,16 +330,21 @@ Geometry geometry_for(int op, int64_t cols, int vec, int64_t units, int64_t out_
   // Except 16-bit rows that fill the 2 waves exactly, in launches of up to
   // kLn2WaveRows rows: one row group per 128-lane workgroup, where the
   // unguarded persistent kernel runs (it needs a workgroup of one row group),
-  // at most kLn2WaveBytes of rows in flight per CU.  MI355X, bf16 4096
+  // with its cap of rows in flight per CU (kPipeFullBytesPerCu).  MI355X, bf16 4096
   // columns, 512-lane workgroups -> this: 1024 rows 2348 -> 3183 GB/s, 2048
   // 2985 -> 4603, 4096 3982 -> 4934, 8192 4734 -> 5545, 16384 5334 -> 5753;
   // larger launches keep 512 lanes (65536 rows: 5813 against 5118).
-  if (op == VBH_OP_LAYER_NORM && !g.stream && g.tpr == 2 * kWave && g_block[op].load() <= 0) {
-    if (vec == 8 && cols % vec == 0 && cols / vec == int64_t(g.maxit) * g.tpr &&
-        units <= kLn2WaveRows)
-      g.pipe_bytes = kLn2WaveBytes;
-    else
-      g.block = 8 * kWave;
+  const bool ln_2wave = op == VBH_OP_LAYER_NORM && !g.stream && g.tpr == 2 * kWave &&
+                        g_block[op].load() <= 0;
+  if (ln_2wave && !(vec == 8 && cols % vec == 0 && cols / vec == int64_t(g.maxit) * g.tpr &&
+                    units <= kLn2WaveRows))
+    g.block = 8 * kWave;
+  // the unguarded persistent kernels (16-bit rows filling a row group that is
+  // the whole workgroup: pipe_full in rownorm.hip)
+  if (norm && g.persist && vec == 8 && cols % vec == 0 && g.block == g.tpr &&
+      cols / vec == int64_t(g.maxit) * g.tpr) {
+    g.pipe_bytes = kPipeFullBytesPerCu;
+    g.pipe_min_rows = ln_2wave ? 0 : kPipeFullMinRows;
   }
   if (op == VBH_OP_LOGSUMEXP && lse_two_rows_per_block(g, dtype) && g_block[op].load() <= 0)
     g.block = 16 * kWave;
@@ -513,11 +530,15 @@ constexpr int kPipeCapMinBlock = 256;
 int64_t pipe_grid(const void* kernel, const Geometry& g, int64_t rows, int64_t row_bytes) {
   const int64_t per_block = 2 * (g.block / g.tpr) * row_bytes;  // current + next rows
   const int64_t pb = std::max<int64_t>(per_block, 1);
-  const int max_per_cu =
-      g.pipe_bytes > 0 ? static_cast<int>(std::max<int64_t>(1, g.pipe_bytes / pb))
-      : g.block < kPipeCapMinBlock
-          ? 1 << 30
-          : static_cast<int>(std::max<int64_t>(2, kPipeBytesPerCu / pb));
+  if (g.pipe_bytes > 0) {
+    const int per_cu = static_cast<int>(std::max<int64_t>(2, g.pipe_bytes / pb));
+    const int64_t grid = std::min<int64_t>(grid_for(rows, g),
+                                           std::max<int64_t>(resident_blocks(kernel, g.block, per_cu), 1));
+    if (rows >= mul_sat(mul_sat(g.pipe_min_rows, grid), g.block / g.tpr)) return grid;
+  }
+  const int max_per_cu = g.block < kPipeCapMinBlock
+                             ? 1 << 30
+                             : static_cast<int>(std::max<int64_t>(2, kPipeBytesPerCu / pb));
   const int64_t cap = resident_blocks(kernel, g.block, max_per_cu);
   return std::min<int64_t>(grid_for(rows, g), std::max<int64_t>(cap, 1));
 }

@@ -42,8 +42,10 @@ struct Geometry {
   // kernels; v is the vector width, tpr >= v)
   bool mis = false;
   // persistent grid: input bytes of current and next rows a CU may hold in
-  // flight (0: pipe_grid's rule by workgroup size)
+  // flight (0: pipe_grid's rule by workgroup size), where that leaves every
+  // row group at least pipe_min_rows rows (0: always)
   int64_t pipe_bytes = 0;
+  int pipe_min_rows = 0;
 };
 
 // The current device's hipFunction_t of `kernel` (a __global__ function of
