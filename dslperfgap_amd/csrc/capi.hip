@@ -232,7 +232,7 @@ constexpr int64_t kSplitLongVecs = 12288;   // ... of rows of at least this many
 constexpr int64_t kSplitTarget = 1024;      // segments per launch to aim for
 constexpr int64_t kSplitMinVecs = 512;      // 16-byte vectors per segment, at least
 constexpr int kSplitMaxSegs = 64;
-static_assert(kSplitMaxSegs <= kWave, "the split softmax combines one segment per lane");
+static_assert(kSplitMaxSegs <= kWave, "the second stages combine one segment per lane of a wave");
 
 // Segments per row (a power of two dividing the row's vectors unless `even` is
 // false), or 1.  `long_from`: the op also splits launches of long_from to 511

@@ -358,36 +358,42 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_stream(
 
 // Second stage of a split row (one column block per row, cut into `segs`
 // segments that a first stage reduced with SPLIT semantics into seg_loss, and
-// into SegPairs seg_max / seg_sum, at flat index k * n_rows + row).  One lane
-// per row: the row's lse = M + log S from its segments' pairs under the
+// into SegPairs seg_max / seg_sum, at flat index k * n_rows + row).  One wave
+// per row, lane k holding segment k (segs <= 64): the row's lse = M + log S
+// from its segments' pairs under the
 // golden's rule (a NaN logit, a +inf or an all -inf row give NaN), and the
 // loss adds the lse term the first stage left out (pytorch_impl.py:54-70):
 // lse where the row holds the label, smoothing * lse elsewhere with smoothing,
 // 0 with SPLIT; plus z = lse_square_scale * lse^2 without SPLIT.  The segment
 // losses sum to the rest of the golden's loss (-logit_label and the smoothing
 // sums are additive over segments).
+constexpr int kCombineRowsPerBlock = 4;  // waves of a 256-lane workgroup
+
 __global__ __launch_bounds__(256) void ce_combine(
     const float* __restrict__ seg_loss, const float* __restrict__ seg_sum,
     const float* __restrict__ seg_max, const void* __restrict__ labels, int label_i64,
     float* __restrict__ loss, float* __restrict__ lse_out, float* __restrict__ z_out,
     int64_t n_rows, int n_cols, int segs, CeScalars c) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (row >= n_rows) return;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kCombineRowsPerBlock +
+                      static_cast<int>(threadIdx.x >> 6);
+  if (row >= n_rows) return;  // a whole wave
+  const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
   const Span ssl = VBH_SPAN(seg_loss, segs * n_rows), sss = VBH_SPAN(seg_sum, segs * n_rows);
   const Span ssm = VBH_SPAN(seg_max, segs * n_rows);
   const Span sb = VBH_LABEL_SPAN(labels, label_i64, n_rows);
   const CeOutSpans so{VBH_SPAN(loss, n_rows), VBH_SPAN(lse_out, n_rows), VBH_SPAN(z_out, n_rows)};
-  float rest = 0.f;
-  for (int k = 0; k < segs; ++k) {
-    float sl;
-    load_f32<float, 1>(seg_loss + static_cast<int64_t>(k) * n_rows + row, &sl, ssl);
-    rest += sl;
+  // lane k < segs: segment k's SPLIT loss and SegPair, one load each
+  const bool has = lane < segs;
+  float sl = 0.f, mk = 0.f, tk = 0.f;
+  if (has) {
+    const int64_t i = static_cast<int64_t>(lane) * n_rows + row;
+    load_f32<float, 1>(seg_loss + i, &sl, ssl);
+    load_f32<float, 1>(seg_max + i, &mk, ssm);
+    load_f32<float, 1>(seg_sum + i, &tk, sss);
   }
-  const RowPairs rp = combine_seg_pairs(segs, [&](int k, float* mt) {
-    const int64_t i = static_cast<int64_t>(k) * n_rows + row;
-    load_f32<float, 1>(seg_max + i, &mt[0], ssm);
-    load_f32<float, 1>(seg_sum + i, &mt[1], sss);
-  });
+  const float rest = wave_allreduce<Sum>(sl, kWave);
+  const RowPairs rp = wave_combine_seg_pairs(has, mk, tk);
+  if (lane != 0) return;
   // a +inf max gives inf - inf in the golden: NaN, as an all -inf row does
   const float lse = rp.nan || __builtin_isinf(rp.m) ? __builtin_nanf("") : fast_log(rp.s) + rp.m;
   if (VBH_IN_SPAN(so.lse, lse_out + row, sizeof(float))) lse_out[row] = lse;
@@ -580,9 +586,10 @@ hipError_t launch_cross_entropy_combine(const CeArgs& a, const float* seg_loss,
   const CeScalars c =
       make_scalars(a.smoothing, a.logit_scale, a.lse_square_scale, a.total_classes,
                    a.ignored_index, a.class_start, a.has_smoothing, a.split);
-  launch_kernel(ce_combine, dim3((a.n_rows + 255) / 256), dim3(256), 0, s, seg_loss,
-                     seg_sum, seg_max, a.labels, a.label_i64, a.loss, a.lse, a.z_loss, a.n_rows,
-                     a.n_cols, segs, c);
+  launch_kernel(ce_combine,
+                dim3((a.n_rows + kCombineRowsPerBlock - 1) / kCombineRowsPerBlock),
+                dim3(kCombineRowsPerBlock * kWave), 0, s, seg_loss, seg_sum, seg_max, a.labels,
+                a.label_i64, a.loss, a.lse, a.z_loss, a.n_rows, a.n_cols, segs, c);
   return hipGetLastError();
 }
 

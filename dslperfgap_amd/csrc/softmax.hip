@@ -260,19 +260,26 @@ __global__ __launch_bounds__(kMaxBlock) void logsumexp_rows(const Ti* __restrict
   }
 }
 
-// Second stage of a split logsumexp: one lane per row combines the row's
-// `segs` SegPairs (pairs[2 * (row * segs + k)]) under torch's rules (NaN
-// anywhere: NaN; a +inf max: +inf; all -inf: -inf).
+// Second stage of a split logsumexp: one wave per row, lane k holding the
+// row's segment k (segs <= 64), merges the row's `segs` SegPairs
+// (pairs[2 * (row * segs + k)]) under torch's rules (NaN anywhere: NaN; a +inf
+// max: +inf; all -inf: -inf).
+constexpr int kCombineRowsPerBlock = 4;  // waves of a 256-lane workgroup
+
 template <typename To>
 __global__ __launch_bounds__(256) void logsumexp_pairs_combine(const float* __restrict__ pairs,
                                                                To* __restrict__ y, int64_t rows,
                                                                int segs) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (row >= rows) return;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kCombineRowsPerBlock +
+                      static_cast<int>(threadIdx.x >> 6);
+  if (row >= rows) return;  // a whole wave
+  const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
   const Span sp = VBH_SPAN(pairs, 2 * rows * segs), sy = VBH_SPAN(y, rows);
-  const RowPairs rp = combine_seg_pairs(segs, [&](int k, float* mt) {
-    load_f32<float, 2>(pairs + 2 * (row * segs + k), mt, sp);
-  });
+  const bool has = lane < segs;
+  float mt[2] = {0.f, 0.f};
+  if (has) load_f32<float, 2>(pairs + 2 * (row * segs + lane), mt, sp);
+  const RowPairs rp = wave_combine_seg_pairs(has, mt[0], mt[1]);
+  if (lane != 0) return;
   float r;
   if (rp.nan) r = __builtin_nanf("");
   else if (__builtin_isinf(rp.m)) r = rp.m;
@@ -631,8 +638,10 @@ hipError_t launch_logsumexp_combine(const float* pairs, void* y, int64_t rows, i
   hipError_t err = hipErrorInvalidValue;
   dispatch_float_type(odt, [&](auto to) {
     using To = typename decltype(to)::type;
-    launch_kernel(logsumexp_pairs_combine<To>, dim3((rows + 255) / 256), dim3(256), 0, s, pairs,
-                  static_cast<To*>(y), rows, segs);
+    launch_kernel(logsumexp_pairs_combine<To>,
+                  dim3((rows + kCombineRowsPerBlock - 1) / kCombineRowsPerBlock),
+                  dim3(kCombineRowsPerBlock * kWave), 0, s, pairs, static_cast<To*>(y), rows,
+                  segs);
     err = hipGetLastError();
   });
   return err;

@@ -495,7 +495,7 @@ struct ExpSub {  // exp(x - m) on a subtract
 // The first stage of a split row writes one SegPair per segment: its max m
 // (NaN if it holds a NaN, -inf if it holds only -inf) and t, the sum over it of
 // exp(x - m) (0 for an all -inf segment).  A second stage merges a row's pairs
-// with combine_seg_pairs: M = max m_k, S = sum t_k * exp(m_k - M) over the
+// (wave_combine_seg_pairs): M = max m_k, S = sum t_k * exp(m_k - M) over the
 // segments whose m_k > -inf, and `nan` if any m_k or t_k is NaN (S is then
 // meaningless, as it is when M is infinite).  The row's logsumexp M + log S is
 // then rounded once, as in a single pass; a logsumexp per segment would round
@@ -505,26 +505,21 @@ struct RowPairs {
   bool nan;
 };
 
-// load(k, mt) puts segment k's (m_k, t_k) into mt[0], mt[1]
-template <class Load>
-__device__ __forceinline__ RowPairs combine_seg_pairs(int segs, Load&& load) {
+// The merge of one row's SegPairs by one wave: lane k < segs (`has`) holds
+// segment k's (m_k, t_k), the other lanes nothing, and every lane gets the
+// row's M, S and `nan`.  The segments' values arrive in one round of loads
+// (one per lane) instead of a loop over them in one lane, whose dependent
+// loads made the second stage of a split row several microseconds long.
+__device__ __forceinline__ RowPairs wave_combine_seg_pairs(bool has, float mk, float tk) {
   const float neg_inf = -__builtin_huge_valf();
-  float mx = neg_inf;
-  bool nan = false;
-  for (int k = 0; k < segs; ++k) {
-    float mt[2];
-    load(k, mt);
-    nan |= mt[0] != mt[0] || mt[1] != mt[1];
-    mx = fmaxf(mx, mt[0]);
+  if (!has) {
+    mk = neg_inf;
+    tk = 0.f;
   }
-  float s = 0.f;
-  if (!nan && !__builtin_isinf(mx)) {
-    for (int k = 0; k < segs; ++k) {
-      float mt[2];
-      load(k, mt);
-      if (mt[0] != neg_inf) s += mt[1] * fast_exp(mt[0] - mx);
-    }
-  }
+  const bool nan = wave_allreduce<Max>(mk != mk || tk != tk ? 1.f : 0.f, kWave) > 0.f;
+  const float mx = wave_allreduce<Max>(mk, kWave);  // NaN where `nan` (then unused)
+  const bool use = !nan && !__builtin_isinf(mx) && mk != neg_inf;
+  const float s = wave_allreduce<Sum>(use ? tk * fast_exp(mk - mx) : 0.f, kWave);
   return RowPairs{mx, s, nan};
 }
 
