@@ -279,13 +279,17 @@ RowSplit split_row(int64_t rows, int64_t cols, int vn, int64_t long_from) {
 constexpr int64_t kMisMinVecs = 4;  // shorter rows keep the scalar kernel
 
 // logsumexp rows of 512 lanes at 8 vectors per lane (4096-vector rows: fp32
-// 16384, 16-bit 32768 columns) run two to a 1024-lane workgroup.  MI355X, one
-// -> two per workgroup: fp32 4096 / 8192 / 16384 x 16384 +7.0 / +6.1 / +5.4%,
-// fp16 2048 / 4096 / 8192 x 32768 +4.7 / +8.7 / +8.2%.  Not bf16: its kernel
+// 16384, 16-bit 32768 columns) run two to a 1024-lane workgroup in launches of
+// at least kLseTwoRowsMin rows.  MI355X, one -> two per workgroup: fp32 4096 /
+// 8192 / 16384 x 16384 +7.0 / +6.1 / +5.4%, fp16 2048 / 4096 / 8192 x 32768
+// +4.7 / +8.7 / +8.2%, but fp32 1024 x 16384 -4%.  Not bf16: its kernel
 // keeps the row widened to fp32 as well (105 VGPRs against 58 for fp16), so
 // two 16-wave workgroups do not fit a CU (bf16 8192 x 32768 -26%).
-bool lse_two_rows_per_block(const Geometry& g, int dtype) {
-  return !g.stream && g.tpr == 8 * kWave && g.maxit == 8 && dtype >= 0 && dtype != kBF16;
+constexpr int64_t kLseTwoRowsMin = 2048;
+
+bool lse_two_rows_per_block(const Geometry& g, int dtype, int64_t rows) {
+  return !g.stream && g.tpr == 8 * kWave && g.maxit == 8 && dtype >= 0 && dtype != kBF16 &&
+         rows >= kLseTwoRowsMin;
 }
 
 // 16-bit LayerNorm rows of exactly 2 waves: launches of up to this many rows
@@ -346,7 +350,8 @@ Geometry geometry_for(int op, int64_t cols, int vec, int64_t units, int64_t out_
     g.pipe_bytes = kPipeFullBytesPerCu;
     g.pipe_min_rows = ln_2wave ? 0 : kPipeFullMinRows;
   }
-  if (op == VBH_OP_LOGSUMEXP && lse_two_rows_per_block(g, dtype) && g_block[op].load() <= 0)
+  if (op == VBH_OP_LOGSUMEXP && lse_two_rows_per_block(g, dtype, units) &&
+      g_block[op].load() <= 0)
     g.block = 16 * kWave;
   const bool full_output =
       op == VBH_OP_LAYER_NORM || op == VBH_OP_RMS_NORM || op == VBH_OP_SOFTMAX;

@@ -194,48 +194,115 @@ __global__ __launch_bounds__(kMaxBlock) void reduce_rows(const Ti* __restrict__ 
     s = group_allreduce<Sum>(s, tpr, lds);
     if (live && g == 0) write_result<To, V, OP>(vals, idx, row, s, 0, n, sv, si);
   } else {
-    // The lane's vectors are visited in increasing position order.  Per vector
-    // only its IEEE maximum (NaN if it holds one) is formed and compared with
-    // the lane's best; the winning vector is kept raw, and the position of its
-    // first maximal (or first NaN) element is looked up once, after the loop.
-    // A later vector wins only with a strictly larger maximum, or with the
-    // first NaN, so the lane's result is its first maximal position.
-    float bv = kNegInf;  // best vector's maximum
-    int bj = -1;         // its vector index (-1: none yet)
-    RT braw = RT{};
-    for (int base = g; base < nvec; base += kChunk * tpr) {
-      RT r[kChunk];
+    ValIdx best;
+    if (nvec >= kChunk * tpr) {  // uniform: every lane holds a chunk of vectors or more
+      // The lane's vectors are visited in increasing position order.  Per vector
+      // only its IEEE maximum (NaN if it holds one) is formed and compared with
+      // the lane's best; the winning vector is kept raw, and the position of its
+      // first maximal (or first NaN) element is looked up once, after the loop.
+      // A later vector wins only with a strictly larger maximum, or with the
+      // first NaN, so the lane's result is its first maximal position.
+      float bv = kNegInf;  // best vector's maximum
+      int bj = -1;         // its vector index (-1: none yet)
+      RT braw = RT{};
+      for (int base = g; base < nvec; base += kChunk * tpr) {
+        RT r[kChunk];
 #pragma unroll
-      for (int c = 0; c < kChunk; ++c) {
-        const int j = base + c * tpr;
-        r[c] = j < nvec ? load_raw<Ti, V, true>(xr + static_cast<int64_t>(j) * V, sx) : RT{};
-      }
+        for (int c = 0; c < kChunk; ++c) {
+          const int j = base + c * tpr;
+          r[c] = j < nvec ? load_raw<Ti, V, true>(xr + static_cast<int64_t>(j) * V, sx) : RT{};
+        }
 #pragma unroll
-      for (int c = 0; c < kChunk; ++c) {
-        const int j = base + c * tpr;
-        const float m = vec_max_nan<Ti, V>(r[c]);
-        const bool win = j < nvec && (bj < 0 || m > bv || (m != m && bv == bv));
-        bv = win ? m : bv;
-        bj = win ? j : bj;
-        braw = win ? r[c] : braw;
+        for (int c = 0; c < kChunk; ++c) {
+          const int j = base + c * tpr;
+          if (j >= nvec) break;  // the lane's later vectors are past the row too
+          const float m = vec_max_nan<Ti, V>(r[c]);
+          const bool win = bj < 0 || m > bv || (m != m && bv == bv);
+          bv = win ? m : bv;
+          bj = win ? j : bj;
+          braw = win ? r[c] : braw;
+        }
       }
-    }
-    ValIdx best{kNegInf, n};  // an empty lane loses to any element
-    if (bj >= 0) {
-      const ValIdx f = first_max_at<Ti, V>(braw, bv);
-      best = ValIdx{f.v, head + bj * V + f.i};
-    }
-    // the head element precedes every body position and the tail element
-    // follows them; pick() orders by value (NaN largest), then position
-    if (hv) {
-      float v;
-      load_f32<Ti, 1>(x + start + g, &v, sx);
-      best = pick(candidate(v, g), best);
-    }
-    if (tv) {
-      float v;
-      load_f32<Ti, 1>(x + start + tail0 + g, &v, sx);
-      best = pick(best, candidate(v, tail0 + g));
+      best = ValIdx{kNegInf, n};  // an empty lane loses to any element
+      if (bj >= 0) {
+        const ValIdx f = first_max_at<Ti, V>(braw, bv);
+        best = ValIdx{f.v, head + bj * V + f.i};
+      }
+      // the head element precedes every body position and the tail element
+      // follows them; pick() orders by value (NaN largest), then position
+      if (hv) {
+        float v;
+        load_f32<Ti, 1>(x + start + g, &v, sx);
+        best = pick(candidate(v, g), best);
+      }
+      if (tv) {
+        float v;
+        load_f32<Ti, 1>(x + start + tail0 + g, &v, sx);
+        best = pick(best, candidate(v, tail0 + g));
+      }
+    } else {
+      // Short rows (fewer than kChunk vectors per lane), visited in
+      // increasing position order: head element, body vectors, tail element.
+      // Per vector an fmax tree and a NaN test; the index search runs where
+      // the vector beats the lane's best (a later value only wins when it is
+      // strictly larger, or the first NaN).  With one or two vectors per lane
+      // this is 3-8% faster than the search after the loop (fp16, 64, 100 and
+      // 255 columns).
+      best = ValIdx{kNegInf, n};  // an empty lane loses to any element
+      bool done = false;        // a NaN was found: nothing later can win
+      if (hv) {
+        float v;
+        load_f32<Ti, 1>(x + start + g, &v, sx);
+        if (v != v) {
+          best = ValIdx{__builtin_nanf(""), g};
+          done = true;
+        } else {
+          best = ValIdx{v, g};
+        }
+      }
+      for (int base = g; base < nvec; base += kChunk * tpr) {
+        RT r[kChunk];
+#pragma unroll
+        for (int c = 0; c < kChunk; ++c) {
+          const int j = base + c * tpr;
+          r[c] = j < nvec ? load_raw<Ti, V, true>(xr + static_cast<int64_t>(j) * V, sx) : RT{};
+        }
+#pragma unroll
+        for (int c = 0; c < kChunk; ++c) {
+          const int j = base + c * tpr;
+          if (done || j >= nvec) continue;
+          float v[V];
+#pragma unroll
+          for (int k = 0; k < V; ++k) v[k] = raw_at<Ti, V>(r[c], k);
+          float m = v[0];
+          bool nan = v[0] != v[0];
+#pragma unroll
+          for (int k = 1; k < V; ++k) {
+            m = fmaxf(m, v[k]);
+            nan |= v[k] != v[k];
+          }
+          if (nan) {  // first NaN of the vector (unrolled selects, no indexed registers)
+            int kk = V - 1;
+#pragma unroll
+            for (int k = V - 1; k >= 0; --k)
+              if (v[k] != v[k]) kk = k;
+            best = ValIdx{__builtin_nanf(""), head + j * V + kk};
+            done = true;
+          } else if (m > best.v || best.i == n) {  // first position of the vector max
+            int kk = V - 1;
+#pragma unroll
+            for (int k = V - 1; k >= 0; --k)
+              if (v[k] == m) kk = k;
+            best = ValIdx{m, head + j * V + kk};
+          }
+        }
+      }
+      if (tv && !done) {
+        float v;
+        load_f32<Ti, 1>(x + start + tail0 + g, &v, sx);
+        if (v != v) best = ValIdx{__builtin_nanf(""), tail0 + g};
+        else if (v > best.v || best.i == n) best = ValIdx{v, tail0 + g};
+      }
     }
     best = group_allreduce_vi(best, tpr, lds);
     if (live && g == 0) write_result<To, V, OP>(vals, idx, row, best.v, best.i, n, sv, si);
