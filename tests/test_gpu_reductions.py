@@ -88,6 +88,45 @@ def test_benchmark_shapes(shape, dtype):
         _close(mean_reduction(xd, 1), ref.mean_reduction(x, 1), "mean")
 
 
+@pytest.mark.parametrize("cols_per_vec", [12, 16, 17, 32, 33, 64, 65, 96])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_max_argmax_both_lane_loops(cols_per_vec, dtype):
+    """Row lengths around the switch between the two max / argmax lane loops
+    (the search after the loop where every lane holds a batch of vectors or
+    more, the per-vector search below): the row's maximum tied across vectors,
+    in the first or last vector of a lane, NaN first or last, and all -inf
+    rows; values and indices exactly."""
+    vn = 16 // torch.empty(0, dtype=dtype).element_size()
+    cols = cols_per_vec * vn
+    g = _g(900 + cols)
+    rows = 48
+    x = torch.randint(-5, 6, (rows, cols), generator=g).float()
+    for r in range(rows):
+        k = r % 6
+        if k == 0:
+            x[r, 0] = 9.0
+            x[r, cols - 1] = 9.0         # tie between the first and the last element
+        elif k == 1:
+            x[r, cols - vn] = 9.0       # first element of the last vector
+        elif k == 2:
+            x[r, vn - 1] = 9.0          # last element of the first vector
+            x[r, cols // 2] = 9.0
+        elif k == 3:
+            x[r, cols - 1] = float("nan")
+        elif k == 4:
+            x[r, 1] = float("nan")
+            x[r, cols - 2] = float("nan")
+        else:
+            x[r, :] = float("-inf")
+    x = x.to(dtype)
+    xd = x.to(DEV)
+    v, i = max_reduction(xd, 1)
+    rv, ri = ref.max_reduction(x, 1)
+    _same(v, rv, f"values cols={cols}")
+    _same(i, ri, f"indices cols={cols}")
+    _same(argmax(xd, 1), ref.argmax(x, 1), f"argmax cols={cols}")
+
+
 @pytest.mark.parametrize("cols", [1, 7, 64, 100, 1000, 4096, 65537])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_widths_ties_and_special_values(cols, dtype):
