@@ -225,6 +225,10 @@ bool write_through_ok(int64_t out_bytes, int64_t units) {
 // entropy starts above 256 rows; 384 x 32768 logsumexp: 3929 unsplit,
 // 3569-3848 split); the streaming mean does not (fp32 256 x 65536: 5217
 // unsplit, 4840-5004 split).
+// Default launches of the persistent cross-entropy forward (ce_fwd_persist):
+// at least this many rows, of at least this many of its chunks.
+constexpr int64_t kCePersistMinRows = 1024;
+constexpr int64_t kCePersistMinChunks = 3;
 constexpr int64_t kSplitMaxRows = 256;      // split launches of fewer rows ...
 constexpr int64_t kSplitRowVecs = 16384;    // ... of 16-byte vectors per row, at least
 constexpr int64_t kSplitMaxRowsLong = 512;  // two-round launches (logsumexp, CE) ...
@@ -1016,6 +1020,19 @@ int vbh_cross_entropy_fwd_ws(const void* logits, const void* labels, int logits_
     }
   }
   const int64_t segments = mul_sat(n_rows, ncb);
+  // the persistent forward (one workgroup per CU walking the rows chunk by
+  // chunk): fp32 rows of one column block and at least one chunk; by default
+  // in launches of at least kCePersistMinRows rows of kCePersistMinChunks
+  // chunks or more.  kFlagPersist lifts those two limits, kFlagNoPersist or a
+  // tpr / block override keeps ce_fwd_rows.
+  const int over = g_flags[VBH_OP_CROSS_ENTROPY].load();
+  if (vec_ok && ncb == 1 && cross_entropy_fwd_persist_fits(logits_dtype, n_cols) &&
+      g_tpr[VBH_OP_CROSS_ENTROPY].load() <= 0 && g_block[VBH_OP_CROSS_ENTROPY].load() <= 0 &&
+      !(over & kFlagNoPersist) &&
+      ((over & kFlagPersist) ||
+       (n_rows >= kCePersistMinRows &&
+        n_cols >= kCePersistMinChunks * cross_entropy_fwd_persist_chunk_cols())))
+    return hip_status(launch_cross_entropy_fwd_persist(a, 0, s), "cross_entropy_fwd launch");
   const bool mis_ok = !vec_ok && aligned16(logits) && bs >= kMisMinVecs * vn;
   Geometry g = geometry_for(VBH_OP_CROSS_ENTROPY, bs, vec_ok || mis_ok ? vn : 1, segments, 0,
                             ncb > 1);

@@ -90,36 +90,44 @@ struct CeOutSpans {
   Span loss, lse, z;
 };
 
-// Per-segment epilogue (pytorch_impl.py:37-76), executed by one lane.
+// Per-segment outputs (pytorch_impl.py:37-76): loss and z_loss from the lse.
+struct CeOut {
+  float loss, z;
+};
+
+__device__ __forceinline__ CeOut ce_outputs(float lse, float sum_logits, bool in_block,
+                                            float logit_label, bool ignored,
+                                            const CeScalars& c) {
+  if (ignored) return CeOut{0.f, 0.f};
+  float l, z;
+  const float lse_term = c.split ? 0.f : lse;
+  if (c.has_smoothing) {
+    if (in_block)
+      l = lse_term - c.smoothing * sum_logits / c.total_classes -
+          c.one_minus_smoothing * logit_label;
+    else
+      l = c.smoothing * (lse_term - sum_logits / c.total_classes);
+  } else {
+    l = in_block ? lse_term - logit_label : 0.f;
+  }
+  if (!c.split) {
+    z = c.lse_square_scale * lse * lse;
+    l = l + z;
+  } else {
+    z = 0.f;
+  }
+  return CeOut{l, z};
+}
+
+// The per-segment epilogue, executed by one lane.
 __device__ __forceinline__ void ce_store(float lse, float sum_logits, bool in_block,
                                          float logit_label, bool ignored,
                                          const CeScalars& c, float* loss, float* lse_out,
                                          float* z_out, int64_t idx, const CeOutSpans& so) {
   if (VBH_IN_SPAN(so.lse, lse_out + idx, sizeof(float))) lse_out[idx] = lse;
-  float l, z;
-  if (ignored) {
-    l = 0.f;
-    z = 0.f;
-  } else {
-    const float lse_term = c.split ? 0.f : lse;
-    if (c.has_smoothing) {
-      if (in_block)
-        l = lse_term - c.smoothing * sum_logits / c.total_classes -
-            c.one_minus_smoothing * logit_label;
-      else
-        l = c.smoothing * (lse_term - sum_logits / c.total_classes);
-    } else {
-      l = in_block ? lse_term - logit_label : 0.f;
-    }
-    if (!c.split) {
-      z = c.lse_square_scale * lse * lse;
-      l = l + z;
-    } else {
-      z = 0.f;
-    }
-  }
-  if (VBH_IN_SPAN(so.loss, loss + idx, sizeof(float))) loss[idx] = l;
-  if (VBH_IN_SPAN(so.z, z_out + idx, sizeof(float))) z_out[idx] = z;
+  const CeOut o = ce_outputs(lse, sum_logits, in_block, logit_label, ignored, c);
+  if (VBH_IN_SPAN(so.loss, loss + idx, sizeof(float))) loss[idx] = o.loss;
+  if (VBH_IN_SPAN(so.z, z_out + idx, sizeof(float))) z_out[idx] = o.z;
 }
 
 // A split row's first stage: the segment's SegPair (max m, sum t of
@@ -184,7 +192,7 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
     const int64_t adj = label - c.class_start;
     in_block = adj >= col0 && adj < col_end;
     if (!ignored && in_block && VBH_IN_SPAN(sx, lr + adj, sizeof(T)))
-      logit_label = static_cast<float>(lr[adj]) * c.logit_scale;
+      logit_label = mul_rn(static_cast<float>(lr[adj]), c.logit_scale);
   }
 
   RT xr[IT];
@@ -237,7 +245,15 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
   const float mb = m * kLog2e;
   const float es = c.exp_scale;
   auto efma = [=](float x) { return __builtin_amdgcn_exp2f(fmaf(x, es, -mb)); };
-  auto esub = [=](float x) { return fast_exp(x * scale - m); };
+  // a scale other than 1: the product rounded first, as the golden rounds
+  // x * scale before it subtracts the max (x * exp_scale would carry
+  // exp_scale's own rounding, up to |x * scale| * 2^-24 in the exponent)
+  auto efms = [=](float x) {
+    return __builtin_amdgcn_exp2f(fmaf(mul_rn(x, scale), kLog2e, -mb));
+  };
+  auto esub = [=](float x) { return fast_exp(mul_rn(x, scale) - m); };
+  const bool one = scale == 1.f;
+  auto ex1 = [&](float x) { return fma_ok ? (one ? efma(x) : efms(x)) : esub(x); };
   auto sum_exp = [&](auto ex) {
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
@@ -251,8 +267,9 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
       }
     }
   };
-  if (fma_ok) sum_exp(efma);
-  else sum_exp(esub);
+  if (!fma_ok) sum_exp(esub);
+  else if (one) sum_exp(efma);
+  else sum_exp(efms);
 #pragma unroll
   for (int w = V / 2; w >= 1; w /= 2)
 #pragma unroll
@@ -261,11 +278,11 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_rows(
       sl[k] += sl[k + w];
     }
   if (hv) {
-    se[0] += fma_ok ? efma(hr) : esub(hr);
+    se[0] += ex1(hr);
     sl[0] += hx;
   }
   if (tv) {
-    se[0] += fma_ok ? efma(tr) : esub(tr);
+    se[0] += ex1(tr);
     sl[0] += tx;
   }
   const float s = group_allreduce<Sum>(se[0], tpr, lds[1]);
@@ -316,7 +333,7 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_stream(
     float cm = kNegInf;
 #pragma unroll
     for (int k = 0; k < V; ++k) {
-      v[k] *= c.logit_scale;
+      v[k] = mul_rn(v[k], c.logit_scale);
       cm = fmaxf(cm, v[k]);
       sl += v[k];
       if (v[k] != v[k]) nan = 1.f;
@@ -349,11 +366,258 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_stream(
   const bool in_block = adj >= col0 && adj < col_end;
   float logit_label = 0.f;
   if (!ignored && in_block && VBH_IN_SPAN(sx, logits + row * ld + adj, sizeof(T)))
-    logit_label = static_cast<float>(logits[row * ld + adj]) * c.logit_scale;
+    logit_label = mul_rn(static_cast<float>(logits[row * ld + adj]), c.logit_scale);
   const int64_t idx = static_cast<int64_t>(cb) * n_rows + row;
   ce_store(lse, gl, in_block, logit_label, ignored, c, loss, lse_out, z_out, idx, so);
   if (c.pair_out) ce_store_pair(has_nan ? __builtin_nanf("") : gm, finite ? gs : 0.f, lse_out,
                                 z_out, idx, so);
+}
+
+// Persistent forward for fp32 rows of one column block (the whole row is the
+// segment): a grid of one 512-lane workgroup per CU, workgroup b taking rows
+// b, b + G, b + 2G, ... (G the grid) in chunks of kCePersistLanes x
+// kCePersistVecs 16-byte vectors (32 KiB), the next chunk's loads in flight
+// while the current one is folded.  All workgroups move through the logits
+// together; ce_fwd_rows (one row per 1024-lane workgroup) leaves a CU's loads
+// idle while a finished workgroup reduces its row and the next one starts.
+// MI355X, fp32 32000 columns, against ce_fwd_rows on the same box: 1024 rows
+// +9%, 2048 +5%, 8192 (C4) +0.9%, 16384 +-0; rows of one chunk or less lose
+// (8192 x 8192: -14%), hence the launcher's default of at least 3 chunks per
+// row.  Chunks of 16 KiB with two or three in flight, 8 KiB with three or four
+// and three of 32 KiB all measured slower at C4 (-0.1 to -20%).
+//
+// Each lane folds its share of a row into an online pair: m, the max of its
+// scaled logits (NaN if any is NaN), and s, the sum of exp(x - m) over its
+// scaled logits x, held relative to 2^nb with nb = m * log2 e rounded -- the
+// FMA form of ce_fwd_rows, 2^(x * log2 e - nb) per logit -- and rescaled by
+// 2^(nb_old - nb) when m grows.  A lane whose max lies beyond that form's
+// range (shift_fma_ok) holds s relative to e^m and takes exp(x - m) on a
+// subtract; a wave takes that path only when one of its lanes needs it.  At
+// the row's end each lane's pair becomes a SegPair (t = s * 2^-shift_residual
+// in the FMA form), and the workgroup merges them as the second stage of a
+// split row merges segments: M = max m, S = sum t * exp(m - M) over the lanes
+// with m > -inf; a NaN anywhere, an infinite M or an all -inf row give the
+// golden's NaN lse (pytorch_impl.py:37-47).  Lanes 0, 1 and 2 then store the
+// row's loss, lse and z_loss.  The label comes from a scalar
+// load one row ahead, its logit from a scalar load at the row's first chunk.
+// Buffer loads with a range of one row: vectors past its end (the last
+// chunk's spare lanes, the loads past a workgroup's last row) read nothing.
+constexpr int kCePersistLanes = 512;
+constexpr int kCePersistVecs = 4;
+constexpr int kCePersistChunk = kCePersistLanes * kCePersistVecs;  // vectors
+constexpr int kCePersistBufs = 2;  // chunks in rotation (loads NB - 1 ahead)
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct CeChunk {
+  f32x4 v[kCePersistVecs];
+};
+
+// SL: the row's sum of scaled logits is needed (smoothing); ONE: logit_scale
+// is 1 (else each logit's product with it is rounded once, as the golden
+// rounds it, and used for the max, the exps and the sum).
+template <bool SL, typename LabelT, bool ONE>
+__global__ __launch_bounds__(kCePersistLanes) void ce_fwd_persist(
+    const float* __restrict__ logits, const LabelT* __restrict__ labels,
+    float* __restrict__ loss, float* __restrict__ lse_out, float* __restrict__ z_out,
+    int64_t n_rows, int n_cols, int64_t ld, CeScalars c) {
+  constexpr int L = kCePersistLanes, U = kCePersistVecs, CH = kCePersistChunk;
+  constexpr int W = L / kWave;
+  // per wave, by row parity: the wave's max, its sum of t * exp(m - max) and
+  // its sum of logits
+  __shared__ float lds_pair[2][3][W];
+  const int lane = static_cast<int>(threadIdx.x);
+  const int wave = lane >> 6;
+  const int64_t b = blockIdx.x;
+  if (b >= n_rows) return;  // the whole workgroup
+  const int64_t grid = gridDim.x;
+  const int nvec = n_cols / 4;
+  const int cpr = (nvec + CH - 1) / CH;
+  const int64_t chunks = ((n_rows - 1 - b) / grid + 1) * cpr;
+  const Span sx = VBH_SPAN(logits, strided_extent(n_rows, ld, n_cols));
+  const Span sb = VBH_SPAN(labels, n_rows);
+  const Span sloss = VBH_SPAN(loss, n_rows), slse = VBH_SPAN(lse_out, n_rows),
+             sz = VBH_SPAN(z_out, n_rows);
+  const float scale = c.logit_scale;
+
+  // the load cursor: row lrow, chunk lc
+  int64_t lrow = b;
+  int lc = 0;
+  // (every lambda is inlined: a call would put the captured cursors in memory)
+  auto load = [&](CeChunk& ch, bool real) __attribute__((always_inline)) {
+    const float* base = logits + (real ? lrow * ld : 0);
+    const bool ok = real && VBH_IN_SPAN(sx, base, static_cast<int64_t>(nvec) * 16);
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(base), static_cast<short>(0), ok ? nvec * 16 : 0, kRawBufferWord3);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int j = lc * CH + u * L + lane;
+      ch.v[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, j * 16, 0, 2));
+    }
+    if (++lc == cpr) {
+      lc = 0;
+      lrow += grid;
+    }
+  };
+
+  // the fold cursor and this lane's pair for the fold's row
+  int64_t frow = b;
+  int fc = 0;
+  float m = kNegInf, nb = kNegInf, s = 0.f, sl = 0.f;
+  // the row's label facts; the next row's label (loaded one row ahead)
+  LabelT label_next = VBH_IN_SPAN(sb, labels + b, sizeof(LabelT)) ? labels[b] : LabelT(0);
+  bool ignored = false, in_row = false;
+  int parity = 0;  // of the fold's row: its LDS slots
+  float logit_raw = 0.f;  // the label's logit, scaled where used (at the row's end)
+
+  auto fold_values = [&](const CeChunk& ch, auto mask) __attribute__((always_inline)) {
+    constexpr bool MASK = decltype(mask)::value;
+    const int c0 = fc * CH;
+    float xv[U][4];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) xv[u][k] = ONE ? ch.v[u][k] : mul_rn(ch.v[u][k], scale);
+    float cm = kNegInf;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool ok = !MASK || c0 + u * L + lane < nvec;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) cm = max_nan(cm, ok ? xv[u][k] : kNegInf);
+    }
+    const float nm = max_nan(m, cm);
+    const float nnb = nm * kLog2e;
+    float xs = 0.f;
+    const bool lane_fma = shift_fma_ok(m) && shift_fma_ok(nm);
+    if (__builtin_amdgcn_ballot_w64(!lane_fma) == 0) {
+      // every lane in the FMA form: s relative to 2^nb
+      float e = 0.f;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const bool ok = !MASK || c0 + u * L + lane < nvec;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float v = __builtin_amdgcn_exp2f(fmaf(xv[u][k], kLog2e, -nnb));
+          e += ok ? v : 0.f;
+          if constexpr (SL) xs += ok ? xv[u][k] : 0.f;
+        }
+      }
+      // an all -inf share so far holds nothing (its exps would be NaN)
+      s = nm == kNegInf ? 0.f : fmaf(s, __builtin_amdgcn_exp2f(nb - nnb), e);
+    } else {
+      // some lane beyond the FMA form: each lane through the sum relative to
+      // e^m (t), the exps on a subtract, back to its new form
+      float e = 0.f;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const bool ok = !MASK || c0 + u * L + lane < nvec;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float v = fast_exp(xv[u][k] - nm);
+          e += ok ? v : 0.f;
+          if constexpr (SL) xs += ok ? xv[u][k] : 0.f;
+        }
+      }
+      float t = m == kNegInf ? 0.f
+                             : (shift_fma_ok(m) ? s * __builtin_amdgcn_exp2f(-shift_residual(m, nb))
+                                                : s);
+      t = nm == kNegInf ? 0.f : t * fast_exp(m - nm) + e;
+      s = shift_fma_ok(nm) && nm != kNegInf
+              ? t * __builtin_amdgcn_exp2f(shift_residual(nm, nnb))
+              : t;
+    }
+    m = nm;
+    nb = nnb;
+    if constexpr (SL) sl += xs;
+    // every path has waited for the whole chunk here, so the loads that reuse
+    // its registers need no wait of their own
+#pragma unroll
+    for (int u = 0; u < U; ++u) asm volatile("" ::"v"(ch.v[u]));
+  };
+
+  auto fold = [&](const CeChunk& ch) __attribute__((always_inline)) {
+    if (fc == 0) {  // a new row: its label facts and logit, the next row's label
+      const int64_t label = static_cast<int64_t>(label_next);
+      ignored = label == c.ignored_index;
+      const int64_t adj = label - c.class_start;
+      in_row = adj >= 0 && adj < n_cols;
+      logit_raw = 0.f;
+      if (!ignored && in_row && VBH_IN_SPAN(sx, logits + frow * ld + adj, sizeof(float)))
+        logit_raw = logits[frow * ld + adj];
+      const int64_t nrow = frow + grid < n_rows ? frow + grid : n_rows - 1;
+      label_next = VBH_IN_SPAN(sb, labels + nrow, sizeof(LabelT)) ? labels[nrow] : LabelT(0);
+    }
+    if (fc == cpr - 1) fold_values(ch, std::true_type{});
+    else fold_values(ch, std::false_type{});
+    if (fc == cpr - 1) {
+      // each wave merges its lanes' pairs into one (a NaN max or sum
+      // propagates into it), one LDS exchange and one barrier per row, and
+      // lanes 0-2 merge the waves' pairs: reads of row k's slots end before
+      // the barrier of row k + 1, writes of row k + 2 come after it
+      const float wm = wave_allreduce<Max>(m, kWave);
+      // this lane's SegPair sum, relative to e^m
+      const float t = shift_fma_ok(m) ? s * __builtin_amdgcn_exp2f(-shift_residual(m, nb)) : s;
+      const bool use = m != kNegInf && !__builtin_isinf(wm);
+      const float ws = wave_allreduce<Sum>(use ? t * fast_exp(m - wm) : 0.f, kWave);
+      const float wl = SL ? wave_allreduce<Sum>(sl, kWave) : 0.f;
+      if ((lane & (kWave - 1)) == 0) {
+        lds_pair[parity][0][wave] = wm;
+        lds_pair[parity][1][wave] = ws;
+        if constexpr (SL) lds_pair[parity][2][wave] = wl;
+      }
+      __syncthreads();
+      if (lane < 3) {
+        float mx = lds_pair[parity][0][0];
+        bool nan = false;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+          const float mw = lds_pair[parity][0][w], sw = lds_pair[parity][1][w];
+          mx = max_nan(mx, mw);
+          nan = nan || mw != mw || sw != sw;
+        }
+        float sum = 0.f, sum_logits = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+          const float mw = lds_pair[parity][0][w];
+          sum += mw != kNegInf ? lds_pair[parity][1][w] * fast_exp(mw - mx) : 0.f;
+          if constexpr (SL) sum_logits += lds_pair[parity][2][w];
+        }
+        const float lse = nan || __builtin_isinf(mx) ? __builtin_nanf("") : fast_log(sum) + mx;
+        const float logit_label = ONE ? logit_raw : mul_rn(logit_raw, scale);
+        const CeOut o = ce_outputs(lse, sum_logits, in_row, logit_label, ignored, c);
+        // (one pointer chosen per lane would put the kernel's locals in scratch)
+        if (lane == 0 && VBH_IN_SPAN(sloss, loss + frow, sizeof(float))) loss[frow] = o.loss;
+        if (lane == 1 && VBH_IN_SPAN(slse, lse_out + frow, sizeof(float))) lse_out[frow] = lse;
+        if (lane == 2 && VBH_IN_SPAN(sz, z_out + frow, sizeof(float))) z_out[frow] = o.z;
+      }
+      parity ^= 1;
+      m = kNegInf;
+      nb = kNegInf;
+      s = 0.f;
+      sl = 0.f;
+    }
+    if (++fc == cpr) {
+      fc = 0;
+      frow += grid;
+    }
+  };
+
+  constexpr int NB = kCePersistBufs;
+  CeChunk buf[NB];
+#pragma unroll
+  for (int i = 0; i < NB - 1; ++i) load(buf[i], i < chunks);
+  const int64_t rounds = chunks / NB;
+  for (int64_t q = 0; q < rounds; ++q) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      load(buf[(i + NB - 1) % NB], q * NB + i + NB - 1 < chunks);
+      fold(buf[i]);
+    }
+  }
+  const int64_t rest = chunks - NB * rounds;  // buf[0 .. rest) hold these chunks
+#pragma unroll
+  for (int i = 0; i < NB - 1; ++i)
+    if (i < rest) fold(buf[i]);
 }
 
 // Second stage of a split row (one column block per row, cut into `segs`
@@ -424,20 +688,26 @@ constexpr int kBwdLanes = kCeBwdLanes;
 // 2^(x * exp_scale - lb) * 2^-res with lb = lse * log2 e rounded and res its
 // rounding error (exact, one FMA), so each element costs one FMA ahead of
 // v_exp_f32; 2^-res rides on the factor (1 + 2 * lss * lse) that multiplies p.
-// Rows whose lse is too large for that form (shift_fma_ok; `fma` false) take
+// Rows whose lse is too large for that form (shift_fma_ok; `form` 0) take
 // exp(x * logit_scale - lse) on a multiply and a subtract, with pf = 1 + 2 * lss * lse.
 struct CeBwdRow {
   float lse, lb, pf, hit, smooth_neg, scale;
-  bool fma;
+  int form;  // ce_grad's FORM for the row
 };
 
 // dlogits of one element: q = p + 2 * lss * lse * p, minus the (smoothed)
 // one-hot (`is_label`); times dloss * logit_scale.  FMA: the row's form of p.
-template <bool FMA>
+// FORM 1: the FMA form (scale 1); 2: the FMA form on the rounded product
+// x * logit_scale (any other scale: x * exp_scale would carry exp_scale's own
+// rounding, |x * scale| * 2^-24 in the exponent, where the golden rounds the
+// product and subtracts lse); 0: the subtract form.
+template <int FORM>
 __device__ __forceinline__ float ce_grad(float xv, bool is_label, const CeBwdRow& b,
                                          const CeScalars& c) {
-  const float p = FMA ? __builtin_amdgcn_exp2f(fmaf(xv, c.exp_scale, -b.lb))
-                      : fast_exp(xv * c.logit_scale - b.lse);
+  const float p =
+      FORM == 1   ? __builtin_amdgcn_exp2f(fmaf(xv, c.exp_scale, -b.lb))
+      : FORM == 2 ? __builtin_amdgcn_exp2f(fmaf(mul_rn(xv, c.logit_scale), kLog2e, -b.lb))
+                  : fast_exp(mul_rn(xv, c.logit_scale) - b.lse);
   float q = p * b.pf;
   if (is_label) q = q - b.hit;
   if (c.has_smoothing) q = q - b.smooth_neg;
@@ -487,9 +757,10 @@ __global__ __launch_bounds__(kBwdLanes) void ce_bwd_tiles(
   CeBwdRow b;
   b.lse = lse_r;
   // the workgroup's tile is one row's: a scalar branch on the row's form
-  b.fma = __builtin_amdgcn_readfirstlane(static_cast<int>(shift_fma_ok(lse_r))) != 0;
+  const bool fma = __builtin_amdgcn_readfirstlane(static_cast<int>(shift_fma_ok(lse_r))) != 0;
+  b.form = fma ? (c.logit_scale == 1.f ? 1 : 2) : 0;
   b.lb = lse_r * kLog2e;
-  b.pf = (b.fma ? __builtin_amdgcn_exp2f(-shift_residual(lse_r, b.lb)) : 1.0f) *
+  b.pf = (fma ? __builtin_amdgcn_exp2f(-shift_residual(lse_r, b.lb)) : 1.0f) *
          (1.0f + c.two_lse_square_scale * lse_r);
   // (dl * logit_scale) is a Python-double product in the golden
   b.scale = static_cast<float>(static_cast<double>(dl) * c.logit_scale);
@@ -501,30 +772,37 @@ __global__ __launch_bounds__(kBwdLanes) void ce_bwd_tiles(
   if (j < nvec) {
     const int64_t rel = adj - head - static_cast<int64_t>(j) * V;  // label's place in r
     float o[V];
-    if (b.fma) {
+    if (b.form == 1) {
 #pragma unroll
-      for (int k = 0; k < V; ++k) o[k] = ce_grad<true>(raw_at<T, V>(r, k), rel == k, b, c);
+      for (int k = 0; k < V; ++k) o[k] = ce_grad<1>(raw_at<T, V>(r, k), rel == k, b, c);
+    } else if (b.form == 2) {
+#pragma unroll
+      for (int k = 0; k < V; ++k) o[k] = ce_grad<2>(raw_at<T, V>(r, k), rel == k, b, c);
     } else {
 #pragma unroll
-      for (int k = 0; k < V; ++k) o[k] = ce_grad<false>(raw_at<T, V>(r, k), rel == k, b, c);
+      for (int k = 0; k < V; ++k) o[k] = ce_grad<0>(raw_at<T, V>(r, k), rel == k, b, c);
     }
     out.template store<V>(dr + static_cast<int64_t>(j) * V, static_cast<int>(threadIdx.x) * V, o,
                           sd);
   }
   if (MIS && tix == 0) {
     const int t = static_cast<int>(threadIdx.x);
+    auto grad = [&](float v, bool is_label) {
+      return b.form == 1   ? ce_grad<1>(v, is_label, b, c)
+             : b.form == 2 ? ce_grad<2>(v, is_label, b, c)
+                           : ce_grad<0>(v, is_label, b, c);
+    };
     if (t < head) {
       float v;
       load_f32<T, 1>(logits + in0 + t, &v, sx);
-      const float o = b.fma ? ce_grad<true>(v, adj == t, b, c) : ce_grad<false>(v, adj == t, b, c);
+      const float o = grad(v, adj == t);
       store_from_f32<T, 1>(dr - head + t, &o, sd);
     }
     if (t < tail) {
       const int64_t k = static_cast<int64_t>(nvec) * V + t;
       float v;
       load_f32<T, 1>(lr + k, &v, sx);
-      const float o = b.fma ? ce_grad<true>(v, adj == head + k, b, c)
-                            : ce_grad<false>(v, adj == head + k, b, c);
+      const float o = grad(v, adj == head + k);
       store_from_f32<T, 1>(dr + k, &o, sd);
     }
   }
@@ -577,6 +855,46 @@ hipError_t launch_cross_entropy_fwd(const CeArgs& a, const Geometry& g, hipStrea
     if (g.v == 1) go(std::integral_constant<int, 1>{});
     else go(std::integral_constant<int, VN>{});
   });
+  return err;
+}
+
+bool cross_entropy_fwd_persist_fits(int logits_dtype, int64_t n_cols) {
+  return logits_dtype == kF32 && n_cols % 4 == 0 && n_cols / 4 >= kCePersistChunk &&
+         n_cols * 4 < (int64_t(1) << 30);
+}
+
+int64_t cross_entropy_fwd_persist_chunk_cols() { return int64_t(kCePersistChunk) * 4; }
+
+hipError_t launch_cross_entropy_fwd_persist(const CeArgs& a, int64_t max_grid, hipStream_t s) {
+  if (!cross_entropy_fwd_persist_fits(a.logits_dt, a.n_cols) || a.ncb != 1 || a.pair_out ||
+      a.empty_neg_inf)
+    return hipErrorInvalidValue;
+  const CeScalars c =
+      make_scalars(a.smoothing, a.logit_scale, a.lse_square_scale, a.total_classes,
+                   a.ignored_index, a.class_start, a.has_smoothing, a.split);
+  hipError_t err = hipErrorInvalidValue;
+  auto launch = [&](auto kern, auto labels) {
+    const int64_t cus = resident_blocks(reinterpret_cast<const void*>(kern), kCePersistLanes, 1);
+    int64_t grid = std::min<int64_t>(a.n_rows, std::max<int64_t>(cus, 1));
+    if (max_grid > 0) grid = std::min(grid, max_grid);
+    launch_kernel(kern, dim3(grid), dim3(kCePersistLanes), 0, s,
+                  static_cast<const float*>(a.logits), labels, a.loss, a.lse, a.z_loss, a.n_rows,
+                  a.n_cols, a.ld, c);
+    err = hipGetLastError();
+  };
+  auto pick = [&](auto lt) {
+    using LabelT = typename decltype(lt)::type;
+    const LabelT* labels = static_cast<const LabelT*>(a.labels);
+    if (c.logit_scale == 1.f) {
+      if (c.has_smoothing) launch(ce_fwd_persist<true, LabelT, true>, labels);
+      else launch(ce_fwd_persist<false, LabelT, true>, labels);
+    } else {
+      if (c.has_smoothing) launch(ce_fwd_persist<true, LabelT, false>, labels);
+      else launch(ce_fwd_persist<false, LabelT, false>, labels);
+    }
+  };
+  if (a.label_i64) pick(TypeTag<int64_t>{});
+  else pick(TypeTag<int32_t>{});
   return err;
 }
 

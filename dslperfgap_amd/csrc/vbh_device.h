@@ -441,6 +441,16 @@ __device__ __forceinline__ Moments group_allreduce_moments(Moments m, int tpr, f
   return r;
 }
 
+// x * y rounded to fp32 by itself, never fused with a following add or
+// subtract into one FMA.  exp(x * scale - m) where m is the rounded product of
+// the row's max needs it: fused, x * scale - m is the product's rounding error
+// for the max element itself, up to half an ulp of the product (1e31 at 2e38),
+// not 0.
+__device__ __forceinline__ float mul_rn(float x, float y) {
+#pragma clang fp contract(off)
+  return x * y;
+}
+
 // Fast exp / log on the hardware transcendental unit (v_exp_f32 / v_log_f32,
 // 1 ulp in the base-2 domain).  exp(x) = 2^(x * log2 e); log(x) = log2(x) * ln 2.
 __device__ __forceinline__ float fast_exp(float x) {

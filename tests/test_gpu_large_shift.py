@@ -111,7 +111,11 @@ CE_ARGS = [dict(smoothing=0.0, logit_scale=1.0, lse_square_scale=0.0, HAS_SMOOTH
            dict(smoothing=0.0, logit_scale=0.5, lse_square_scale=0.0, HAS_SMOOTHING=False,
                 SPLIT=False),
            dict(smoothing=0.0, logit_scale=1.0, lse_square_scale=0.0, HAS_SMOOTHING=False,
-                SPLIT=True)]
+                SPLIT=True),
+           # a scale whose products round (0.5 is exact): x * scale - m must
+           # subtract the rounded product, not fuse into one FMA
+           dict(smoothing=0.0, logit_scale=0.7, lse_square_scale=0.0, HAS_SMOOTHING=False,
+                SPLIT=False)]
 
 
 @pytest.mark.parametrize("cols", WIDTHS)
