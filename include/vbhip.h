@@ -274,7 +274,10 @@ int64_t vbh_stream_read_partial_bytes(int64_t bytes);
  * heuristic, block = 0 its workgroup size, flags = 0 its kernel choice.
  * Process-wide setting.
  * Replaces: the import-time config injection of ViperBench/tuning/cache.py:31-36. */
-#define VBH_TUNE_PERSIST 1      /* force the persistent pipelined row kernel    */
+#define VBH_TUNE_PERSIST 1      /* force the persistent pipelined row kernel
+                                   (cross entropy: the persistent forward for
+                                   fp32 rows of one column block of at least
+                                   8192 columns)                             */
 #define VBH_TUNE_NO_PERSIST 2   /* force one row group per workgroup            */
 #define VBH_TUNE_NONTEMPORAL 4  /* force nontemporal row loads / output stores  */
 #define VBH_TUNE_TEMPORAL 8     /* force plain row loads / output stores        */

@@ -82,8 +82,8 @@ CONFIG_SYMBOLS = {
                   "false>(float const*, float*, long, int, int)",
     "C3_logsumexp": "void vbh::(anonymous namespace)::logsumexp_rows<float, float, 4, 8, true, "
                     "false>(float const*, float*, long, int, int, int, int)",
-    "C4_cross_entropy": "void vbh::(anonymous namespace)::ce_fwd_rows<float, 4, 8, true, false, false>"
-                        "(float const*, void const*, int, float*, float*, float*)",
+    "C4_cross_entropy": "void vbh::(anonymous namespace)::ce_fwd_persist<false, long, true>"
+                        "(float const*, long const*, float*, float*, float*, long, int, long)",
     "C4_cross_entropy_bwd": "void vbh::(anonymous namespace)::ce_bwd_tiles<float, 4, 2, false>"
                             "(float const*, float const*, float const*)",
     "C5_layer_norm": "_ZN3vbh12_GLOBAL__N_115layer_norm_pipeIDF16bDF16bLi8ELi4ELi2ELb1EEEvPKT_"
@@ -172,8 +172,8 @@ def test_bench_reads_traffic_of_every_config_from_the_committed_summary():
 # ---------------------------------------------------------------------------
 # timed mode: dispatches inside bench.py's roctx range only
 # ---------------------------------------------------------------------------
-CE = ("void vbh::(anonymous namespace)::ce_fwd_rows<float, 4, 8, true, false, false>"
-      "(float const*, void const*, int, float*, float*, float*)")
+CE = ("void vbh::(anonymous namespace)::ce_fwd_persist<false, long, true>"
+      "(float const*, long const*, float*, float*, float*, long, int, long)")
 
 
 def _timed_fixture(tmp_path, steps=4):
@@ -215,7 +215,7 @@ def test_timed_summary_counts_only_the_timed_dispatches(tmp_path):
     kt, mk, bl, span = _timed_fixture(tmp_path)
     combined, per = rs.render_timed(kt, mk, bl)
     (name, txt), = per.values()
-    assert name == "ce_fwd_rows_C4_cross_entropy_timed_trace.txt"
+    assert name == "ce_fwd_persist_C4_cross_entropy_timed_trace.txt"
     row = rs.timed_row(rs.read_dispatches(kt), rs.read_ranges(mk)[0],
                        WORKLOADS["C4_cross_entropy"].bytes_per_launch)
     assert row["calls"] == 4 and row["others"] == 1
@@ -249,7 +249,7 @@ def test_counter_tail_keeps_the_last_dispatches(tmp_path):
 
 
 def test_kernel_base_names():
-    assert rs.kernel_base(CE) == "ce_fwd_rows"
+    assert rs.kernel_base(CE) == "ce_fwd_persist"
     assert rs.kernel_base(C2) == "rms_norm_rows"
     assert rs.kernel_base(COPYK) == "copy_kernel"
     assert rs.kernel_base(CONFIG_SYMBOLS["C5_layer_norm"]) == "layer_norm_pipe"
