@@ -228,7 +228,7 @@ bool write_through_ok(int64_t out_bytes, int64_t units) {
 // Default launches of the persistent cross-entropy forward (ce_fwd_persist):
 // at least this many rows, of at least this many of its chunks.
 constexpr int64_t kCePersistMinRows = 1024;
-constexpr int64_t kCePersistMinChunks = 3;
+constexpr int64_t kCePersistMinChunks = 2;
 constexpr int64_t kSplitMaxRows = 256;      // split launches of fewer rows ...
 constexpr int64_t kSplitRowVecs = 16384;    // ... of 16-byte vectors per row, at least
 constexpr int64_t kSplitMaxRowsLong = 512;  // two-round launches (logsumexp, CE) ...

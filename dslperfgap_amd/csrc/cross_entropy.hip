@@ -378,13 +378,16 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_stream(
 // b, b + G, b + 2G, ... (G the grid) in chunks of kCePersistLanes x
 // kCePersistVecs 16-byte vectors (32 KiB), the next chunk's loads in flight
 // while the current one is folded.  All workgroups move through the logits
-// together; ce_fwd_rows (one row per 1024-lane workgroup) leaves a CU's loads
-// idle while a finished workgroup reduces its row and the next one starts.
-// MI355X, fp32 32000 columns, against ce_fwd_rows on the same box: 1024 rows
-// +9%, 2048 +5%, 8192 (C4) +0.9%, 16384 +-0; rows of one chunk or less lose
-// (8192 x 8192: -14%), hence the launcher's default of at least 3 chunks per
-// row.  Chunks of 16 KiB with two or three in flight, 8 KiB with three or four
-// and three of 32 KiB all measured slower at C4 (-0.1 to -20%).
+// together, the waves of a workgroup in step (a barrier after every chunk);
+// ce_fwd_rows (one row per 1024-lane workgroup) leaves a CU's loads idle
+// while a finished workgroup reduces its row and the next one starts.
+// MI355X, fp32, against ce_fwd_rows on the same box: 32000 columns, 1024 rows
+// +14%, 2048 +7%, 4096 +4%, 8192 (C4) +2.2%, 16384 +0.8%; 1024 x 50304 +32%,
+// 2048 x 65536 +25%, 8192 x 16384 (two chunks per row) +2.4%; rows of one
+// chunk lose (8192 x 8192: -12%), hence the launcher's default of at least
+// two chunks per row.  Chunks of 16 KiB with two or three in flight, 8 KiB
+// with three or four and three of 32 KiB all measured slower at C4 (-0.1 to
+// -20%).
 //
 // Each lane folds its share of a row into an online pair: m, the max of its
 // scaled logits (NaN if any is NaN), and s, the sum of exp(x - m) over its
@@ -397,8 +400,9 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_stream(
 // in the FMA form), and the workgroup merges them as the second stage of a
 // split row merges segments: M = max m, S = sum t * exp(m - M) over the lanes
 // with m > -inf; a NaN anywhere, an infinite M or an all -inf row give the
-// golden's NaN lse (pytorch_impl.py:37-47).  Lanes 0, 1 and 2 then store the
-// row's loss, lse and z_loss.  The label comes from a scalar
+// golden's NaN lse (pytorch_impl.py:37-47): each wave merges its lanes' pairs,
+// and wave 0 the waves' pairs, one per lane of a group of 8.  Lanes 0, 1 and 2
+// then store the row's loss, lse and z_loss.  The label comes from a scalar
 // load one row ahead, its logit from a scalar load at the row's first chunk.
 // Buffer loads with a range of one row: vectors past its end (the last
 // chunk's spare lanes, the loads past a workgroup's last row) read nothing.
@@ -549,11 +553,15 @@ __global__ __launch_bounds__(kCePersistLanes) void ce_fwd_persist(
     }
     if (fc == cpr - 1) fold_values(ch, std::true_type{});
     else fold_values(ch, std::false_type{});
+    // the waves issue each chunk's loads together: a barrier after every
+    // chunk (the row's last one has the merge's) kept them in step, +1% at C4
+    // on MI355X against a barrier per row only
+    if (fc != cpr - 1) __syncthreads();
     if (fc == cpr - 1) {
       // each wave merges its lanes' pairs into one (a NaN max or sum
       // propagates into it), one LDS exchange and one barrier per row, and
-      // lanes 0-2 merge the waves' pairs: reads of row k's slots end before
-      // the barrier of row k + 1, writes of row k + 2 come after it
+      // wave 0 merges the waves' pairs: reads of row k's slots end before the
+      // barrier of row k + 1, writes of row k + 2 come after it
       const float wm = wave_allreduce<Max>(m, kWave);
       // this lane's SegPair sum, relative to e^m
       const float t = shift_fma_ok(m) ? s * __builtin_amdgcn_exp2f(-shift_residual(m, nb)) : s;
@@ -566,22 +574,16 @@ __global__ __launch_bounds__(kCePersistLanes) void ce_fwd_persist(
         if constexpr (SL) lds_pair[parity][2][wave] = wl;
       }
       __syncthreads();
-      if (lane < 3) {
-        float mx = lds_pair[parity][0][0];
-        bool nan = false;
-#pragma unroll
-        for (int w = 0; w < W; ++w) {
-          const float mw = lds_pair[parity][0][w], sw = lds_pair[parity][1][w];
-          mx = max_nan(mx, mw);
-          nan = nan || mw != mw || sw != sw;
-        }
-        float sum = 0.f, sum_logits = 0.f;
-#pragma unroll
-        for (int w = 0; w < W; ++w) {
-          const float mw = lds_pair[parity][0][w];
-          sum += mw != kNegInf ? lds_pair[parity][1][w] * fast_exp(mw - mx) : 0.f;
-          if constexpr (SL) sum_logits += lds_pair[parity][2][w];
-        }
+      if (wave == 0) {
+        // lane k of each group of 8 holds wave k's pair (W = 8): the merge
+        // in three DPP steps per reduction instead of a loop over the waves
+        static_assert(W == 8, "one wave pair per lane of a group of 8");
+        const int k = lane & (W - 1);
+        const float mw = lds_pair[parity][0][k], sw = lds_pair[parity][1][k];
+        const float mx = wave_allreduce<Max>(mw, W);
+        const bool nan = wave_allreduce<Max>(mw != mw || sw != sw ? 1.f : 0.f, W) > 0.f;
+        const float sum = wave_allreduce<Sum>(mw != kNegInf ? sw * fast_exp(mw - mx) : 0.f, W);
+        const float sum_logits = SL ? wave_allreduce<Sum>(lds_pair[parity][2][k], W) : 0.f;
         const float lse = nan || __builtin_isinf(mx) ? __builtin_nanf("") : fast_log(sum) + mx;
         const float logit_label = ONE ? logit_raw : mul_rn(logit_raw, scale);
         const CeOut o = ce_outputs(lse, sum_logits, in_row, logit_label, ignored, c);

@@ -1,7 +1,7 @@
 """GPU parity of the persistent cross-entropy forward (ce_fwd_persist).
 
-Launches of at least 1024 fp32 rows of one column block and at least three
-32 KiB chunks (24576 columns) take the persistent kernel by default: one
+Launches of at least 1024 fp32 rows of one column block and at least two
+32 KiB chunks (16384 columns) take the persistent kernel by default: one
 workgroup per CU folding its rows chunk by chunk into per-lane online (max,
 sum of exp) pairs; the tune flag TUNE_PERSIST takes it down to one chunk (8192
 columns) and any row count.  16-bit logits and column blocks stay on
@@ -89,6 +89,7 @@ def _inputs(rows, cols, dtype, seed, start, specials=True):
 
 
 @pytest.mark.parametrize("rows,cols,bs,dtype", [
+    (1024, 16384, 16384, torch.float32),   # two full chunks
     (1024, 24576, 24576, torch.float32),   # three full chunks
     (1030, 24580, 24580, torch.float32),   # four chunks, the last of one vector
     (1100, 32000, 32000, torch.float32),   # C4's row: four chunks, the last of 1856 vectors
