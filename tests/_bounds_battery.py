@@ -105,6 +105,17 @@ def run() -> dict:
             n = rows * -(-cols // bs)
             for i, t in enumerate(res):
                 out[f"ce {rows}x{cols} bs{bs} sm{sm} out{i}"] = t.reshape(-1)[:n].clone()
+    # the persistent forward (forced: a few rows, the last chunk of a row partly
+    # past its end, int32 labels, smoothing)
+    with _override(_lib.OP_CROSS_ENTROPY, _lib.TUNE_PERSIST):
+        rows, cols = 40, 20000
+        logits = _x(rows, cols, 17, scale=2.0)
+        labels = torch.randint(0, cols, (rows,), generator=_g(18)).to(torch.int32)
+        labels[3] = -100
+        res = cross_entropy_fwd(logits, labels.to(DEV), 0.1, 0.9, 0.01, -100, cols, 0, cols,
+                                True, False)
+        for i, t in enumerate(res):
+            out[f"ce persistent {rows}x{cols} out{i}"] = t.reshape(-1)[:rows].clone()
     for rows, cols, dt in ((48, 3000, torch.float32), (37, 1001, torch.float32),
                            (37, 4099, torch.bfloat16)):
         logits = _x(rows, cols, 12, dt)
