@@ -149,3 +149,26 @@ def test_persistent_cross_entropy_repeatable():
     b = cross_entropy_fwd(xd, ld, *args)
     for x, y in zip(a, b):
         assert torch.equal(x.reshape(-1)[:rows], y.reshape(-1)[:rows])
+
+
+@pytest.mark.parametrize("rows,cols,pad", [(1030, 16388, 4), (300, 8192, 12)])
+def test_persistent_cross_entropy_strided_rows(rows, cols, pad):
+    """Rows `pad` elements apart beyond their width (a column slice of a wider
+    buffer): the persistent kernel reads each row from its own stride; 300
+    rows forced with TUNE_PERSIST, 1030 by default."""
+    g = _g(950 + rows)
+    big = 2 * torch.randn(rows, cols + pad, generator=g)
+    logits = big[:, :cols]
+    labels = torch.randint(0, cols, (rows,), generator=g)
+    labels[7] = -100
+    args = (0.1, 1.0, 1e-4, -100, cols, 0, cols, True, False)
+    bd = big.to(DEV)
+    print(f"[ce persist] strided {rows}x{cols} pad {pad}", flush=True)
+    try:
+        if rows < 1024:
+            _lib.tune_override(_lib.OP_CROSS_ENTROPY, 0, 0, _lib.TUNE_PERSIST)
+        got = cross_entropy_fwd(bd[:, :cols], labels.to(DEV), *args)
+    finally:
+        _lib.tune_override(_lib.OP_CROSS_ENTROPY, 0, 0, 0)
+    want = ref.cross_entropy_fwd(logits, labels, *args)
+    _check(got, want, rows, f"strided {rows}x{cols} pad {pad}")
