@@ -1023,16 +1023,21 @@ int vbh_cross_entropy_fwd_ws(const void* logits, const void* labels, int logits_
   // the persistent forward (one workgroup per CU walking the rows chunk by
   // chunk): fp32 rows of one column block and at least one chunk; by default
   // in launches of at least kCePersistMinRows rows of kCePersistMinChunks
-  // chunks or more.  kFlagPersist lifts those two limits, kFlagNoPersist or a
-  // tpr / block override keeps ce_fwd_rows.
+  // chunks or more, its workgroup size the launcher's choice.  kFlagPersist
+  // lifts those two limits, and with it a block override of 256 or 512 sets
+  // the workgroup size; kFlagNoPersist, a tpr override or another block
+  // override keeps ce_fwd_rows.
   const int over = g_flags[VBH_OP_CROSS_ENTROPY].load();
+  const int ce_block = g_block[VBH_OP_CROSS_ENTROPY].load();
+  const bool ce_lanes_ok =
+      ce_block <= 0 || ((over & kFlagPersist) && (ce_block == 256 || ce_block == 512));
   if (vec_ok && ncb == 1 && cross_entropy_fwd_persist_fits(logits_dtype, n_cols) &&
-      g_tpr[VBH_OP_CROSS_ENTROPY].load() <= 0 && g_block[VBH_OP_CROSS_ENTROPY].load() <= 0 &&
-      !(over & kFlagNoPersist) &&
+      g_tpr[VBH_OP_CROSS_ENTROPY].load() <= 0 && ce_lanes_ok && !(over & kFlagNoPersist) &&
       ((over & kFlagPersist) ||
        (n_rows >= kCePersistMinRows &&
         n_cols >= kCePersistMinChunks * cross_entropy_fwd_persist_chunk_cols())))
-    return hip_status(launch_cross_entropy_fwd_persist(a, 0, s), "cross_entropy_fwd launch");
+    return hip_status(launch_cross_entropy_fwd_persist(a, 0, ce_block > 0 ? ce_block : 0, s),
+                      "cross_entropy_fwd launch");
   const bool mis_ok = !vec_ok && aligned16(logits) && bs >= kMisMinVecs * vn;
   Geometry g = geometry_for(VBH_OP_CROSS_ENTROPY, bs, vec_ok || mis_ok ? vn : 1, segments, 0,
                             ncb > 1);

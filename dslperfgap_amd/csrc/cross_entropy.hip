@@ -374,20 +374,26 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_stream(
 }
 
 // Persistent forward for fp32 rows of one column block (the whole row is the
-// segment): a grid of one 512-lane workgroup per CU, workgroup b taking rows
-// b, b + G, b + 2G, ... (G the grid) in chunks of kCePersistLanes x
-// kCePersistVecs 16-byte vectors (32 KiB), the next chunk's loads in flight
-// while the current one is folded.  All workgroups move through the logits
-// together, the waves of a workgroup in step (a barrier after every chunk);
-// ce_fwd_rows (one row per 1024-lane workgroup) leaves a CU's loads idle
-// while a finished workgroup reduces its row and the next one starts.
-// MI355X, fp32, against ce_fwd_rows on the same box: 32000 columns, 1024 rows
-// +14%, 2048 +7%, 4096 +4%, 8192 (C4) +2.2%, 16384 +0.8%; 1024 x 50304 +32%,
-// 2048 x 65536 +25%, 8192 x 16384 (two chunks per row) +2.4%; rows of one
-// chunk lose (8192 x 8192: -12%), hence the launcher's default of at least
-// two chunks per row.  Chunks of 16 KiB with two or three in flight, 8 KiB
-// with three or four and three of 32 KiB all measured slower at C4 (-0.1 to
-// -20%).
+// segment): a grid of one workgroup per CU, workgroup b taking rows b, b + G,
+// b + 2G, ... (G the grid) in chunks of kCePersistChunk 16-byte vectors (32
+// KiB), the next chunk's loads in flight while the current one is folded.  All
+// workgroups move through the logits together, the waves of a workgroup in
+// step (a barrier after every chunk); ce_fwd_rows (one row per 1024-lane
+// workgroup) leaves a CU's loads idle while a finished workgroup reduces its
+// row and the next one starts.  MI355X, fp32, 512-lane workgroups against
+// ce_fwd_rows on the same box: 32000 columns, 1024 rows +14%, 2048 +7%, 4096
+// +4%, 8192 (C4) +2.2%, 16384 +0.8%; 1024 x 50304 +32%, 2048 x 65536 +25%,
+// 8192 x 16384 (two chunks per row) +2.4%; rows of one chunk lose (8192 x
+// 8192: -12%), hence the launcher's default of at least two chunks per row.
+// Chunks of 16 KiB with two or three in flight, 8 KiB with three or four and
+// three of 32 KiB all measured slower at C4 (-0.1 to -20%).  256-lane
+// workgroups (8 vectors per lane per chunk) stream faster and start and drain
+// slower: against 512 lanes, 64 chunks per CU or more +1.0 to +2.3% (C4
+// +1.0%, 16384 x 32000 +1.5%, 8192 x 16384 and 2048 x 65536 +2.2%), 48 or
+// fewer -1.1 to -2.8% (4096 x 24576, 2048 x 32000, 1024 x 50304, 1024 x
+// 32000), so the launcher takes 256 lanes from 64 chunks per CU up.  1024
+// lanes x 2 vectors -0.9%, 128 x 16 -10%, global instead of buffer loads
+// +-0.5% (C4).
 //
 // Each lane folds its share of a row into an online pair: m, the max of its
 // scaled logits (NaN if any is NaN), and s, the sum of exp(x - m) over its
@@ -401,32 +407,34 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_stream(
 // split row merges segments: M = max m, S = sum t * exp(m - M) over the lanes
 // with m > -inf; a NaN anywhere, an infinite M or an all -inf row give the
 // golden's NaN lse (pytorch_impl.py:37-47): each wave merges its lanes' pairs,
-// and wave 0 the waves' pairs, one per lane of a group of 8.  Lanes 0, 1 and 2
+// and wave 0 the waves' pairs, one per lane of a group of W.  Lanes 0, 1 and 2
 // then store the row's loss, lse and z_loss.  The label comes from a scalar
 // load one row ahead, its logit from a scalar load at the row's first chunk.
 // Buffer loads with a range of one row: vectors past its end (the last
 // chunk's spare lanes, the loads past a workgroup's last row) read nothing.
-constexpr int kCePersistLanes = 512;
-constexpr int kCePersistVecs = 4;
-constexpr int kCePersistChunk = kCePersistLanes * kCePersistVecs;  // vectors
-constexpr int kCePersistBufs = 2;  // chunks in rotation (loads NB - 1 ahead)
+constexpr int kCePersistChunk = 2048;  // 16-byte vectors per chunk (32 KiB)
+constexpr int kCePersistBufs = 2;      // chunks in rotation (loads NB - 1 ahead)
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+template <int U>
 struct CeChunk {
-  f32x4 v[kCePersistVecs];
+  f32x4 v[U];
 };
 
 // SL: the row's sum of scaled logits is needed (smoothing); ONE: logit_scale
 // is 1 (else each logit's product with it is rounded once, as the golden
-// rounds it, and used for the max, the exps and the sum).
-template <bool SL, typename LabelT, bool ONE>
-__global__ __launch_bounds__(kCePersistLanes) void ce_fwd_persist(
+// rounds it, and used for the max, the exps and the sum).  L: lanes per
+// workgroup (256 or 512), each loading kCePersistChunk / L vectors per chunk.
+template <bool SL, typename LabelT, bool ONE, int L>
+__global__ __launch_bounds__(L) void ce_fwd_persist(
     const float* __restrict__ logits, const LabelT* __restrict__ labels,
     float* __restrict__ loss, float* __restrict__ lse_out, float* __restrict__ z_out,
     int64_t n_rows, int n_cols, int64_t ld, CeScalars c) {
-  constexpr int L = kCePersistLanes, U = kCePersistVecs, CH = kCePersistChunk;
+  constexpr int CH = kCePersistChunk, U = CH / L;
   constexpr int W = L / kWave;
+  static_assert(U * L == CH && (W & (W - 1)) == 0 && W <= kWave, "a chunk's shape");
+  using Chunk = CeChunk<U>;
   // per wave, by row parity: the wave's max, its sum of t * exp(m - max) and
   // its sum of logits
   __shared__ float lds_pair[2][3][W];
@@ -448,7 +456,7 @@ __global__ __launch_bounds__(kCePersistLanes) void ce_fwd_persist(
   int64_t lrow = b;
   int lc = 0;
   // (every lambda is inlined: a call would put the captured cursors in memory)
-  auto load = [&](CeChunk& ch, bool real) __attribute__((always_inline)) {
+  auto load = [&](Chunk& ch, bool real) __attribute__((always_inline)) {
     const float* base = logits + (real ? lrow * ld : 0);
     const bool ok = real && VBH_IN_SPAN(sx, base, static_cast<int64_t>(nvec) * 16);
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
@@ -474,7 +482,7 @@ __global__ __launch_bounds__(kCePersistLanes) void ce_fwd_persist(
   int parity = 0;  // of the fold's row: its LDS slots
   float logit_raw = 0.f;  // the label's logit, scaled where used (at the row's end)
 
-  auto fold_values = [&](const CeChunk& ch, auto mask) __attribute__((always_inline)) {
+  auto fold_values = [&](const Chunk& ch, auto mask) __attribute__((always_inline)) {
     constexpr bool MASK = decltype(mask)::value;
     const int c0 = fc * CH;
     float xv[U][4];
@@ -539,7 +547,7 @@ __global__ __launch_bounds__(kCePersistLanes) void ce_fwd_persist(
     for (int u = 0; u < U; ++u) asm volatile("" ::"v"(ch.v[u]));
   };
 
-  auto fold = [&](const CeChunk& ch) __attribute__((always_inline)) {
+  auto fold = [&](const Chunk& ch) __attribute__((always_inline)) {
     if (fc == 0) {  // a new row: its label facts and logit, the next row's label
       const int64_t label = static_cast<int64_t>(label_next);
       ignored = label == c.ignored_index;
@@ -575,9 +583,8 @@ __global__ __launch_bounds__(kCePersistLanes) void ce_fwd_persist(
       }
       __syncthreads();
       if (wave == 0) {
-        // lane k of each group of 8 holds wave k's pair (W = 8): the merge
-        // in three DPP steps per reduction instead of a loop over the waves
-        static_assert(W == 8, "one wave pair per lane of a group of 8");
+        // lane k of each group of W holds wave k's pair: the merge in
+        // log2(W) DPP steps per reduction instead of a loop over the waves
         const int k = lane & (W - 1);
         const float mw = lds_pair[parity][0][k], sw = lds_pair[parity][1][k];
         const float mx = wave_allreduce<Max>(mw, W);
@@ -605,7 +612,7 @@ __global__ __launch_bounds__(kCePersistLanes) void ce_fwd_persist(
   };
 
   constexpr int NB = kCePersistBufs;
-  CeChunk buf[NB];
+  Chunk buf[NB];
 #pragma unroll
   for (int i = 0; i < NB - 1; ++i) load(buf[i], i < chunks);
   const int64_t rounds = chunks / NB;
@@ -867,36 +874,51 @@ bool cross_entropy_fwd_persist_fits(int logits_dtype, int64_t n_cols) {
 
 int64_t cross_entropy_fwd_persist_chunk_cols() { return int64_t(kCePersistChunk) * 4; }
 
-hipError_t launch_cross_entropy_fwd_persist(const CeArgs& a, int64_t max_grid, hipStream_t s) {
+// Chunks per CU from which the launcher's default takes 256-lane workgroups
+// (measured on MI355X; see ce_fwd_persist).
+constexpr int64_t kCePersistWideChunksPerCu = 64;
+
+hipError_t launch_cross_entropy_fwd_persist(const CeArgs& a, int64_t max_grid, int lanes,
+                                            hipStream_t s) {
   if (!cross_entropy_fwd_persist_fits(a.logits_dt, a.n_cols) || a.ncb != 1 || a.pair_out ||
-      a.empty_neg_inf)
+      a.empty_neg_inf || (lanes != 0 && lanes != 256 && lanes != 512))
     return hipErrorInvalidValue;
   const CeScalars c =
       make_scalars(a.smoothing, a.logit_scale, a.lse_square_scale, a.total_classes,
                    a.ignored_index, a.class_start, a.has_smoothing, a.split);
+  if (lanes == 0) {
+    const int64_t cpr = (a.n_cols / 4 + kCePersistChunk - 1) / kCePersistChunk;
+    const int64_t cus = resident_blocks(
+        reinterpret_cast<const void*>(ce_fwd_persist<false, int64_t, true, 256>), 256, 1);
+    lanes = a.n_rows * cpr >= kCePersistWideChunksPerCu * cus ? 256 : 512;
+  }
   hipError_t err = hipErrorInvalidValue;
-  auto launch = [&](auto kern, auto labels) {
-    const int64_t cus = resident_blocks(reinterpret_cast<const void*>(kern), kCePersistLanes, 1);
+  auto launch = [&](auto kern, auto labels, int block) {
+    const int64_t cus = resident_blocks(reinterpret_cast<const void*>(kern), block, 1);
     int64_t grid = std::min<int64_t>(a.n_rows, std::max<int64_t>(cus, 1));
     if (max_grid > 0) grid = std::min(grid, max_grid);
-    launch_kernel(kern, dim3(grid), dim3(kCePersistLanes), 0, s,
-                  static_cast<const float*>(a.logits), labels, a.loss, a.lse, a.z_loss, a.n_rows,
-                  a.n_cols, a.ld, c);
+    launch_kernel(kern, dim3(grid), dim3(block), 0, s, static_cast<const float*>(a.logits),
+                  labels, a.loss, a.lse, a.z_loss, a.n_rows, a.n_cols, a.ld, c);
     err = hipGetLastError();
   };
-  auto pick = [&](auto lt) {
+  auto pick = [&](auto lt, auto lc) {
     using LabelT = typename decltype(lt)::type;
+    constexpr int L = decltype(lc)::value;
     const LabelT* labels = static_cast<const LabelT*>(a.labels);
     if (c.logit_scale == 1.f) {
-      if (c.has_smoothing) launch(ce_fwd_persist<true, LabelT, true>, labels);
-      else launch(ce_fwd_persist<false, LabelT, true>, labels);
+      if (c.has_smoothing) launch(ce_fwd_persist<true, LabelT, true, L>, labels, L);
+      else launch(ce_fwd_persist<false, LabelT, true, L>, labels, L);
     } else {
-      if (c.has_smoothing) launch(ce_fwd_persist<true, LabelT, false>, labels);
-      else launch(ce_fwd_persist<false, LabelT, false>, labels);
+      if (c.has_smoothing) launch(ce_fwd_persist<true, LabelT, false, L>, labels, L);
+      else launch(ce_fwd_persist<false, LabelT, false, L>, labels, L);
     }
   };
-  if (a.label_i64) pick(TypeTag<int64_t>{});
-  else pick(TypeTag<int32_t>{});
+  auto by_labels = [&](auto lc) {
+    if (a.label_i64) pick(TypeTag<int64_t>{}, lc);
+    else pick(TypeTag<int32_t>{}, lc);
+  };
+  if (lanes == 256) by_labels(std::integral_constant<int, 256>{});
+  else by_labels(std::integral_constant<int, 512>{});
   return err;
 }
 

@@ -234,10 +234,12 @@ hipError_t launch_cross_entropy_fwd(const CeArgs& a, const Geometry& g, hipStrea
 // column block per row) hold at least one chunk of
 // cross_entropy_fwd_persist_chunk_cols() columns, under 1 GiB, in
 // 16-byte-aligned rows.  Its grid is one workgroup per CU, at most `max_grid`
-// (0: no limit).
+// (0: no limit), of `lanes` lanes: 256 or 512, or 0 for the launcher's choice
+// by the launch's chunks per CU.
 bool cross_entropy_fwd_persist_fits(int logits_dtype, int64_t n_cols);
 int64_t cross_entropy_fwd_persist_chunk_cols();
-hipError_t launch_cross_entropy_fwd_persist(const CeArgs& a, int64_t max_grid, hipStream_t s);
+hipError_t launch_cross_entropy_fwd_persist(const CeArgs& a, int64_t max_grid, int lanes,
+                                            hipStream_t s);
 // Second stage of a split row: `a` describes the caller's launch (one column
 // block per row); seg_loss / seg_lse hold the first stage's `segs` segments
 // per row at flat index k * n_rows + row.

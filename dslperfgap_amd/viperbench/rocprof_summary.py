@@ -70,7 +70,7 @@ CONFIG_KERNELS = [
     ("C3_softmax", r"softmax_rows<float, float, 4, 2, false, \d(, false)?>"),
     ("C3_logsumexp", r"logsumexp_rows<float, float, 4, 8, true(, false){0,2}>|"
                      r"logsumexp_rowsIffLi4ELi8ELb1E(Lb0E){0,2}E"),
-    ("C4_cross_entropy", r"ce_fwd_persist<false, long, true>|ce_fwd_persistILb0ElLb1EE"),
+    ("C4_cross_entropy", r"ce_fwd_persist<false, long, true, 256>|ce_fwd_persistILb0ElLb1ELi256EE"),
     ("C4_cross_entropy_bwd", r"ce_bwd_tiles<float, 4, \d(, false)?>|ce_bwd_tilesIfLi4ELi\dE"),
     ("C5_layer_norm", r"layer_norm_pipeIDF16bDF16bLi8ELi4ELi\dELb1E"),
     (COPY, r"copy_kernel\("),

@@ -277,7 +277,8 @@ int64_t vbh_stream_read_partial_bytes(int64_t bytes);
 #define VBH_TUNE_PERSIST 1      /* force the persistent pipelined row kernel
                                    (cross entropy: the persistent forward for
                                    fp32 rows of one column block of at least
-                                   8192 columns)                             */
+                                   8192 columns; a block of 256 or 512 with
+                                   it sets that kernel's workgroup size)     */
 #define VBH_TUNE_NO_PERSIST 2   /* force one row group per workgroup            */
 #define VBH_TUNE_NONTEMPORAL 4  /* force nontemporal row loads / output stores  */
 #define VBH_TUNE_TEMPORAL 8     /* force plain row loads / output stores        */

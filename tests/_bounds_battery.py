@@ -43,10 +43,10 @@ def _x(rows, cols, seed, dtype=torch.float32, scale=1.0):
     return (scale * torch.randn(rows, cols, generator=_g(seed))).to(dtype).to(DEV)
 
 
-def _override(op, flags):
+def _override(op, flags, block=0):
     class _Ctx:
         def __enter__(self):
-            _lib.tune_override(op, 0, 0, flags)
+            _lib.tune_override(op, 0, block, flags)
 
         def __exit__(self, *exc):
             _lib.tune_override(op, 0, 0, 0)
@@ -106,16 +106,17 @@ def run() -> dict:
             for i, t in enumerate(res):
                 out[f"ce {rows}x{cols} bs{bs} sm{sm} out{i}"] = t.reshape(-1)[:n].clone()
     # the persistent forward (forced: a few rows, the last chunk of a row partly
-    # past its end, int32 labels, smoothing)
-    with _override(_lib.OP_CROSS_ENTROPY, _lib.TUNE_PERSIST):
-        rows, cols = 40, 20000
-        logits = _x(rows, cols, 17, scale=2.0)
-        labels = torch.randint(0, cols, (rows,), generator=_g(18)).to(torch.int32)
-        labels[3] = -100
-        res = cross_entropy_fwd(logits, labels.to(DEV), 0.1, 0.9, 0.01, -100, cols, 0, cols,
-                                True, False)
+    # past its end, int32 labels, smoothing; workgroups of 256 and 512 lanes)
+    rows, cols = 40, 20000
+    logits = _x(rows, cols, 17, scale=2.0)
+    labels = torch.randint(0, cols, (rows,), generator=_g(18)).to(torch.int32)
+    labels[3] = -100
+    for lanes in (256, 512):
+        with _override(_lib.OP_CROSS_ENTROPY, _lib.TUNE_PERSIST, lanes):
+            res = cross_entropy_fwd(logits, labels.to(DEV), 0.1, 0.9, 0.01, -100, cols, 0, cols,
+                                    True, False)
         for i, t in enumerate(res):
-            out[f"ce persistent {rows}x{cols} out{i}"] = t.reshape(-1)[:rows].clone()
+            out[f"ce persistent {rows}x{cols} {lanes} lanes out{i}"] = t.reshape(-1)[:rows].clone()
     for rows, cols, dt in ((48, 3000, torch.float32), (37, 1001, torch.float32),
                            (37, 4099, torch.bfloat16)):
         logits = _x(rows, cols, 12, dt)

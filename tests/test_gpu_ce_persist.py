@@ -3,8 +3,11 @@
 Launches of at least 1024 fp32 rows of one column block and at least two
 32 KiB chunks (16384 columns) take the persistent kernel by default: one
 workgroup per CU folding its rows chunk by chunk into per-lane online (max,
-sum of exp) pairs; the tune flag TUNE_PERSIST takes it down to one chunk (8192
-columns) and any row count.  16-bit logits and column blocks stay on
+sum of exp) pairs, in workgroups of 256 lanes from 64 chunks per CU up and of
+512 below; the tune flag TUNE_PERSIST takes it down to one chunk (8192
+columns) and any row count, and with a block override of 256 or 512 sets the
+workgroup size (both are run on every case here).  16-bit logits and column
+blocks stay on
 ce_fwd_rows (cases below as well).  These tests hold it to the oracle (the restated
 golden, oracle/pytorch_impl.py) at the strict fp32 tolerance of the measured
 configs, on every output, with the golden's special values (NaN, +inf, all
@@ -60,6 +63,24 @@ def _check(got, want, n, what, split=False):
                                              for i in idx))
 
 
+# (flags, block) of vbh_tune_override for the persistent kernel's launches:
+# the default choice, then each workgroup size forced
+SHAPES = [(0, 0), (_lib.TUNE_PERSIST, 256), (_lib.TUNE_PERSIST, 512)]
+
+
+def _run_shapes(fn, what):
+    """fn() under each of SHAPES; returns the outputs' valid rows per shape."""
+    outs = []
+    try:
+        for flags, block in SHAPES:
+            _lib.tune_override(_lib.OP_CROSS_ENTROPY, 0, block, flags)
+            print(f"[ce persist] {what} flags={flags} block={block}", flush=True)
+            outs.append(fn(f"{what} flags={flags} block={block}"))
+    finally:
+        _lib.tune_override(_lib.OP_CROSS_ENTROPY, 0, 0, 0)
+    return outs
+
+
 def _inputs(rows, cols, dtype, seed, start, specials=True):
     g = _g(seed)
     logits = 2 * torch.randn(rows, cols, generator=g)
@@ -105,11 +126,20 @@ def test_persistent_cross_entropy_matches_oracle(rows, cols, bs, dtype, pi, ldt)
     labels = labels.to(ldt)
     args = dict(ignored_index=-100, total_classes=cols + start, class_start_idx=start,
                 BLOCK_SIZE=bs, **p)
-    print(f"[ce persist] {rows}x{cols} bs={bs} {dtype} {ldt} params {pi}", flush=True)
-    got = cross_entropy_fwd(logits.to(DEV), labels.to(DEV), **args)
     want = ref.cross_entropy_fwd(logits, labels, **args)
     n = rows * (cols // bs)
-    _check(got, want, n, f"{rows}x{cols} bs={bs} {dtype} {ldt} {p}", p["SPLIT"])
+    xd, ld = logits.to(DEV), labels.to(DEV)
+
+    def run(what):
+        got = cross_entropy_fwd(xd, ld, **args)
+        _check(got, want, n, what, p["SPLIT"])
+
+    tag = f"{rows}x{cols} bs={bs} {dtype} {ldt} params {pi}"
+    if dtype == torch.float32 and bs == cols:
+        _run_shapes(run, tag)
+    else:
+        print(f"[ce persist] {tag}", flush=True)
+        run(tag)
 
 
 @pytest.mark.parametrize("rows", [1, 3, 12, 257, 300])
@@ -126,36 +156,45 @@ def test_persistent_cross_entropy_forced_few_segments(rows, cols, dtype):
     want = ref.cross_entropy_fwd(logits, labels, **args)
     outs = []
     try:
-        for flags in (_lib.TUNE_PERSIST, _lib.TUNE_NO_PERSIST):
-            _lib.tune_override(_lib.OP_CROSS_ENTROPY, 0, 0, flags)
-            print(f"[ce persist] forced rows={rows} cols={cols} {dtype} flags={flags}", flush=True)
+        for flags, block in ((_lib.TUNE_PERSIST, 256), (_lib.TUNE_PERSIST, 512),
+                             (_lib.TUNE_NO_PERSIST, 0)):
+            _lib.tune_override(_lib.OP_CROSS_ENTROPY, 0, block, flags)
+            what = f"rows={rows} cols={cols} {dtype} flags={flags} block={block}"
+            print(f"[ce persist] forced {what}", flush=True)
             got = cross_entropy_fwd(logits.to(DEV), labels.to(DEV), **args)
-            _check(got, want, rows, f"rows={rows} cols={cols} {dtype} flags={flags}")
+            _check(got, want, rows, what)
             outs.append([t.reshape(-1)[:rows].cpu() for t in got])
     finally:
         _lib.tune_override(_lib.OP_CROSS_ENTROPY, 0, 0, 0)
-    for a, b in zip(*outs):
-        assert torch.allclose(a, b, atol=1e-5, rtol=1e-5, equal_nan=True), (a - b).abs().max()
+    for other in outs[1:]:
+        for a, b in zip(outs[0], other):
+            assert torch.allclose(a, b, atol=1e-5, rtol=1e-5, equal_nan=True), \
+                (a - b).abs().max()
 
 
 def test_persistent_cross_entropy_repeatable():
     """Two launches on the same inputs give bit-identical outputs (each
-    segment's fold order is fixed by the grid, not by timing)."""
+    segment's fold order is fixed by the grid, not by timing), for the
+    default and each forced workgroup size."""
     rows, cols = 2048, 24576
     logits, labels = _inputs(rows, cols, torch.float32, 900, 0, specials=False)
     xd, ld = logits.to(DEV), labels.to(DEV)
     args = (0.1, 1.0, 1e-4, -100, cols, 0, cols, True, False)
-    a = [t.clone() for t in cross_entropy_fwd(xd, ld, *args)]
-    b = cross_entropy_fwd(xd, ld, *args)
-    for x, y in zip(a, b):
-        assert torch.equal(x.reshape(-1)[:rows], y.reshape(-1)[:rows])
+
+    def run(what):
+        a = [t.clone() for t in cross_entropy_fwd(xd, ld, *args)]
+        b = cross_entropy_fwd(xd, ld, *args)
+        for x, y in zip(a, b):
+            assert torch.equal(x.reshape(-1)[:rows], y.reshape(-1)[:rows]), what
+
+    _run_shapes(run, f"repeat {rows}x{cols}")
 
 
 @pytest.mark.parametrize("rows,cols,pad", [(1030, 16388, 4), (300, 8192, 12)])
 def test_persistent_cross_entropy_strided_rows(rows, cols, pad):
     """Rows `pad` elements apart beyond their width (a column slice of a wider
     buffer): the persistent kernel reads each row from its own stride; 300
-    rows forced with TUNE_PERSIST, 1030 by default."""
+    rows forced with TUNE_PERSIST (256 lanes), 1030 by default."""
     g = _g(950 + rows)
     big = 2 * torch.randn(rows, cols + pad, generator=g)
     logits = big[:, :cols]
@@ -166,7 +205,7 @@ def test_persistent_cross_entropy_strided_rows(rows, cols, pad):
     print(f"[ce persist] strided {rows}x{cols} pad {pad}", flush=True)
     try:
         if rows < 1024:
-            _lib.tune_override(_lib.OP_CROSS_ENTROPY, 0, 0, _lib.TUNE_PERSIST)
+            _lib.tune_override(_lib.OP_CROSS_ENTROPY, 0, 256, _lib.TUNE_PERSIST)
         got = cross_entropy_fwd(bd[:, :cols], labels.to(DEV), *args)
     finally:
         _lib.tune_override(_lib.OP_CROSS_ENTROPY, 0, 0, 0)

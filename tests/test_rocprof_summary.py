@@ -82,7 +82,7 @@ CONFIG_SYMBOLS = {
                   "false>(float const*, float*, long, int, int)",
     "C3_logsumexp": "void vbh::(anonymous namespace)::logsumexp_rows<float, float, 4, 8, true, "
                     "false>(float const*, float*, long, int, int, int, int)",
-    "C4_cross_entropy": "void vbh::(anonymous namespace)::ce_fwd_persist<false, long, true>"
+    "C4_cross_entropy": "void vbh::(anonymous namespace)::ce_fwd_persist<false, long, true, 256>"
                         "(float const*, long const*, float*, float*, float*, long, int, long)",
     "C4_cross_entropy_bwd": "void vbh::(anonymous namespace)::ce_bwd_tiles<float, 4, 2, false>"
                             "(float const*, float const*, float const*)",
@@ -172,7 +172,7 @@ def test_bench_reads_traffic_of_every_config_from_the_committed_summary():
 # ---------------------------------------------------------------------------
 # timed mode: dispatches inside bench.py's roctx range only
 # ---------------------------------------------------------------------------
-CE = ("void vbh::(anonymous namespace)::ce_fwd_persist<false, long, true>"
+CE = ("void vbh::(anonymous namespace)::ce_fwd_persist<false, long, true, 256>"
       "(float const*, long const*, float*, float*, float*, long, int, long)")
 
 
