@@ -388,12 +388,12 @@ __global__ __launch_bounds__(kMaxBlock) void ce_fwd_stream(
 // Chunks of 16 KiB with two or three in flight, 8 KiB with three or four and
 // three of 32 KiB all measured slower at C4 (-0.1 to -20%).  256-lane
 // workgroups (8 vectors per lane per chunk) stream faster and start and drain
-// slower: against 512 lanes, 64 chunks per CU or more +1.0 to +2.3% (C4
-// +1.0%, 16384 x 32000 +1.5%, 8192 x 16384 and 2048 x 65536 +2.2%), 48 or
-// fewer -1.1 to -2.8% (4096 x 24576, 2048 x 32000, 1024 x 50304, 1024 x
-// 32000), so the launcher takes 256 lanes from 64 chunks per CU up.  1024
-// lanes x 2 vectors -0.9%, 128 x 16 -10%, global instead of buffer loads
-// +-0.5% (C4).
+// slower: against 512 lanes, 64 chunks per CU or more +0.9 to +2.0% (C4
+// +0.9%, 4096 x 32000 and 8192 x 16384 +1.0%, 16384 x 32000 +1.5%, 2048 x
+// 65536 +2.0%), 48 or fewer -1.7 to -2.8% (4096 x 24576, 2048 x 32000,
+// 1024 x 50304, 1024 x 32000), so the launcher takes 256 lanes from 64
+// chunks per CU up.  At C4, 1024 lanes x 2 vectors -0.9%, 128 x 16 -10%,
+// 256 x 4 (16 KiB chunks) -15%, global instead of buffer loads +-0.1%.
 //
 // Each lane folds its share of a row into an online pair: m, the max of its
 // scaled logits (NaN if any is NaN), and s, the sum of exp(x - m) over its
